@@ -1,0 +1,111 @@
+"""apk_amd -- MI355X (gfx950) preemptible persistent GEMM.
+
+Python access to the C ABI declared in include/apk.h (lib/libapk.so), used
+by the tests, smoke() and bench.py. The product is the HIP library and the
+C++ measurement binaries in bin/; this module only binds the library with
+ctypes and fails loudly when it has not been built. There is no CPU
+fallback: every compute call runs the gfx950 kernels.
+"""
+import ctypes
+import os
+import re
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(_HERE)
+LIB_PATH = os.path.join(_HERE, "lib", "libapk.so")
+BIN_DIR = os.path.join(_HERE, "bin")
+HEADER = os.path.join(ROOT, "include", "apk.h")
+
+APK_OK, APK_EINVAL, APK_EHIP, APK_ERANGE = 0, 1, 2, 3
+ENGINE_VALU64, ENGINE_MFMA128 = 0, 1
+ENGINES = {"valu64": ENGINE_VALU64, "mfma128": ENGINE_MFMA128}
+
+
+class ApkError(RuntimeError):
+    pass
+
+
+class TileRecord(ctypes.Structure):
+    _fields_ = [("start", ctypes.c_int64), ("end", ctypes.c_int64),
+                ("smid", ctypes.c_int32), ("block", ctypes.c_int32)]
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("name", ctypes.c_char * 128), ("arch", ctypes.c_char * 64),
+                ("cu_count", ctypes.c_int), ("wall_clock_khz", ctypes.c_int),
+                ("clock_khz", ctypes.c_int), ("lds_per_cu", ctypes.c_int),
+                ("regs_per_cu", ctypes.c_int), ("xcc_count", ctypes.c_int)]
+
+
+class EngineGeometry(ctypes.Structure):
+    _fields_ = [("tile_m", ctypes.c_int), ("tile_n", ctypes.c_int),
+                ("k_stage", ctypes.c_int), ("threads", ctypes.c_int),
+                ("lds_bytes", ctypes.c_int)]
+
+
+_P = ctypes.c_void_p
+_I = ctypes.c_int
+_SIGNATURES = {
+    "apk_last_error": (ctypes.c_char_p, []),
+    "apk_get_device_info": (_I, [_I, ctypes.POINTER(DeviceInfo)]),
+    "apk_engine_geometry_of": (_I, [_I, ctypes.POINTER(EngineGeometry)]),
+    "apk_persistent_gemm_occupancy": (_I, [_I, ctypes.POINTER(_I)]),
+    "apk_persistent_gemm": (_I, [_I, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
+}
+
+_lib = None
+
+
+def header_symbols(path=HEADER):
+    """Names of every function declared in include/apk.h."""
+    text = open(path).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(apk_\w+)\s*\(", text, re.M)))
+
+
+def load():
+    """Load lib/libapk.so (once) and set argument types. Raises ApkError if
+    the library has not been built: there is no fallback path."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ApkError(f"{LIB_PATH} is missing: run __graft_entry__.build() "
+                       "(make -C apk_amd) first")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in _SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = lib
+    return lib
+
+
+def check(rc):
+    if rc != APK_OK:
+        msg = load().apk_last_error().decode(errors="replace")
+        raise ApkError(f"apk error {rc}: {msg}")
+
+
+def device_info(device=0):
+    info = DeviceInfo()
+    check(load().apk_get_device_info(device, ctypes.byref(info)))
+    return info
+
+
+def geometry(engine):
+    g = EngineGeometry()
+    check(load().apk_engine_geometry_of(engine, ctypes.byref(g)))
+    return g
+
+
+def occupancy(engine):
+    n = ctypes.c_int(0)
+    check(load().apk_persistent_gemm_occupancy(engine, ctypes.byref(n)))
+    return n.value
+
+
+def persistent_gemm(engine, A, B, C, M, N, K, k_chunk, next_task, log, blocks,
+                    stream=0):
+    """Launch apk_persistent_gemm on device pointers (ints). Asynchronous."""
+    check(load().apk_persistent_gemm(engine, A, B, C, M, N, K, k_chunk,
+                                     next_task, log, blocks, stream))

@@ -1,0 +1,109 @@
+// device.hpp -- gfx950 device primitives shared by every persistent kernel:
+// the flag contract, the work-queue atomic, timers, LDS-only barriers,
+// explicit vmcnt waits and buffer-resource direct-to-LDS loads.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace apk {
+
+// ---------------------------------------------------------------------------
+// Flag contract (reference src/tile.cuh:15-30): the generation flag carries
+// only its value; nothing is published through it. Loads and stores are
+// relaxed and agent-scope, so the value is coherent across the 8 XCD L2s
+// (the load compiles to `global_load_dword ... sc1`).
+__device__ __forceinline__ int flag_load(const int* f) {
+  return __hip_atomic_load(f, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void flag_store(int* f, int v) {
+  __hip_atomic_store(f, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned fetch_add_u32(unsigned* p, unsigned v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int fetch_add_i32(int* p, int v) {
+  return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int cas_i32(int* p, int expected, int desired) {
+  __hip_atomic_compare_exchange_strong(p, &expected, desired, __ATOMIC_RELAXED,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return expected;  // previous value
+}
+__device__ __forceinline__ void atomic_max_u64(unsigned long long* p,
+                                               unsigned long long v) {
+  __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// ---------------------------------------------------------------------------
+// Timers. wall_ticks() is s_memrealtime: a constant-rate counter shared by
+// all CUs and XCDs (rate from hipDeviceAttributeWallClockRate, 100 MHz on
+// MI355X), the analog of %globaltimer (reference src/tile.cuh:50-57).
+// hw_slot() encodes XCC, SE and CU of the executing wave (the %smid analog,
+// src/tile.cuh:44-48).
+__device__ __forceinline__ int64_t wall_ticks() { return (int64_t)wall_clock64(); }
+__device__ __forceinline__ unsigned hw_slot() { return __smid(); }
+
+// ---------------------------------------------------------------------------
+// Barriers. __syncthreads() carries a workgroup release/acquire fence, which
+// on gfx950 waits vmcnt(0) and would drain every in-flight direct-to-LDS
+// load. lds_sync() fences only LDS (lgkmcnt) and then barriers, so a
+// software pipeline keeps its prefetches in flight across it. Waits for the
+// prefetched data itself are explicit (wait_vmcnt).
+__device__ __forceinline__ void lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding:
+// vmcnt[3:0] in bits 3:0 and vmcnt[5:4] in bits 15:14; expcnt=7 and
+// lgkmcnt=15 mean "no wait" for those counters).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// ---------------------------------------------------------------------------
+// Buffer resources and direct-to-LDS loads. A raw buffer with stride 0
+// returns zero for loads beyond num_records bytes instead of touching
+// memory, so a direct-to-LDS load can never fault even if a tile coordinate
+// were wrong. dword3 = 0x00020000 is the gfx9 raw 32-bit data format.
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)base;
+  i32x4 r;
+  r.x = (int)(uint32_t)(a & 0xffffffffu);
+  r.y = (int)(uint32_t)(a >> 32);  // stride 0
+  r.z = (int)bytes;
+  r.w = 0x00020000;
+  return r;
+}
+
+// One 16-byte-per-lane buffer load written straight into LDS: lane l's 16
+// bytes land at lds_base + 16*l (lds_base is wave-uniform, passed in M0).
+//
+// Issued as inline asm on purpose: the compiler's waitcnt pass cannot tell
+// which LDS bytes a DMA load writes when the ring slot is chosen at run
+// time, so with the builtin it puts vmcnt(0) before every LDS read and the
+// prefetch pipeline collapses. Kernels here wait for their DMA data
+// explicitly (wait_vmcnt + lds_sync), and the pass only ever over-waits for
+// its own loads because these DMA loads are invisible to its count. M0 holds
+// no long-lived value on gfx9+ (LDS instructions do not read it), so setting
+// it here is local to the asm.
+__device__ __forceinline__ void load_lds_x4(i32x4 rsrc, const void* lds_base,
+                                            uint32_t voffset_bytes) {
+  const uint32_t lds_addr = (uint32_t)(uintptr_t)(
+      (__attribute__((address_space(3))) const void*)lds_base);
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "buffer_load_dwordx4 %1, %2, 0 offen lds"
+      :
+      : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(voffset_bytes),
+        "s"(rsrc)
+      : "memory");
+}
+
+__device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
+
+}  // namespace apk

@@ -1,0 +1,176 @@
+// engine_mfma128.hpp -- 128x128 fp32 output tile on the gfx950 fp32 matrix
+// cores (v_mfma_f32_32x32x2_f32), fed by a 3-stage LDS ring of
+// buffer_load_dwordx4 ... lds (direct-to-LDS, no VGPR staging).
+//
+// Block: 256 threads = 4 wave64s in a 2x2 arrangement; each wave owns a
+// 64x64 sub-tile held as 2x2 32x32 accumulators (64 VGPRs per lane).
+// Stage: k depth KS=32 -> A stage 128x32 fp32 (16 KiB) + B stage 32x128 fp32
+// (16 KiB); 3 stages = 96 KiB of the 160 KiB LDS (1 block per CU).
+//
+// LDS layouts (bank-conflict-free for the MFMA operand reads):
+//  A stage: 128 rows x 128 B. 16-byte quad q of row r is stored at slot
+//           q ^ (r & 7), so eight consecutive rows reading the same quad hit
+//           eight different 16-byte bank groups.
+//  B stage: 32 rows x 512 B, natural order; an operand read is 32
+//           consecutive dwords of one row per half-wave.
+//
+// k order inside a stage: k-group g (8 values) is consumed in 4 MFMA steps;
+// in step s the lower half-wave supplies k = 8g+s and the upper half-wave
+// k = 8g+4+s. The order is fixed, so a tile's result is a deterministic
+// function of its inputs whatever worker computes it and however often it
+// is checkpointed and resumed.
+#pragma once
+#include "device.hpp"
+
+namespace apk {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+struct EngMfma128 {
+  static constexpr int TM = 128, TN = 128, KS = 32, NS = 3, THREADS = 256;
+  static constexpr int A_STAGE = TM * KS * 4;               // bytes
+  static constexpr int B_STAGE = KS * TN * 4;               // bytes
+  static constexpr int STAGE = A_STAGE + B_STAGE;           // 32 KiB
+  static constexpr int LDS_BYTES = NS * STAGE;              // 96 KiB
+  static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 4 per thread
+  static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 4 per thread
+  static constexpr int LOADS = LOADS_A + LOADS_B;           // per stage
+
+  struct Acc {
+    f32x16 c[2][2];
+  };
+
+  struct Ctx {
+    i32x4 ra, rb;
+    int K, N;
+  };
+
+  static __device__ __forceinline__ Ctx make_ctx(const float* A, const float* B,
+                                                 int M, int N, int K) {
+    Ctx c;
+    c.ra = make_rsrc(A, (uint32_t)((size_t)M * K * 4));
+    c.rb = make_rsrc(B, (uint32_t)((size_t)K * N * 4));
+    c.K = K;
+    c.N = N;
+    return c;
+  }
+
+  static __device__ __forceinline__ void zero(Acc& a) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a.c[i][j][r] = 0.0f;
+  }
+
+  // Issue the direct-to-LDS loads of k-stage `s` (k0 = s*KS) of the tile at
+  // (row0, col0) into ring slot `buf`. LOADS instructions per thread.
+  static __device__ __forceinline__ void issue(char* smem, const Ctx& c, int buf,
+                                               int row0, int col0, int s) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int k0 = s * KS;
+    char* abase = smem + buf * STAGE;
+    char* bbase = abase + A_STAGE;
+#pragma unroll
+    for (int i = 0; i < LOADS_A; ++i) {
+      const int ci = i * 4 + w;          // 1 KiB piece = 8 rows of 128 B
+      const int r = ci * 8 + (l >> 3);
+      const int q = (l & 7) ^ (r & 7);   // global quad landing in slot l&7
+      const uint32_t off = (uint32_t)(((row0 + r) * c.K + k0 + 4 * q) * 4);
+      load_lds_x4(c.ra, abase + ci * 1024, off);
+    }
+#pragma unroll
+    for (int i = 0; i < LOADS_B; ++i) {
+      const int ci = i * 4 + w;          // 1 KiB piece = 2 rows of 512 B
+      const int r = ci * 2 + (l >> 5);
+      const uint32_t off = (uint32_t)(((k0 + r) * c.N + col0 + 4 * (l & 31)) * 4);
+      load_lds_x4(c.rb, bbase + ci * 1024, off);
+    }
+  }
+
+  static __device__ __forceinline__ void compute(const char* smem, int buf,
+                                                 Acc& acc) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w & 1, wn = w >> 1;
+    const int lr = l & 31, h = l >> 5;
+    const char* abase = smem + buf * STAGE;
+    const float* bbase = (const float*)(abase + A_STAGE);
+#pragma unroll
+    for (int g = 0; g < KS / 8; ++g) {
+      f32x4 a4[2];
+      float bv[2][4];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const int row = wm * 64 + rb * 32 + lr;
+        const int slot = (2 * g + h) ^ (row & 7);
+        a4[rb] = *(const f32x4*)(abase + row * 128 + slot * 16);
+      }
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb) {
+        const int col = wn * 64 + cb * 32 + lr;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) bv[cb][s] = bbase[(8 * g + 4 * h + s) * TN + col];
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+          for (int cb = 0; cb < 2; ++cb)
+            acc.c[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(
+                a4[rb][s], bv[cb][s], acc.c[rb][cb], 0, 0, 0);
+    }
+  }
+
+  // Wait until k-stage s has landed, given `ahead` later stages already
+  // issued behind it (0..NS-1). vmcnt is in-order, so allowing
+  // ahead*LOADS outstanding operations guarantees stage s is complete.
+  static __device__ __forceinline__ void wait_stage(int ahead) {
+    if (ahead >= 2) wait_vmcnt<2 * LOADS>();
+    else if (ahead == 1) wait_vmcnt<LOADS>();
+    else wait_vmcnt<0>();
+  }
+
+  // Software-pipelined K loop over k-stages [s_begin, s_end) of one tile.
+  // hook(s) runs uniformly at the top of every stage, before its prefetch.
+  template <class Hook>
+  static __device__ __forceinline__ void mainloop(char* smem, const Ctx& c,
+                                                  Acc& acc, int row0, int col0,
+                                                  int s_begin, int s_end,
+                                                  Hook&& hook) {
+    constexpr int P = NS - 1;
+#pragma unroll
+    for (int p = 0; p < P; ++p)
+      if (s_begin + p < s_end) issue(smem, c, (s_begin + p) % NS, row0, col0, s_begin + p);
+    for (int s = s_begin; s < s_end; ++s) {
+      hook(s);
+      if (s + P < s_end) issue(smem, c, (s + P) % NS, row0, col0, s + P);
+      const int ahead = (s_end - 1 - s) < P ? (s_end - 1 - s) : P;
+      wait_stage(ahead);
+      lds_sync();
+      compute(smem, s % NS, acc);
+      lds_sync();
+    }
+  }
+
+  static __device__ __forceinline__ void store(const Acc& acc, float* C, int N,
+                                               int row0, int col0) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w & 1, wn = w >> 1;
+    const int lr = l & 31, h = l >> 5;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = row0 + wm * 64 + rb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          const int col = col0 + wn * 64 + cb * 32 + lr;
+          C[(size_t)row * N + col] = acc.c[rb][cb][r];
+        }
+  }
+};
+
+}  // namespace apk

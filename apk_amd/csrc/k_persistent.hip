@@ -1,0 +1,132 @@
+// k_persistent.hip -- the persistent GEMM worker pool (calibration path).
+//
+// Counterpart of persistent_gemm (reference src/persistent.cu:51-79): a grid
+// of resident workers pops output tiles from one fetch-add counter in HBM
+// until the tile space is exhausted (termination by queue exhaustion, so
+// correctness never depends on co-residency). A tile's K range is walked in
+// k_chunk-wide chunks in order; chunk boundaries are the points where the
+// preemptible variants poll, and here they are where per-chunk timing
+// records are taken.
+#include "capi.hpp"
+#include "engine_mfma128.hpp"
+#include "engine_valu64.hpp"
+
+namespace apk {
+
+template <class E>
+__global__ void __launch_bounds__(E::THREADS)
+    k_persistent_gemm(const float* __restrict__ A, const float* __restrict__ B,
+                      float* __restrict__ C, int M, int N, int K, int kChunk,
+                      unsigned* next_task, apk_tile_record* log) {
+  __shared__ __attribute__((aligned(16))) char smem[E::LDS_BYTES];
+  __shared__ unsigned s_task;
+
+  const int tilesN = N / E::TN;
+  const unsigned numTasks = (unsigned)((M / E::TM) * tilesN);
+  const int nChunks = K / kChunk;
+  const int spc = kChunk / E::KS;  // k-stages per chunk
+  const typename E::Ctx ctx = E::make_ctx(A, B, M, N, K);
+
+  for (;;) {
+    if (threadIdx.x == 0) s_task = fetch_add_u32(next_task, 1u);
+    __syncthreads();
+    const unsigned task = s_task;
+    __syncthreads();  // every thread has read s_task before it is rewritten
+    if (task >= numTasks) break;
+
+    const int row0 = (int)(task / tilesN) * E::TM;
+    const int col0 = (int)(task % tilesN) * E::TN;
+    int64_t prev = 0;
+    apk_tile_record* rec = log ? log + (size_t)task * nChunks : nullptr;
+
+    typename E::Acc acc;
+    E::zero(acc);
+    E::mainloop(smem, ctx, acc, row0, col0, 0, K / E::KS, [&](int s) {
+      if (threadIdx.x == 0 && rec && s % spc == 0) {
+        const int64_t now = wall_ticks();
+        const int c = s / spc;
+        if (c > 0) {
+          rec[c - 1].start = prev;
+          rec[c - 1].end = now;
+          rec[c - 1].smid = (int)hw_slot();
+          rec[c - 1].block = (int)blockIdx.x;
+        }
+        prev = now;
+      }
+    });
+    E::store(acc, C, N, row0, col0);
+    __syncthreads();  // whole tile committed before the clock closes
+    if (threadIdx.x == 0 && rec) {
+      rec[nChunks - 1].start = prev;
+      rec[nChunks - 1].end = wall_ticks();
+      rec[nChunks - 1].smid = (int)hw_slot();
+      rec[nChunks - 1].block = (int)blockIdx.x;
+    }
+  }
+}
+
+template <class E>
+static int launch_persistent_gemm(const float* A, const float* B, float* C,
+                                  int M, int N, int K, int kChunk,
+                                  unsigned* next, apk_tile_record* log,
+                                  int blocks, hipStream_t st) {
+  APK_REQUIRE(A && B && C && next, "persistent_gemm: NULL pointer");
+  APK_REQUIRE(M > 0 && N > 0 && K > 0, "persistent_gemm: empty shape");
+  APK_REQUIRE(M % E::TM == 0 && N % E::TN == 0,
+              "persistent_gemm: M=%d N=%d not multiples of the %dx%d tile", M, N,
+              E::TM, E::TN);
+  APK_REQUIRE(kChunk > 0 && kChunk % E::KS == 0 && K % kChunk == 0,
+              "persistent_gemm: k_chunk=%d must divide K=%d and be a multiple "
+              "of %d", kChunk, K, E::KS);
+  APK_REQUIRE((size_t)M * K * 4 < (1ull << 31) && (size_t)K * N * 4 < (1ull << 31) &&
+                  (size_t)M * N < (1ull << 31),
+              "persistent_gemm: operands above 2 GiB are not supported");
+  APK_REQUIRE(blocks > 0, "persistent_gemm: blocks=%d", blocks);
+  hipLaunchKernelGGL(k_persistent_gemm<E>, dim3(blocks), dim3(E::THREADS), 0, st,
+                     A, B, C, M, N, K, kChunk, next, log);
+  APK_LAUNCHED();
+  return APK_OK;
+}
+
+template <class E>
+static int occupancy_of(int* out) {
+  APK_REQUIRE(out != nullptr, "occupancy: out is NULL");
+  int n = 0;
+  APK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, k_persistent_gemm<E>,
+                                                       E::THREADS, 0));
+  *out = n;
+  return APK_OK;
+}
+
+}  // namespace apk
+
+extern "C" int apk_persistent_gemm(int engine, const float* A, const float* B,
+                                   float* C, int M, int N, int K, int k_chunk,
+                                   unsigned int* next_task, apk_tile_record* log,
+                                   int blocks, void* stream) {
+  using namespace apk;
+  switch (engine) {
+    case APK_ENGINE_VALU64:
+      return launch_persistent_gemm<EngValu64>(A, B, C, M, N, K, k_chunk,
+                                               next_task, log, blocks,
+                                               as_stream(stream));
+    case APK_ENGINE_MFMA128:
+      return launch_persistent_gemm<EngMfma128>(A, B, C, M, N, K, k_chunk,
+                                                next_task, log, blocks,
+                                                as_stream(stream));
+    default:
+      set_error("persistent_gemm: unknown engine %d", engine);
+      return APK_EINVAL;
+  }
+}
+
+extern "C" int apk_persistent_gemm_occupancy(int engine, int* blocks_per_cu) {
+  using namespace apk;
+  switch (engine) {
+    case APK_ENGINE_VALU64: return occupancy_of<EngValu64>(blocks_per_cu);
+    case APK_ENGINE_MFMA128: return occupancy_of<EngMfma128>(blocks_per_cu);
+    default:
+      set_error("occupancy: unknown engine %d", engine);
+      return APK_EINVAL;
+  }
+}

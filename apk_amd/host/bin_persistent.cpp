@@ -1,0 +1,209 @@
+// persistent -- tile calibration of the persistent fp32 GEMM on MI355X.
+//
+// Measurement surface of the reference's bin/persistent (src/persistent.cu:
+// 96-264): same flags and defaults (--k 128 --tiles-m 48 --tiles-n 48
+// --passes 3 --verify 1 --blocks 0 --sm-clock-mhz 0 --csv
+// results/raw/phase1_tiles.csv), same stdout lines and the same per-task CSV
+// schema "task,block,smid,start_cyc,end_cyc,dur_cyc,dur_us" (extra columns
+// tile,chunk appended). Additions:
+//   --engine valu64|mfma128   tile engine (valu64 = the reference's 64x64
+//                             fmaf tile; mfma128 = 128x128 on fp32 MFMA)
+//   --gemm-k K                full GEMM depth, walked in --k wide chunks
+//                             (default = --k: one chunk per tile, as the
+//                             reference); records are per (tile, chunk)
+//   --blocks-per-cu n         workers per CU when --blocks is 0 (default 1)
+//   --seed s                  glibc srand seed (default 21 = reference)
+//   --verify-rows r           verify only the first r rows (0 = all)
+// Timer: records hold device wall-clock ticks (s_memrealtime), so
+// --sm-clock-mhz defaults to that clock's rate and dur_us needs no clock lock.
+#include <omp.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "host_common.hpp"
+
+using namespace host;
+
+int main(int argc, char** argv) {
+  const int kChunk = (int)parse_arg(argc, argv, "--k", 128);
+  const int tilesM = (int)parse_arg(argc, argv, "--tiles-m", 48);
+  const int tilesN = (int)parse_arg(argc, argv, "--tiles-n", 48);
+  const int passes = (int)parse_arg(argc, argv, "--passes", 3);
+  const int verify = (int)parse_arg(argc, argv, "--verify", 1);
+  int blocks = (int)parse_arg(argc, argv, "--blocks", 0);
+  double clkMHz = parse_arg(argc, argv, "--sm-clock-mhz", 0.0);
+  const char* csvPath = parse_str(argc, argv, "--csv", "results/raw/phase1_tiles.csv");
+  const std::string engName = parse_str(argc, argv, "--engine", "valu64");
+  const int gemmK = (int)parse_arg(argc, argv, "--gemm-k", kChunk);
+  const int bpc = (int)parse_arg(argc, argv, "--blocks-per-cu", 1);
+  const unsigned seed = (unsigned)parse_arg(argc, argv, "--seed", 21);
+  const int verifyRows = (int)parse_arg(argc, argv, "--verify-rows", 0);
+
+  int engine = -1;
+  if (engName == "valu64") engine = APK_ENGINE_VALU64;
+  else if (engName == "mfma128") engine = APK_ENGINE_MFMA128;
+  if (engine < 0) {
+    fprintf(stderr, "unknown --engine %s (valu64|mfma128)\n", engName.c_str());
+    return 1;
+  }
+  apk_engine_geometry geo;
+  APK_CHECK(apk_engine_geometry_of(engine, &geo));
+  if (kChunk <= 0 || kChunk % geo.k_stage != 0) {
+    fprintf(stderr, "--k must be a multiple of %d\n", geo.k_stage);
+    return 1;
+  }
+  if (gemmK % kChunk != 0) {
+    fprintf(stderr, "--gemm-k must be a multiple of --k\n");
+    return 1;
+  }
+
+  const Device dev = device_query();
+  int maxPerCU = 0;
+  APK_CHECK(apk_persistent_gemm_occupancy(engine, &maxPerCU));
+  if (blocks <= 0) blocks = dev.info.cu_count * std::max(1, std::min(bpc, maxPerCU));
+  if (clkMHz <= 0.0) clkMHz = dev.wall_mhz;
+
+  const int M = tilesM * geo.tile_m, N = tilesN * geo.tile_n, K = gemmK;
+  const int numTasks = tilesM * tilesN;
+  const int nChunks = K / kChunk;
+  const int64_t numRecs = (int64_t)numTasks * nChunks;
+  const double flopPerChunk = 2.0 * geo.tile_m * geo.tile_n * kChunk;
+  const double flopTotal = 2.0 * M * N * (double)K;
+
+  printf("GPU: %s | %s | %d CUs | wall clock %.0f MHz\n", dev.info.name,
+         dev.info.arch, dev.info.cu_count, dev.wall_mhz);
+  printf("config: M=%d N=%d K=%d | tile %dx%d (%s) | k-chunk %d (%d chunks/tile) "
+         "| tasks=%d | blocks=%d x %d threads (%d/CU max) | passes=%d | seed %u%s\n",
+         M, N, K, geo.tile_m, geo.tile_n, engName.c_str(), kChunk, nChunks,
+         numTasks, blocks, geo.threads, maxPerCU, passes, seed,
+         seed == 0 ? " (glibc: srand(0) == srand(1))" : "");
+  printf("clock for us conversion: %.0f MHz (device wall clock ticks)\n", clkMHz);
+
+  std::vector<float> hA((size_t)M * K), hB((size_t)K * N);
+  fill_uniform_pm1(seed, hA, hB);
+
+  float *dA, *dB, *dC;
+  unsigned* dNext;
+  apk_tile_record* dLog;
+  HIP_CHECK(hipMalloc(&dA, hA.size() * sizeof(float)));
+  HIP_CHECK(hipMalloc(&dB, hB.size() * sizeof(float)));
+  HIP_CHECK(hipMalloc(&dC, (size_t)M * N * sizeof(float)));
+  HIP_CHECK(hipMalloc(&dNext, sizeof(unsigned)));
+  HIP_CHECK(hipMalloc(&dLog, (size_t)numRecs * sizeof(apk_tile_record)));
+  HIP_CHECK(hipMemcpy(dA, hA.data(), hA.size() * sizeof(float), hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemcpy(dB, hB.data(), hB.size() * sizeof(float), hipMemcpyHostToDevice));
+
+  hipEvent_t e0, e1;
+  HIP_CHECK(hipEventCreate(&e0));
+  HIP_CHECK(hipEventCreate(&e1));
+  float lastMs = 0.f;
+  for (int p = 0; p < passes; ++p) {
+    // 0xFF fill: C becomes NaN and log.block -1, so a tile that never runs
+    // fails loudly (src/persistent.cu:156-160).
+    HIP_CHECK(hipMemset(dC, 0xFF, (size_t)M * N * sizeof(float)));
+    HIP_CHECK(hipMemset(dLog, 0xFF, (size_t)numRecs * sizeof(apk_tile_record)));
+    HIP_CHECK(hipMemset(dNext, 0, sizeof(unsigned)));
+    HIP_CHECK(hipDeviceSynchronize());
+    HIP_CHECK(hipEventRecord(e0, 0));
+    APK_CHECK(apk_persistent_gemm(engine, dA, dB, dC, M, N, K, kChunk, dNext, dLog,
+                                  blocks, nullptr));
+    HIP_CHECK(hipEventRecord(e1, 0));
+    HIP_CHECK(hipEventSynchronize(e1));
+    HIP_CHECK(hipGetLastError());
+    HIP_CHECK(hipEventElapsedTime(&lastMs, e0, e1));
+    printf("pass %d: %.3f ms wall | %.1f GFLOP/s | %.2f TFLOP/s (%.1f%% of %.1f fp32 peak) "
+           "| %.0f tasks/s%s\n",
+           p, lastMs, flopTotal / (lastMs * 1e6), tflops(flopTotal, lastMs * 1e-3),
+           100.0 * tflops(flopTotal, lastMs * 1e-3) / kPeakFp32TF, kPeakFp32TF,
+           numTasks / (lastMs * 1e-3), p + 1 < passes ? " (warmup)" : "");
+  }
+
+  std::vector<apk_tile_record> hLog(numRecs);
+  HIP_CHECK(hipMemcpy(hLog.data(), dLog, numRecs * sizeof(apk_tile_record),
+                      hipMemcpyDeviceToHost));
+  int64_t unlogged = 0;
+  for (int64_t t = 0; t < numRecs; ++t)
+    if (hLog[t].block < 0) ++unlogged;
+  if (unlogged) {
+    fprintf(stderr, "FAIL: %lld of %lld task records never logged\n",
+            (long long)unlogged, (long long)numRecs);
+    return 1;
+  }
+
+  std::vector<double> durUs(numRecs);
+  for (int64_t t = 0; t < numRecs; ++t)
+    durUs[t] = (hLog[t].end - hLog[t].start) / clkMHz;
+  std::vector<double> sorted = durUs;
+  std::sort(sorted.begin(), sorted.end());
+  auto pct = [&](double q) {
+    return sorted[std::min((size_t)(q * sorted.size()), sorted.size() - 1)];
+  };
+  double mean = 0;
+  for (double d : sorted) mean += d;
+  mean /= sorted.size();
+  printf("tile duration (us, final pass, n=%lld): min %.2f | p50 %.2f | p90 %.2f | "
+         "p99 %.2f | max %.2f | mean %.2f\n",
+         (long long)numRecs, sorted.front(), pct(0.50), pct(0.90), pct(0.99),
+         sorted.back(), mean);
+  const bool inBand = pct(0.50) >= 2.0 && pct(0.50) <= 25.0;
+  printf("2-25 us band check (p50): %s\n", inBand ? "IN BAND" : "OUT OF BAND");
+  const double perTileTF = flopPerChunk / (pct(0.50) * 1e-6) / 1e12;
+  printf("per-tile throughput at p50: %.3f TFLOP/s per worker | x%d workers = %.1f "
+         "TFLOP/s\n", perTileTF, blocks, perTileTF * blocks);
+
+  std::vector<int> perBlock(blocks, 0);
+  for (int64_t t = 0; t < numRecs; t += nChunks) ++perBlock[hLog[t].block];
+  printf("tasks/block: min %d | max %d (ideal %.1f)\n",
+         *std::min_element(perBlock.begin(), perBlock.end()),
+         *std::max_element(perBlock.begin(), perBlock.end()),
+         (double)numTasks / blocks);
+
+  int rc = 0;
+  if (verify) {
+    const int vr = (verifyRows > 0 && verifyRows < M) ? verifyRows : M;
+    std::vector<float> hC((size_t)vr * N);
+    HIP_CHECK(hipMemcpy(hC.data(), dC, hC.size() * sizeof(float), hipMemcpyDeviceToHost));
+    printf("verifying %d of %d rows against float64 host reference (%d threads)...\n",
+           vr, M, omp_get_max_threads());
+    std::vector<double> ref((size_t)vr * N);
+    const int64_t t0 = now_ns();
+    gemm_f64(hA.data(), hB.data(), ref.data(), vr, N, K, 0);
+    const double refS = (now_ns() - t0) / 1e9;
+    const CheckResult r = check(hC.data(), ref.data(), (int64_t)ref.size(), 1e-4, 1e-4);
+    printf("host float64 reference: %.2f s on %d threads (%.2f GFLOP/s)\n", refS,
+           omp_get_max_threads(), 2.0 * vr * N * (double)K / refS / 1e9);
+    const double frobTol = 1e-5;
+    if (r.nans || r.bad || !(r.rel_frob <= frobTol)) {
+      fprintf(stderr, "FAIL: %lld NaN (never-written) elements, %lld beyond tolerance, "
+              "max rel err %.3e, rel-Frobenius %.3e (tol %.0e)\n",
+              (long long)r.nans, (long long)r.bad, r.max_rel, r.rel_frob, frobTol);
+      rc = 1;
+    } else {
+      printf("PASS: all %zu elements within rtol=%g atol=%g (max rel err %.3e) | "
+             "rel-Frobenius %.3e <= %.0e\n",
+             ref.size(), 1e-4, 1e-4, r.max_rel, r.rel_frob, frobTol);
+    }
+  } else {
+    printf("verification SKIPPED (--verify 0)\n");
+  }
+
+  FILE* csv = fopen(csvPath, "w");
+  if (csv) {
+    fprintf(csv, "task,block,smid,start_cyc,end_cyc,dur_cyc,dur_us,tile,chunk\n");
+    for (int64_t t = 0; t < numRecs; ++t)
+      fprintf(csv, "%lld,%d,%d,%lld,%lld,%lld,%.3f,%lld,%lld\n", (long long)t,
+              hLog[t].block, hLog[t].smid, (long long)hLog[t].start,
+              (long long)hLog[t].end, (long long)(hLog[t].end - hLog[t].start),
+              durUs[t], (long long)(t / nChunks), (long long)(t % nChunks));
+    fclose(csv);
+    printf("raw tile records: %s\n", csvPath);
+  } else {
+    fprintf(stderr, "warning: could not open %s for writing\n", csvPath);
+  }
+  return rc;
+}

@@ -1,0 +1,117 @@
+// host_common.cpp -- see host_common.hpp.
+#include "host_common.hpp"
+
+#include <omp.h>
+
+#include <algorithm>
+#include <chrono>
+#include <cmath>
+#include <cstring>
+#include <random>
+
+namespace host {
+
+double parse_arg(int argc, char** argv, const char* name, double dflt) {
+  for (int i = 1; i + 1 < argc; ++i)
+    if (strcmp(argv[i], name) == 0) return atof(argv[i + 1]);
+  return dflt;
+}
+
+const char* parse_str(int argc, char** argv, const char* name, const char* dflt) {
+  for (int i = 1; i + 1 < argc; ++i)
+    if (strcmp(argv[i], name) == 0) return argv[i + 1];
+  return dflt;
+}
+
+int64_t now_ns() {
+  using namespace std::chrono;
+  return duration_cast<nanoseconds>(steady_clock::now().time_since_epoch()).count();
+}
+
+void spin_until_ns(int64_t deadline) {
+  while (now_ns() < deadline) {
+  }
+}
+
+void spin_for_ns(int64_t ns) { spin_until_ns(now_ns() + ns); }
+
+double percentile(std::vector<double> v, double q) {
+  if (v.empty()) return NAN;
+  std::sort(v.begin(), v.end());
+  return v[std::min((size_t)(q * v.size()), v.size() - 1)];
+}
+
+void fill_uniform_pm1(unsigned seed, std::vector<float>& A, std::vector<float>& B) {
+  srand(seed);
+  for (auto& v : A) v = (float)(rand() / (double)RAND_MAX * 2.0 - 1.0);
+  for (auto& v : B) v = (float)(rand() / (double)RAND_MAX * 2.0 - 1.0);
+}
+
+void gemm_f64_rows(const float* A, const float* B, double* C, int N, int K,
+                   int r0, int nr) {
+  for (int ii = 0; ii < nr; ++ii) {
+    const int i = r0 + ii;
+    double* crow = C + (size_t)ii * N;
+    std::fill(crow, crow + N, 0.0);
+    for (int k = 0; k < K; ++k) {
+      const double a = A[(size_t)i * K + k];
+      const float* brow = B + (size_t)k * N;
+      for (int j = 0; j < N; ++j) crow[j] += a * brow[j];
+    }
+  }
+}
+
+void gemm_f64(const float* A, const float* B, double* C, int M, int N, int K,
+              int threads) {
+  if (threads <= 0) threads = omp_get_max_threads();
+#pragma omp parallel for schedule(dynamic, 4) num_threads(threads)
+  for (int i = 0; i < M; ++i) gemm_f64_rows(A, B, C + (size_t)i * N, N, K, i, 1);
+}
+
+CheckResult check(const float* got, const double* ref, int64_t n, double rtol,
+                  double atol) {
+  CheckResult r;
+  long double num = 0, den = 0;
+  for (int64_t i = 0; i < n; ++i) {
+    den += (long double)ref[i] * ref[i];
+    if (std::isnan(got[i])) {
+      ++r.nans;
+      continue;
+    }
+    const double err = std::fabs((double)got[i] - ref[i]);
+    num += (long double)err * err;
+    r.max_rel = std::max(r.max_rel, err / std::max(1.0, std::fabs(ref[i])));
+    if (err > atol + rtol * std::fabs(ref[i])) ++r.bad;
+  }
+  r.rel_frob = den > 0 ? (double)std::sqrt(num / den) : (num > 0 ? INFINITY : 0.0);
+  if (r.nans) r.rel_frob = NAN;
+  return r;
+}
+
+Device device_query() {
+  Device d;
+  APK_CHECK(apk_get_device_info(0, &d.info));
+  d.wall_mhz = d.info.wall_clock_khz / 1000.0;
+  return d;
+}
+
+std::vector<long long> uniform_schedule(unsigned seed, double gmin_us,
+                                        double gmax_us, int events) {
+  std::mt19937 rng(seed);
+  std::uniform_real_distribution<double> gap(gmin_us * 1000.0, gmax_us * 1000.0);
+  std::vector<long long> out(std::max(events, 1), 0);
+  long long acc = 0;
+  for (int e = 0; e < events; ++e) out[e] = (acc += (long long)gap(rng));
+  return out;
+}
+
+std::vector<long long> exp_schedule(unsigned seed, double mean_us, int events) {
+  std::mt19937 rng(seed);
+  std::exponential_distribution<double> gap(1.0 / (mean_us * 1000.0));
+  std::vector<long long> out(std::max(events, 1), 0);
+  long long acc = 0;
+  for (int e = 0; e < events; ++e) out[e] = (acc += (long long)gap(rng));
+  return out;
+}
+
+}  // namespace host

@@ -1,0 +1,407 @@
+// oracle.cpp -- CPU restatement of the reference's host-side algorithms on the
+// preemptible persistent-GEMM path.
+//
+// TEST INFRASTRUCTURE ONLY. Nothing in the product (apk_amd/) links, loads or
+// calls this file. Only tests/, __graft_entry__.smoke() and bench.py's
+// cpu_baseline leg use it, and only as the checker or the timed CPU baseline.
+//
+// Every function names the reference file:line it restates (paths relative to
+// the reference repository root). Pinning of each function (what independent
+// check would catch a plausible mistake) is done in tests/test_oracle.py:
+//   apko_glibc_*            pinned against libc's own srand/rand and against
+//                           published known answers (srand(1) -> 1804289383)
+//   apko_mt19937_*          pinned against the C++ standard's required 10000th
+//                           output and against numpy's MT19937 legacy seeding
+//   apko_canonical/uniform/ pinned against libstdc++ compiled into a test
+//   exponential schedules   helper, plus distribution moments
+//   apko_gemm_f64           pinned against numpy float64 matmul and closed forms
+//   apko_gemm_f32_chain     pinned against exact rational arithmetic (Python
+//                           fractions) on small cases and integer-exact cases
+//   apko_bf16_rne           pinned against torch's bfloat16 cast (RNE)
+//   apko_percentile         pinned by brute-force definition on small inputs
+//   apko_count_*            pinned by planted duplicates/misses on the CPU
+//   apko_tile_hash          pinned by bit-flip sensitivity and order invariance
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+extern "C" {
+
+// ---------------------------------------------------------------------------
+// glibc random(3) TYPE_3 generator, as used by the reference's srand(21) +
+// rand() input generation (src/persistent.cu:131-135, src/yield.cu:367-370,
+// src/midyield.cu:405-408, src/tcyield.cu:461-473). glibc stdlib/random_r.c:
+// degree 31, separation 3, LCG seeding with 16807 mod 2^31-1, 310 discarded
+// outputs, output = (state[f] += state[r]) >> 1.
+typedef struct apko_glibc_state {
+  int32_t s[31];
+  int f, r;
+} apko_glibc_state;
+
+void apko_glibc_srand(apko_glibc_state* st, uint32_t seed) {
+  if (seed == 0) seed = 1;  // glibc: a zero seed is replaced by 1
+  st->s[0] = (int32_t)seed;
+  int64_t word = (int64_t)seed;
+  for (int i = 1; i < 31; ++i) {
+    const int64_t hi = word / 127773;
+    const int64_t lo = word % 127773;
+    word = 16807 * lo - 2836 * hi;
+    if (word < 0) word += 2147483647;
+    st->s[i] = (int32_t)word;
+  }
+  st->f = 3;
+  st->r = 0;
+  for (int i = 0; i < 310; ++i) {
+    uint32_t v = (uint32_t)st->s[st->f] + (uint32_t)st->s[st->r];
+    st->s[st->f] = (int32_t)v;
+    st->f = (st->f + 1) % 31;
+    st->r = (st->r + 1) % 31;
+  }
+}
+
+int32_t apko_glibc_rand(apko_glibc_state* st) {
+  const uint32_t v = (uint32_t)st->s[st->f] + (uint32_t)st->s[st->r];
+  st->s[st->f] = (int32_t)v;
+  st->f = (st->f + 1) % 31;
+  st->r = (st->r + 1) % 31;
+  return (int32_t)(v >> 1);
+}
+
+void apko_glibc_rand_stream(uint32_t seed, int32_t* out, int64_t n) {
+  apko_glibc_state st;
+  apko_glibc_srand(&st, seed);
+  for (int64_t i = 0; i < n; ++i) out[i] = apko_glibc_rand(&st);
+}
+
+// Inputs in [-1, 1]: v = (float)(rand() / (double)RAND_MAX * 2.0 - 1.0), A
+// first (M*K values, row-major) then B (K*N), from one stream
+// (src/persistent.cu:132-135).
+void apko_fill_uniform_pm1(uint32_t seed, float* A, int64_t nA, float* B,
+                           int64_t nB) {
+  apko_glibc_state st;
+  apko_glibc_srand(&st, seed);
+  const double rmax = 2147483647.0;  // RAND_MAX on glibc
+  for (int64_t i = 0; i < nA; ++i)
+    A[i] = (float)(apko_glibc_rand(&st) / rmax * 2.0 - 1.0);
+  for (int64_t i = 0; i < nB; ++i)
+    B[i] = (float)(apko_glibc_rand(&st) / rmax * 2.0 - 1.0);
+}
+
+// ---------------------------------------------------------------------------
+// float64 host reference GEMM, i-k-j loop order with a double accumulator per
+// output (src/persistent.cu:221-227). A is MxK row-major, B is KxN row-major,
+// C is MxN row-major. `threads` > 1 splits rows across std::threads; each
+// output's summation order (k ascending) is unchanged, so the result does not
+// depend on the thread count.
+void apko_gemm_f64(const float* A, const float* B, double* C, int M, int N,
+                   int K, int threads) {
+  auto rows = [&](int r0, int r1) {
+    for (int i = r0; i < r1; ++i) {
+      double* crow = C + (size_t)i * N;
+      for (int j = 0; j < N; ++j) crow[j] = 0.0;
+      for (int k = 0; k < K; ++k) {
+        const double a = A[(size_t)i * K + k];
+        const float* brow = B + (size_t)k * N;
+        for (int j = 0; j < N; ++j) crow[j] += a * brow[j];
+      }
+    }
+  };
+  if (threads <= 1) {
+    rows(0, M);
+    return;
+  }
+  std::vector<std::thread> pool;
+  const int per = (M + threads - 1) / threads;
+  for (int t = 0; t < threads; ++t) {
+    const int r0 = t * per, r1 = std::min(M, r0 + per);
+    if (r0 >= r1) break;
+    pool.emplace_back(rows, r0, r1);
+  }
+  for (auto& th : pool) th.join();
+}
+
+// Same product on bf16-quantized inputs given as float (src/tcyield.cu:
+// 459-483 does this for fp16): A and B hold the dequantized values.
+void apko_gemm_f64_rows(const float* A, const float* B, double* C, int M,
+                        int N, int K, int row0, int nrows) {
+  for (int i = row0; i < row0 + nrows && i < M; ++i) {
+    double* crow = C + (size_t)(i - row0) * N;
+    for (int j = 0; j < N; ++j) crow[j] = 0.0;
+    for (int k = 0; k < K; ++k) {
+      const double a = A[(size_t)i * K + k];
+      const float* brow = B + (size_t)k * N;
+      for (int j = 0; j < N; ++j) crow[j] += a * brow[j];
+    }
+  }
+}
+
+// fp32 fused-multiply-add chain of the reference tile: every output is
+// acc = fmaf(A[i][k], B[k][j], acc) for k = 0..K-1 starting from acc = 0
+// (src/tile.cuh:72, 85-96; src/midyield.cu:292-304). fmaf is correctly
+// rounded (C99 7.12.13.1), so this defines the bits of a VALU tile that keeps
+// the reference's k order.
+void apko_gemm_f32_chain(const float* A, const float* B, float* C, int M,
+                         int N, int K) {
+  std::vector<float> acc((size_t)N);
+  for (int i = 0; i < M; ++i) {
+    std::fill(acc.begin(), acc.end(), 0.0f);
+    for (int k = 0; k < K; ++k) {
+      const float a = A[(size_t)i * K + k];
+      const float* brow = B + (size_t)k * N;
+      for (int j = 0; j < N; ++j) acc[j] = std::fmaf(a, brow[j], acc[j]);
+    }
+    std::memcpy(C + (size_t)i * N, acc.data(), sizeof(float) * N);
+  }
+}
+
+// Elementwise gate |got - ref| <= atol + rtol*|ref|, NaN counted separately,
+// rel metric err / max(1, |ref|) (src/persistent.cu:228-237).
+void apko_check_elementwise(const float* got, const double* ref, int64_t n,
+                            double rtol, double atol, int64_t* bad,
+                            int64_t* nans, double* max_rel) {
+  int64_t b = 0, nn = 0;
+  double mr = 0.0;
+  for (int64_t i = 0; i < n; ++i) {
+    if (std::isnan(got[i])) {
+      ++nn;
+      continue;
+    }
+    const double err = std::fabs((double)got[i] - ref[i]);
+    const double rel = err / std::max(1.0, std::fabs(ref[i]));
+    mr = std::max(mr, rel);
+    if (err > atol + rtol * std::fabs(ref[i])) ++b;
+  }
+  *bad = b;
+  *nans = nn;
+  *max_rel = mr;
+}
+
+// Relative Frobenius error ||got - ref||_F / ||ref||_F (the tolerance form
+// the north star states: fp32 <= 1e-5, bf16 <= 1e-2). NaN yields NaN.
+double apko_rel_frobenius(const float* got, const double* ref, int64_t n) {
+  long double num = 0.0L, den = 0.0L;
+  for (int64_t i = 0; i < n; ++i) {
+    const long double d = (long double)got[i] - (long double)ref[i];
+    num += d * d;
+    den += (long double)ref[i] * (long double)ref[i];
+  }
+  if (den == 0.0L) return num == 0.0L ? 0.0 : INFINITY;
+  return (double)std::sqrt(num / den);
+}
+
+// Nearest-rank percentile: sort, then v[min(int(q*n), n-1)]
+// (src/yield.cu:322-325, src/urgent_baseline.cu:139-142).
+double apko_percentile(const double* v, int64_t n, double q) {
+  if (n <= 0) return NAN;
+  std::vector<double> s(v, v + n);
+  std::sort(s.begin(), s.end());
+  const int64_t idx = std::min((int64_t)(q * (double)n), n - 1);
+  return s[(size_t)idx];
+}
+
+// ---------------------------------------------------------------------------
+// std::mt19937 (Matsumoto & Nishimura 1998, parameters fixed by C++11
+// [rand.predef]) restated, then libstdc++'s generate_canonical<double, 53>
+// over two 32-bit draws and uniform_real_distribution a + (b-a)*u. The
+// reference builds its event schedule this way (src/yield.cu:824-830,
+// src/midyield.cu:625-630, src/tcyield.cu:689-695; trial delays
+// src/urgent_baseline.cu:310-311).
+typedef struct apko_mt {
+  uint32_t mt[624];
+  int idx;
+} apko_mt;
+
+void apko_mt_seed(apko_mt* g, uint32_t seed) {
+  g->mt[0] = seed;
+  for (int i = 1; i < 624; ++i)
+    g->mt[i] = 1812433253u * (g->mt[i - 1] ^ (g->mt[i - 1] >> 30)) + (uint32_t)i;
+  g->idx = 624;
+}
+
+uint32_t apko_mt_next(apko_mt* g) {
+  if (g->idx >= 624) {
+    for (int i = 0; i < 624; ++i) {
+      const uint32_t y = (g->mt[i] & 0x80000000u) | (g->mt[(i + 1) % 624] & 0x7fffffffu);
+      g->mt[i] = g->mt[(i + 397) % 624] ^ (y >> 1) ^ ((y & 1u) ? 0x9908b0dfu : 0u);
+    }
+    g->idx = 0;
+  }
+  uint32_t y = g->mt[g->idx++];
+  y ^= y >> 11;
+  y ^= (y << 7) & 0x9d2c5680u;
+  y ^= (y << 15) & 0xefc60000u;
+  y ^= y >> 18;
+  return y;
+}
+
+void apko_mt_stream(uint32_t seed, uint32_t* out, int64_t n) {
+  apko_mt g;
+  apko_mt_seed(&g, seed);
+  for (int64_t i = 0; i < n; ++i) out[i] = apko_mt_next(&g);
+}
+
+double apko_mt_canonical(apko_mt* g) {
+  const double lo = (double)apko_mt_next(g);
+  const double hi = (double)apko_mt_next(g);
+  double r = (lo + hi * 4294967296.0) / 18446744073709551616.0;
+  if (r >= 1.0) r = std::nextafter(1.0, 0.0);
+  return r;
+}
+
+// Cumulative event schedule in ns: gaps U(gmin_us*1e3, gmax_us*1e3), each
+// truncated to long long, prefix-summed (src/yield.cu:824-830).
+void apko_uniform_gap_schedule(uint32_t seed, double gmin_us, double gmax_us,
+                               int events, int64_t* out_cum_ns) {
+  apko_mt g;
+  apko_mt_seed(&g, seed);
+  const double a = gmin_us * 1000.0, b = gmax_us * 1000.0;
+  int64_t acc = 0;
+  for (int e = 0; e < events; ++e) {
+    const double u = apko_mt_canonical(&g);
+    acc += (int64_t)(a + (b - a) * u);
+    out_cum_ns[e] = acc;
+  }
+}
+
+// Exponential inter-arrival schedule (the BASELINE cfg3 arrival process; no
+// reference counterpart): gap = -mean * log(1 - u) as libstdc++'s
+// exponential_distribution computes it, truncated to ns, prefix-summed.
+void apko_exp_gap_schedule(uint32_t seed, double mean_us, int events,
+                           int64_t* out_cum_ns) {
+  apko_mt g;
+  apko_mt_seed(&g, seed);
+  int64_t acc = 0;
+  for (int e = 0; e < events; ++e) {
+    const double u = apko_mt_canonical(&g);
+    const double gap_ns = -std::log(1.0 - u) / (1.0 / (mean_us * 1000.0));
+    acc += (int64_t)gap_ns;
+    out_cum_ns[e] = acc;
+  }
+}
+
+// ABAB ordering of the overhead measurement: in rep r, the poll-on variant
+// runs first in even pairs and second in odd pairs (src/yield.cu:675-678).
+int apko_abab_poll(int r) {
+  return ((r / 2) % 2 == 0) ? (r % 2 == 0) : (r % 2 == 1);
+}
+
+// ---------------------------------------------------------------------------
+// bfloat16 round-to-nearest-even of an fp32 value (NaN kept quiet). The bf16
+// path quantizes its inputs this way and checks against float64 on the
+// quantized values, as src/tcyield.cu:459-473 does for fp16.
+uint16_t apko_bf16_rne(float x) {
+  uint32_t u;
+  std::memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  const uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+float apko_bf16_to_f32(uint16_t h) {
+  const uint32_t u = (uint32_t)h << 16;
+  float f;
+  std::memcpy(&f, &u, 4);
+  return f;
+}
+
+// N(0,1) inputs for the bf16 configuration: Box-Muller over mt19937 canonical
+// draws (u1 in (0,1], u2 in [0,1)), both outputs of each pair used, A first
+// then B, each value rounded to bf16 (RNE). `deq` receives the dequantized
+// float of every bf16 value (what the float64 check multiplies).
+void apko_fill_normal_bf16(uint32_t seed, uint16_t* A, float* Adeq, int64_t nA,
+                           uint16_t* B, float* Bdeq, int64_t nB) {
+  apko_mt g;
+  apko_mt_seed(&g, seed);
+  const double two_pi = 6.283185307179586476925286766559;
+  bool have = false;
+  double spare = 0.0;
+  auto next = [&]() -> float {
+    if (have) {
+      have = false;
+      return (float)spare;
+    }
+    const double u1 = 1.0 - apko_mt_canonical(&g);
+    const double u2 = apko_mt_canonical(&g);
+    const double r = std::sqrt(-2.0 * std::log(u1));
+    spare = r * std::sin(two_pi * u2);
+    have = true;
+    return (float)(r * std::cos(two_pi * u2));
+  };
+  for (int64_t i = 0; i < nA; ++i) {
+    A[i] = apko_bf16_rne(next());
+    if (Adeq) Adeq[i] = apko_bf16_to_f32(A[i]);
+  }
+  for (int64_t i = 0; i < nB; ++i) {
+    B[i] = apko_bf16_rne(next());
+    if (Bdeq) Bdeq[i] = apko_bf16_to_f32(B[i]);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Exactly-once predicates (src/yield.cu:630-662, src/midyield.cu:767-788).
+// Task counts: every entry must be exactly 1; >1 is a duplicate, 0 a miss.
+void apko_count_tasks(const int32_t* exec, int64_t n, int64_t* dup,
+                      int64_t* missed, int64_t* first_bad) {
+  int64_t d = 0, m = 0, fb = -1;
+  for (int64_t t = 0; t < n; ++t) {
+    if (exec[t] != 1) {
+      if (exec[t] > 1) ++d;
+      else ++m;
+      if (fb < 0) fb = t;
+    }
+  }
+  *dup = d;
+  *missed = m;
+  *first_bad = fb;
+}
+
+// Event predicates: for every fired event (setGT != 0) the urgent count must
+// equal `urgent_per_event` and a claimant must be recorded; fired == events.
+// Returns 1 on PASS.
+int apko_count_events(const int64_t* set_gt, const int32_t* uexec,
+                      const int32_t* claim, int events, int urgent_per_event,
+                      int* fired, int* bad_u, int* unclaimed) {
+  int f = 0, b = 0, u = 0;
+  for (int e = 0; e < events; ++e) {
+    if (set_gt[e] == 0) continue;
+    ++f;
+    if (uexec[e] != urgent_per_event) ++b;
+    if (claim && claim[e] == 0) ++u;
+  }
+  *fired = f;
+  *bad_u = b;
+  *unclaimed = u;
+  return (b == 0 && u == 0 && f == events) ? 1 : 0;
+}
+
+// ---------------------------------------------------------------------------
+// Bit-exact tile fingerprint used by the yield-safety checks: a wrapping sum
+// over elements of mix64(bits(x_e) + (e << 32)), where e is the element index
+// inside the tile (row-major, tile_m x tile_n) and mix64 is the splitmix64
+// finalizer. Order-independent (a sum), position-sensitive (e enters the
+// hash), and any single-bit change alters the result with overwhelming
+// probability. The device computes the same definition in its epilogue.
+static inline uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
+uint64_t apko_tile_hash(const float* C, int ldc, int row0, int col0,
+                        int tile_m, int tile_n) {
+  uint64_t h = 0;
+  for (int i = 0; i < tile_m; ++i)
+    for (int j = 0; j < tile_n; ++j) {
+      uint32_t bits;
+      std::memcpy(&bits, &C[(size_t)(row0 + i) * ldc + (col0 + j)], 4);
+      const uint64_t e = (uint64_t)(i * tile_n + j);
+      h += mix64((uint64_t)bits + (e << 32));
+    }
+  return h;
+}
+
+}  // extern "C"

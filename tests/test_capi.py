@@ -1,0 +1,55 @@
+"""C ABI surface on the CPU: the library loads, exports every function that
+include/apk.h declares, and rejects bad arguments before touching a GPU."""
+import ctypes
+import subprocess
+
+import pytest
+
+import apk_amd
+
+
+def test_header_declares_functions():
+    syms = apk_amd.header_symbols()
+    assert "apk_persistent_gemm" in syms and "apk_last_error" in syms
+    assert len(syms) >= 5
+
+
+def test_library_exports_every_header_symbol():
+    lib = apk_amd.load()
+    missing = [s for s in apk_amd.header_symbols() if not hasattr(lib, s)]
+    assert not missing, missing
+    out = subprocess.check_output(["nm", "-D", "--defined-only", apk_amd.LIB_PATH]).decode()
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    assert set(apk_amd.header_symbols()) <= exported
+
+
+def test_engine_geometry():
+    g = apk_amd.geometry(apk_amd.ENGINE_VALU64)
+    assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (64, 64, 32, 256)
+    g = apk_amd.geometry(apk_amd.ENGINE_MFMA128)
+    assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (128, 128, 32, 256)
+    assert g.lds_bytes <= 160 * 1024
+    with pytest.raises(apk_amd.ApkError):
+        apk_amd.geometry(99)
+
+
+@pytest.mark.parametrize("engine,M,N,K,kc,blocks,frag", [
+    (apk_amd.ENGINE_VALU64, 100, 64, 64, 64, 4, "multiples"),
+    (apk_amd.ENGINE_MFMA128, 128, 128, 96, 64, 4, "k_chunk"),
+    (apk_amd.ENGINE_MFMA128, 128, 128, 64, 48, 4, "k_chunk"),
+    (apk_amd.ENGINE_VALU64, 64, 64, 64, 64, 0, "blocks"),
+    (apk_amd.ENGINE_VALU64, 0, 64, 64, 64, 1, "empty"),
+    (7, 64, 64, 64, 64, 1, "engine"),
+])
+def test_persistent_gemm_rejects_bad_args(engine, M, N, K, kc, blocks, frag):
+    lib = apk_amd.load()
+    fake = ctypes.c_void_p(0x1000)   # never dereferenced: rejected on the host
+    rc = lib.apk_persistent_gemm(engine, fake, fake, fake, M, N, K, kc, fake, None, blocks, None)
+    assert rc == apk_amd.APK_EINVAL
+    assert frag in lib.apk_last_error().decode()
+
+
+def test_null_pointers_rejected():
+    lib = apk_amd.load()
+    rc = lib.apk_persistent_gemm(0, None, None, None, 64, 64, 64, 64, None, None, 1, None)
+    assert rc == apk_amd.APK_EINVAL
