@@ -55,6 +55,19 @@ def cpu_baseline(A_host, B_host, C_gpu_rows, rows):
     }, frob
 
 
+def measured_traffic(profile="profiles/persistent_gemm_mfma128_cfg2.md"):
+    """HBM-side bytes per launch of the GEMM kernel as measured by the two
+    rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE, scaled by a plain copy) and
+    recorded in the profile summary; None if not recorded."""
+    path = os.path.join(ROOT, profile)
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1])
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -64,6 +77,9 @@ def main():
     ap.add_argument("--k-chunk", type=int, default=32)
     ap.add_argument("--cpu-rows", type=int, default=1024)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="only run a plain device-to-device copy of MIB MiB (the "
+                         "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -77,6 +93,15 @@ def main():
     import apk_amd
 
     torch.cuda.set_device(0)
+    if args.calibrate_copy:
+        n = args.calibrate_copy * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device="cuda")
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log(f"copied {args.calibrate_copy} MiB x3")
+        return
     apk_amd.load()
     info = apk_amd.device_info()
     eng = apk_amd.ENGINE_MFMA128
@@ -150,7 +175,7 @@ def main():
             "peak": PEAK_FP32_TF,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_TF, 4),
-            "traffic": None,
+            "traffic": measured_traffic() if (S, kc) == (4096, 32) else None,
         },
     }
     if not args.no_cpu:
