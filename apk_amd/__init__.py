@@ -43,6 +43,33 @@ class EngineGeometry(ctypes.Structure):
                 ("lds_bytes", ctypes.c_int)]
 
 
+POLL_OFF, POLL_CHUNK, POLL_STAGE = 0, 1, 2
+RESUME_CKPT_FULL, RESUME_CKPT_ACC, RESUME_RESTART = 0, 1, 2
+FLAG_STRIDE, FLAG_MAX_COPIES = 4096, 256
+
+
+class YieldParams(ctypes.Structure):
+    """Mirror of apk_yield_params (include/apk.h); pointers are device
+    addresses as ints."""
+    _fields_ = [
+        ("A", ctypes.c_void_p), ("B", ctypes.c_void_p), ("C", ctypes.c_void_p),
+        ("M", ctypes.c_int), ("N", ctypes.c_int), ("K", ctypes.c_int), ("k_chunk", ctypes.c_int),
+        ("num_tasks", ctypes.c_uint), ("next_task", ctypes.c_void_p),
+        ("Au", ctypes.c_void_p), ("Bu", ctypes.c_void_p), ("Cu", ctypes.c_void_p),
+        ("Mu", ctypes.c_int), ("Nu", ctypes.c_int), ("Ku", ctypes.c_int),
+        ("uq_next", ctypes.c_void_p),
+        ("flag", ctypes.c_void_p), ("flag_copies", ctypes.c_int), ("flag_system", ctypes.c_int),
+        ("flag_set", ctypes.c_void_p),
+        ("sched", ctypes.c_void_p), ("num_events", ctypes.c_int),
+        ("stop_after", ctypes.c_longlong), ("poll_every", ctypes.c_int),
+        ("set_gt", ctypes.c_void_p), ("obs_gt", ctypes.c_void_p), ("claim", ctypes.c_void_p),
+        ("claim_site", ctypes.c_void_p), ("u_gt", ctypes.c_void_p), ("u_end_max", ctypes.c_void_p),
+        ("resume", ctypes.c_int), ("ckpt", ctypes.c_void_p), ("poison", ctypes.c_int),
+        ("task_hash", ctypes.c_void_p), ("u_hash", ctypes.c_void_p), ("stats", ctypes.c_void_p),
+        ("exec_count", ctypes.c_void_p), ("u_exec_count", ctypes.c_void_p),
+    ]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _SIGNATURES = {
@@ -51,6 +78,9 @@ _SIGNATURES = {
     "apk_engine_geometry_of": (_I, [_I, ctypes.POINTER(EngineGeometry)]),
     "apk_persistent_gemm_occupancy": (_I, [_I, ctypes.POINTER(_I)]),
     "apk_persistent_gemm": (_I, [_I, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
+    "apk_persistent_yield": (_I, [_I, _I, _I, ctypes.POINTER(YieldParams), _I, _P]),
+    "apk_yield_ckpt_floats": (ctypes.c_longlong, [_I]),
+    "apk_persistent_yield_occupancy": (_I, [_I, _I, ctypes.POINTER(_I)]),
 }
 
 _lib = None
@@ -109,3 +139,19 @@ def persistent_gemm(engine, A, B, C, M, N, K, k_chunk, next_task, log, blocks,
     """Launch apk_persistent_gemm on device pointers (ints). Asynchronous."""
     check(load().apk_persistent_gemm(engine, A, B, C, M, N, K, k_chunk,
                                      next_task, log, blocks, stream))
+
+
+def yield_occupancy(engine, poll):
+    n = ctypes.c_int(0)
+    check(load().apk_persistent_yield_occupancy(engine, poll, ctypes.byref(n)))
+    return n.value
+
+
+def ckpt_floats(engine):
+    return int(load().apk_yield_ckpt_floats(engine))
+
+
+def persistent_yield(engine, poll, oracle, params, blocks, stream=0):
+    """Launch apk_persistent_yield with a YieldParams. Asynchronous."""
+    check(load().apk_persistent_yield(engine, poll, 1 if oracle else 0,
+                                      ctypes.byref(params), blocks, stream))

@@ -106,4 +106,16 @@ __device__ __forceinline__ void load_lds_x4(i32x4 rsrc, const void* lds_base,
 
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
 
+// A value every lane of the block holds identically (read from LDS after a
+// barrier), made scalar for the compiler. Loop exits and branches that
+// enclose barriers must be taken on such values: if the compiler sees a
+// per-lane (VGPR) condition it may structurize the loop as a divergent one,
+// park some lanes of a wave outside an inner loop and let the others run
+// through barriers on their own -- a block that deadlocks or livelocks even
+// though the value was uniform at run time.
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ unsigned uniform(unsigned v) {
+  return (unsigned)__builtin_amdgcn_readfirstlane((int)v);
+}
+
 }  // namespace apk

@@ -36,6 +36,7 @@ struct EngMfma128 {
   static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 4 per thread
   static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 4 per thread
   static constexpr int LOADS = LOADS_A + LOADS_B;           // per stage
+  static constexpr int ACC_PER_THREAD = 64;                 // floats
 
   struct Acc {
     f32x16 c[2][2];
@@ -67,11 +68,11 @@ struct EngMfma128 {
 
   // Issue the direct-to-LDS loads of k-stage `s` (k0 = s*KS) of the tile at
   // (row0, col0) into ring slot `buf`. LOADS instructions per thread.
-  static __device__ __forceinline__ void issue(char* smem, const Ctx& c, int buf,
+  static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot,
                                                int row0, int col0, int s) {
     const int w = threadIdx.x >> 6, l = lane_id();
     const int k0 = s * KS;
-    char* abase = smem + buf * STAGE;
+    char* abase = ring + slot * STAGE;
     char* bbase = abase + A_STAGE;
 #pragma unroll
     for (int i = 0; i < LOADS_A; ++i) {
@@ -90,12 +91,12 @@ struct EngMfma128 {
     }
   }
 
-  static __device__ __forceinline__ void compute(const char* smem, int buf,
+  static __device__ __forceinline__ void compute(const char* ring, int slot,
                                                  Acc& acc) {
     const int w = threadIdx.x >> 6, l = lane_id();
     const int wm = w & 1, wn = w >> 1;
     const int lr = l & 31, h = l >> 5;
-    const char* abase = smem + buf * STAGE;
+    const char* abase = ring + slot * STAGE;
     const float* bbase = (const float*)(abase + A_STAGE);
 #pragma unroll
     for (int g = 0; g < KS / 8; ++g) {
@@ -124,38 +125,39 @@ struct EngMfma128 {
     }
   }
 
-  // Wait until k-stage s has landed, given `ahead` later stages already
-  // issued behind it (0..NS-1). vmcnt is in-order, so allowing
-  // ahead*LOADS outstanding operations guarantees stage s is complete.
-  static __device__ __forceinline__ void wait_stage(int ahead) {
-    if (ahead >= 2) wait_vmcnt<2 * LOADS>();
-    else if (ahead == 1) wait_vmcnt<LOADS>();
-    else wait_vmcnt<0>();
+  // Output element (tile-relative row, col) of accumulator register e.
+  static __device__ __forceinline__ void coord(int e, int& r, int& c) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w & 1, wn = w >> 1, rb = e >> 5, cb = (e >> 4) & 1, q = e & 15;
+    r = wm * 64 + rb * 32 + 8 * (q >> 2) + 4 * (l >> 5) + (q & 3);
+    c = wn * 64 + cb * 32 + (l & 31);
+  }
+  static __device__ __forceinline__ float get(const Acc& a, int e) {
+    return a.c[e >> 5][(e >> 4) & 1][e & 15];
+  }
+  static __device__ __forceinline__ void set(Acc& a, int e, float v) {
+    a.c[e >> 5][(e >> 4) & 1][e & 15] = v;
   }
 
-  // Software-pipelined K loop over k-stages [s_begin, s_end) of one tile.
-  // hook(s) runs uniformly at the top of every stage, before its prefetch.
-  template <class Hook>
-  static __device__ __forceinline__ void mainloop(char* smem, const Ctx& c,
-                                                  Acc& acc, int row0, int col0,
-                                                  int s_begin, int s_end,
-                                                  Hook&& hook) {
-    constexpr int P = NS - 1;
+  // Write the accumulators into LDS as the row-major TM x TN tile (the ring
+  // is free once a tile's last stage has been computed).
+  static __device__ __forceinline__ void stage_tile(const Acc& acc, char* lds) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w & 1, wn = w >> 1;
+    const int lr = l & 31, h = l >> 5;
+    float* t = (float*)lds;
 #pragma unroll
-    for (int p = 0; p < P; ++p)
-      if (s_begin + p < s_end) issue(smem, c, (s_begin + p) % NS, row0, col0, s_begin + p);
-    for (int s = s_begin; s < s_end; ++s) {
-      hook(s);
-      if (s + P < s_end) issue(smem, c, (s + P) % NS, row0, col0, s + P);
-      const int ahead = (s_end - 1 - s) < P ? (s_end - 1 - s) : P;
-      wait_stage(ahead);
-      lds_sync();
-      compute(smem, s % NS, acc);
-      lds_sync();
-    }
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = wm * 64 + rb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
+          t[row * TN + wn * 64 + cb * 32 + lr] = acc.c[rb][cb][r];
+        }
   }
 
-  static __device__ __forceinline__ void store(const Acc& acc, float* C, int N,
+  static __device__ __forceinline__ void store(const Acc& acc, float* C, int ldc,
                                                int row0, int col0) {
     const int w = threadIdx.x >> 6, l = lane_id();
     const int wm = w & 1, wn = w >> 1;
@@ -168,7 +170,7 @@ struct EngMfma128 {
         for (int r = 0; r < 16; ++r) {
           const int row = row0 + wm * 64 + rb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
           const int col = col0 + wn * 64 + cb * 32 + lr;
-          C[(size_t)row * N + col] = acc.c[rb][cb][r];
+          C[(size_t)row * ldc + col] = acc.c[rb][cb][r];
         }
   }
 };

@@ -5,34 +5,46 @@
 //
 // Block: 256 threads = 4 wave64s; thread (tx = t%16, ty = t/16) owns the 4x4
 // outputs rows ty*4..+3, cols tx*4..+3 (the reference's mapping).
-// Stage: k depth 32. A stage is As[64][33] (one pad float per row keeps the
-// per-row column reads on distinct banks), B stage is Bs[32][64] read as
-// 16-byte vectors. Global loads for stage s+1 are issued into registers
-// before the FMAs of stage s, so load latency overlaps compute.
+// Stage: k depth KS=32, A stage 64x32 fp32 (8 KiB) + B stage 32x64 fp32
+// (8 KiB), filled by buffer_load_dwordx4 ... lds into a 3-slot ring (48 KiB).
+//
+// LDS layouts:
+//  A stage: 64 rows x 128 B. 16-byte quad q of row r sits at slot
+//           q ^ ((r >> 2) & 7). One read instruction of a wave touches the
+//           four rows r, r+4, r+8, r+12 (one per ty of the wave); the swizzle
+//           gives them four different slots, hence different banks.
+//  B stage: 32 rows x 256 B, natural; B[kk][tx*4..+3] is one 16-byte read
+//           per lane, 16 lanes covering 256 contiguous bytes.
 #pragma once
 #include "device.hpp"
 
 namespace apk {
 
 struct EngValu64 {
-  static constexpr int TM = 64, TN = 64, KS = 32, THREADS = 256;
-  static constexpr int LDS_BYTES = (TM * (KS + 1) + KS * TN) * 4;
+  static constexpr int TM = 64, TN = 64, KS = 32, NS = 3, THREADS = 256;
+  static constexpr int A_STAGE = TM * KS * 4;               // 8 KiB
+  static constexpr int B_STAGE = KS * TN * 4;               // 8 KiB
+  static constexpr int STAGE = A_STAGE + B_STAGE;           // 16 KiB
+  static constexpr int LDS_BYTES = NS * STAGE;              // 48 KiB
+  static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 2
+  static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 2
+  static constexpr int LOADS = LOADS_A + LOADS_B;
+  static constexpr int ACC_PER_THREAD = 16;                 // floats
 
   struct Acc {
     float v[4][4];
   };
 
   struct Ctx {
-    const float* A;
-    const float* B;
+    i32x4 ra, rb;
     int K, N;
   };
 
   static __device__ __forceinline__ Ctx make_ctx(const float* A, const float* B,
-                                                 int, int N, int K) {
+                                                 int M, int N, int K) {
     Ctx c;
-    c.A = A;
-    c.B = B;
+    c.ra = make_rsrc(A, (uint32_t)((size_t)M * K * 4));
+    c.rb = make_rsrc(B, (uint32_t)((size_t)K * N * 4));
     c.K = K;
     c.N = N;
     return c;
@@ -45,51 +57,45 @@ struct EngValu64 {
       for (int j = 0; j < 4; ++j) a.v[i][j] = 0.0f;
   }
 
-  struct Regs {
-    float4 a[2], b[2];
-  };
+  static __device__ __forceinline__ int aswz(int r) { return (r >> 2) & 7; }
 
-  static __device__ __forceinline__ void fetch(const Ctx& c, int row0, int col0,
-                                               int s, Regs& r) {
-    const int t = threadIdx.x, k0 = s * KS;
+  static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot,
+                                               int row0, int col0, int s) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int k0 = s * KS;
+    char* abase = ring + slot * STAGE;
+    char* bbase = abase + A_STAGE;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int idx = t + i * THREADS;  // 512 float4 per operand stage
-      const int ar = idx >> 3, aq = idx & 7;
-      r.a[i] = *(const float4*)(c.A + (size_t)(row0 + ar) * c.K + k0 + 4 * aq);
-      const int br = idx >> 4, bq = idx & 15;
-      r.b[i] = *(const float4*)(c.B + (size_t)(k0 + br) * c.N + col0 + 4 * bq);
+    for (int i = 0; i < LOADS_A; ++i) {
+      const int ci = i * 4 + w;          // 1 KiB piece = 8 rows of 128 B
+      const int r = ci * 8 + (l >> 3);
+      const int q = (l & 7) ^ aswz(r);
+      const uint32_t off = (uint32_t)(((row0 + r) * c.K + k0 + 4 * q) * 4);
+      load_lds_x4(c.ra, abase + ci * 1024, off);
+    }
+#pragma unroll
+    for (int i = 0; i < LOADS_B; ++i) {
+      const int ci = i * 4 + w;          // 1 KiB piece = 4 rows of 256 B
+      const int r = ci * 4 + (l >> 4);
+      const uint32_t off = (uint32_t)(((k0 + r) * c.N + col0 + 4 * (l & 15)) * 4);
+      load_lds_x4(c.rb, bbase + ci * 1024, off);
     }
   }
 
-  static __device__ __forceinline__ void put(char* smem, const Regs& r) {
-    float* As = (float*)smem;            // [64][33]
-    float* Bs = As + TM * (KS + 1);      // [32][64]
-    const int t = threadIdx.x;
-#pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int idx = t + i * THREADS;
-      const int ar = idx >> 3, aq = idx & 7;
-      float* ap = As + ar * (KS + 1) + 4 * aq;
-      ap[0] = r.a[i].x;
-      ap[1] = r.a[i].y;
-      ap[2] = r.a[i].z;
-      ap[3] = r.a[i].w;
-      const int br = idx >> 4, bq = idx & 15;
-      *(float4*)(Bs + br * TN + 4 * bq) = r.b[i];
-    }
-  }
-
-  static __device__ __forceinline__ void compute(const char* smem, Acc& acc) {
-    const float* As = (const float*)smem;
-    const float* Bs = As + TM * (KS + 1);
+  static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {
+    const char* abase = ring + slot * STAGE;
+    const float* bs = (const float*)(abase + A_STAGE);
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
       float a[4];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) a[i] = As[(ty * 4 + i) * (KS + 1) + kk];
-      const float4 b = *(const float4*)(Bs + kk * TN + tx * 4);
+      for (int i = 0; i < 4; ++i) {
+        const int r = ty * 4 + i;
+        const int slotq = (kk >> 2) ^ aswz(r);
+        a[i] = *(const float*)(abase + r * 128 + slotq * 16 + (kk & 3) * 4);
+      }
+      const float4 b = *(const float4*)(bs + kk * TN + tx * 4);
       const float bb[4] = {b.x, b.y, b.z, b.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -98,30 +104,37 @@ struct EngValu64 {
     }
   }
 
-  template <class Hook>
-  static __device__ __forceinline__ void mainloop(char* smem, const Ctx& c,
-                                                  Acc& acc, int row0, int col0,
-                                                  int s_begin, int s_end,
-                                                  Hook&& hook) {
-    Regs r;
-    if (s_begin < s_end) fetch(c, row0, col0, s_begin, r);
-    for (int s = s_begin; s < s_end; ++s) {
-      hook(s);
-      put(smem, r);
-      __syncthreads();
-      if (s + 1 < s_end) fetch(c, row0, col0, s + 1, r);
-      compute(smem, acc);
-      __syncthreads();
+  // Output element (tile-relative row, col) of accumulator register e.
+  static __device__ __forceinline__ void coord(int e, int& r, int& c) {
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    r = ty * 4 + (e >> 2);
+    c = tx * 4 + (e & 3);
+  }
+  static __device__ __forceinline__ float get(const Acc& a, int e) {
+    return a.v[e >> 2][e & 3];
+  }
+  static __device__ __forceinline__ void set(Acc& a, int e, float v) {
+    a.v[e >> 2][e & 3] = v;
+  }
+
+  // Write the accumulators into LDS as the row-major TM x TN tile.
+  static __device__ __forceinline__ void stage_tile(const Acc& acc, char* lds) {
+    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
+    float* t = (float*)lds;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float4 v = {acc.v[i][0], acc.v[i][1], acc.v[i][2], acc.v[i][3]};
+      *(float4*)(t + (ty * 4 + i) * TN + tx * 4) = v;
     }
   }
 
-  static __device__ __forceinline__ void store(const Acc& acc, float* C, int N,
+  static __device__ __forceinline__ void store(const Acc& acc, float* C, int ldc,
                                                int row0, int col0) {
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       float4 v = {acc.v[i][0], acc.v[i][1], acc.v[i][2], acc.v[i][3]};
-      *(float4*)(C + (size_t)(row0 + ty * 4 + i) * N + col0 + tx * 4) = v;
+      *(float4*)(C + (size_t)(row0 + ty * 4 + i) * ldc + col0 + tx * 4) = v;
     }
   }
 };

@@ -10,6 +10,7 @@
 #include "capi.hpp"
 #include "engine_mfma128.hpp"
 #include "engine_valu64.hpp"
+#include "pipeline.hpp"
 
 namespace apk {
 
@@ -18,7 +19,7 @@ __global__ void __launch_bounds__(E::THREADS)
     k_persistent_gemm(const float* __restrict__ A, const float* __restrict__ B,
                       float* __restrict__ C, int M, int N, int K, int kChunk,
                       unsigned* next_task, apk_tile_record* log) {
-  __shared__ __attribute__((aligned(16))) char smem[E::LDS_BYTES];
+  __shared__ __attribute__((aligned(16))) char ring[E::LDS_BYTES];
   __shared__ unsigned s_task;
 
   const int tilesN = N / E::TN;
@@ -28,9 +29,12 @@ __global__ void __launch_bounds__(E::THREADS)
   const typename E::Ctx ctx = E::make_ctx(A, B, M, N, K);
 
   for (;;) {
+    // Reconverge before the thread-0 pop (no thread-0 region of the previous
+    // iteration may be threaded into this one across the back-edge).
+    lds_sync();
     if (threadIdx.x == 0) s_task = fetch_add_u32(next_task, 1u);
     __syncthreads();
-    const unsigned task = s_task;
+    const unsigned task = uniform(s_task);
     __syncthreads();  // every thread has read s_task before it is rewritten
     if (task >= numTasks) break;
 
@@ -41,7 +45,7 @@ __global__ void __launch_bounds__(E::THREADS)
 
     typename E::Acc acc;
     E::zero(acc);
-    E::mainloop(smem, ctx, acc, row0, col0, 0, K / E::KS, [&](int s) {
+    run_stages<E>(ring, ctx, acc, row0, col0, K / E::KS, [&](int s) {
       if (threadIdx.x == 0 && rec && s % spc == 0) {
         const int64_t now = wall_ticks();
         const int c = s / spc;
@@ -54,7 +58,7 @@ __global__ void __launch_bounds__(E::THREADS)
         prev = now;
       }
     });
-    E::store(acc, C, N, row0, col0);
+    store_tile<E>(acc, ring, C, N, row0, col0, false);
     __syncthreads();  // whole tile committed before the clock closes
     if (threadIdx.x == 0 && rec) {
       rec[nChunks - 1].start = prev;

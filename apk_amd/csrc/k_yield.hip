@@ -1,0 +1,379 @@
+// k_yield.hip -- the preemptible persistent GEMM (cooperative arm).
+//
+// Counterpart of persistent_yield (reference src/yield.cu:95-204) and
+// persistent_midyield (src/midyield.cu:92-320), rebuilt around the gfx950
+// direct-to-LDS pipeline:
+//  * workers pop output tiles from an HBM fetch-add queue (tasks cycle the
+//    tile grid) and walk each tile's K in LDS k-stages;
+//  * the generation flag is sampled by a direct-to-LDS load issued just
+//    before each stage's data loads; it lands with that stage, so reading it
+//    costs one LDS read and never a stall (the value is two stages old);
+//  * at poll sites (every poll_every chunks, or every stage) a new generation
+//    is logged by every block; blocks that pop an urgent tile from the
+//    event's mini-queue yield: drain, checkpoint (accumulators and live LDS
+//    stages to HBM), run urgent tiles through the same ring, restore,
+//    continue -- the tile's k order is untouched, so C is bit-identical to an
+//    unpreempted run;
+//  * block 0 optionally acts as the device setter of a pre-scheduled event
+//    train (src/yield.cu:186-195).
+// Every branch that contains a barrier is taken on values all threads read
+// from LDS after a barrier (the snapshot discipline of src/midyield.cu:
+// 177-200), so a block never splits across barriers.
+#include "capi.hpp"
+#include "engine_mfma128.hpp"
+#include "engine_valu64.hpp"
+#include "pipeline.hpp"
+
+namespace apk {
+
+template <class E, int POLL, bool ORACLE, bool SYS>
+__global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield_params P) {
+  __shared__ __attribute__((aligned(16))) char ring[E::LDS_BYTES];
+  __shared__ int flagring[E::NS][E::THREADS / 64];  // sample preceding stage s: [s % NS][wave]
+  __shared__ unsigned s_u32;
+  __shared__ uint64_t s_red[E::THREADS / 64];
+
+  const int tid = threadIdx.x, bid = blockIdx.x, G = gridDim.x;
+  const int wave = tid >> 6;
+  const int tilesN = P.N / E::TN;
+  const int totalTiles = (P.M / E::TM) * tilesN;
+  const int S = P.K / E::KS;
+  const int spc = P.k_chunk / E::KS;
+  const int pollStride =
+      (POLL == APK_POLL_STAGE) ? 1 : spc * (P.poll_every > 0 ? P.poll_every : 1);
+  const int uTilesN = P.Nu > 0 ? P.Nu / E::TN : 1;
+  const int U = (P.Au && P.Mu > 0 && P.Nu > 0) ? (P.Mu / E::TM) * uTilesN : 0;
+  const int Su = P.Ku / E::KS;
+  const typename E::Ctx ctx = E::make_ctx(P.A, P.B, P.M, P.N, P.K);
+  const typename E::Ctx uctx = E::make_ctx(U ? P.Au : P.A, U ? P.Bu : P.B, P.Mu, P.Nu, P.Ku);
+  const int copies = P.flag_copies > 0 ? P.flag_copies : 1;
+  const i32x4 flag_rsrc =
+      make_rsrc((const char*)P.flag + (size_t)(bid % copies) * APK_FLAG_STRIDE, 4);
+  const i32x4 dummy_rsrc = make_rsrc(P.A, 4);
+  float* ckslot = P.ckpt ? P.ckpt + (size_t)bid * Ckpt<E>::SLOT_FLOATS : nullptr;
+  const bool isSetter = P.flag_set != nullptr && P.sched != nullptr && bid == 0;
+
+  if (tid < E::NS * (E::THREADS / 64)) (&flagring[0][0])[tid] = 0;
+  __syncthreads();
+
+  int lastSeen = 0;     // uniform: every thread derives it from the same samples
+  int fLatest = 0;      // freshest landed sample, for the task-boundary stop check
+  int nextEv = 0;       // setter state (thread 0 of block 0)
+  int64_t gBase = 0;
+  uint64_t stYields = 0, stSave = 0, stUrgent = 0, stRestore = 0;
+
+  // Stages that are poll sites carry a flag sample issued just in front of
+  // their data loads (all waves, same op count).
+  auto sampled = [&](int s) { return POLL != APK_POLL_OFF && s % pollStride == 0; };
+  auto issue_stage = [&](const typename E::Ctx& c, int row0, int col0, int s) {
+    if (sampled(s)) sample_flag<SYS>(flag_rsrc, dummy_rsrc, &flagring[s % E::NS][wave]);
+    E::issue(ring, c, s % E::NS, row0, col0, s);
+  };
+  // Operations issued after stage s's loads by the `ahead` later stages.
+  auto ops_after = [&](int s, int ahead) {
+    int n = 0;
+    for (int j = 1; j <= ahead; ++j) n += E::LOADS + (sampled(s + j) ? 1 : 0);
+    return n;
+  };
+  auto set_flag = [&](int v) {
+    for (int c = 0; c < copies; ++c)
+      flag_store((int*)((char*)P.flag_set + (size_t)c * APK_FLAG_STRIDE), v);
+  };
+
+  // Broadcast a value thread 0 computed (uniform afterwards).
+  auto bcast = [&](unsigned v) -> unsigned {
+    if (tid == 0) s_u32 = v;
+    lds_sync();
+    const unsigned r = uniform(s_u32);
+    lds_sync();
+    return r;
+  };
+
+  auto pop_urgent = [&](int ev) -> int {
+    unsigned v = 0;
+    if (tid == 0) v = (unsigned)fetch_add_i32(&P.uq_next[ev], 1);
+    return (int)bcast(v);
+  };
+
+  // One urgent tile through the ring (non-preemptible).
+  auto urgent_tile = [&](int uidx, int ev) {
+    const int ur0 = (uidx / uTilesN) * E::TM, uc0 = (uidx % uTilesN) * E::TN;
+    typename E::Acc ua;
+    E::zero(ua);
+    if (Su > 0) E::issue(ring, uctx, 0, ur0, uc0, 0);
+    if (Su > 1) E::issue(ring, uctx, 1, ur0, uc0, 1);
+    for (int t = 0; t < Su; ++t) {
+      if (t + kPrefetch < Su) E::issue(ring, uctx, (t + kPrefetch) % E::NS, ur0, uc0, t + kPrefetch);
+      wait_stage<E, 0>(Su - 1 - t < kPrefetch ? Su - 1 - t : kPrefetch);
+      lds_sync();
+      if (P.poison && t == 0) {
+        if (tid == 0) *(float*)(ring + E::A_STAGE) += 1.0f;  // staged B[0][uc0]
+        lds_sync();
+      }
+      E::compute(ring, t % E::NS, ua);
+      lds_sync();
+    }
+    const uint64_t hp = store_tile<E>(ua, ring, P.Cu, P.Nu, ur0, uc0, P.u_hash != nullptr);
+    if (P.u_hash) {
+      const uint64_t h = block_sum_u64(hp, s_red);
+      if (tid == 0) P.u_hash[(size_t)ev * U + uidx] = h;
+    }
+    if (ORACLE && tid == 0) fetch_add_i32(&P.u_exec_count[ev], 1);
+  };
+
+  for (;;) {
+    if (POLL != APK_POLL_OFF && fLatest < 0) break;  // host stop sentinel
+    // Reconverge before the thread-0 pop: without a barrier here the
+    // compiler may thread the previous iteration's thread-0 regions into
+    // this one across the back-edge and split the block's lanes over two
+    // loop iterations (lanes 1..63 spinning on a stale task at the barrier
+    // below while lane 0 waits outside the loop to pop the next one).
+    lds_sync();
+    if (tid == 0) s_u32 = fetch_add_u32(P.next_task, 1u);
+    __syncthreads();
+    const unsigned task = uniform(s_u32);
+    __syncthreads();
+    if (task >= P.num_tasks) break;
+
+    const int tile = (int)(task % (unsigned)totalTiles);
+    const int row0 = (tile / tilesN) * E::TM;
+    const int col0 = (tile % tilesN) * E::TN;
+    typename E::Acc acc;
+    E::zero(acc);
+    if (S > 0) issue_stage(ctx, row0, col0, 0);
+    if (S > 1) issue_stage(ctx, row0, col0, 1);
+
+    int s = 0;
+    while (s < S) {
+      if (s + kPrefetch < S) issue_stage(ctx, row0, col0, s + kPrefetch);
+      wait_ops<E>(ops_after(s, S - 1 - s < kPrefetch ? S - 1 - s : kPrefetch));
+      lds_sync();
+
+      if (sampled(s)) {
+        int f = uniform(flagring[s % E::NS][0]);  // sample taken just before stage s was issued
+        fLatest = f;
+        if (isSetter && tid == 0 && f >= 0) {
+          const int64_t now = wall_ticks();
+          if (gBase == 0) gBase = now;
+          if (nextEv < P.num_events) {
+            if (now >= gBase + P.sched[nextEv]) {
+              P.set_gt[nextEv] = now;
+              set_flag(++nextEv);
+            }
+          } else if (P.stop_after > 0 &&
+                     now >= gBase + (P.num_events ? P.sched[P.num_events - 1] : 0) +
+                                P.stop_after) {
+            set_flag(-1);  // self-terminating run: no host in the loop
+          }
+        }
+        if (f > P.num_events) f = P.num_events;  // never index past the event arrays
+        if (f > lastSeen) {
+          const int64_t g = wall_ticks();
+          if (tid == 0)
+            for (int e = lastSeen; e < f; ++e) P.obs_gt[(size_t)e * G + bid] = g;
+          const int ev = f - 1;
+          lastSeen = f;
+          int uidx = U > 0 ? pop_urgent(ev) : U;
+          if (uidx < U) {
+            // ---- yield: this block hands its CU to the urgent job ----
+            wait_vmcnt<0>();
+            lds_sync();  // every wave's in-flight stage loads have landed
+            const int64_t t0 = wall_ticks();
+            const int live = (S - s) < E::NS ? (S - s) : E::NS;  // stages s.. not yet computed
+            if (P.resume != APK_RESUME_RESTART) {
+              Ckpt<E>::save_acc(acc, ckslot);
+              if (P.resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, ckslot, s % E::NS, live);
+            }
+            lds_sync();  // ring reads done before the urgent tile overwrites it
+            const int64_t t1 = wall_ticks();
+            if (uidx == 0 && tid == 0) {
+              P.claim[ev] = bid + 1;
+              P.claim_site[ev] = s;
+              P.u_gt[2 * (size_t)ev] = t1;
+            }
+            while (uidx < U) {
+              urgent_tile(uidx, ev);
+              uidx = pop_urgent(ev);
+            }
+            const int64_t t2 = wall_ticks();
+            if (tid == 0) {
+              atomic_max_u64(&P.u_end_max[ev], (unsigned long long)t2);
+              P.u_gt[2 * (size_t)ev + 1] = t2;
+            }
+            if (P.resume == APK_RESUME_RESTART) {
+              E::zero(acc);
+              s = 0;
+              issue_stage(ctx, row0, col0, 0);
+              if (S > 1) issue_stage(ctx, row0, col0, 1);
+              if (tid == 0) {
+                ++stYields;
+                stSave += (uint64_t)(t1 - t0);
+                stUrgent += (uint64_t)(t2 - t1);
+              }
+              lds_sync();  // reconverge before the back-edge (see the task loop)
+              continue;
+            }
+            Ckpt<E>::load_acc(acc, ckslot);
+            if (P.resume == APK_RESUME_CKPT_FULL) {
+              Ckpt<E>::load_ring(ring, ckslot, s % E::NS, live);
+            } else {
+              for (int k = 0; k < live; ++k) E::issue(ring, ctx, (s + k) % E::NS, row0, col0, s + k);
+              wait_vmcnt<0>();
+            }
+            __syncthreads();  // restored ring visible to all waves
+            const int64_t t3 = wall_ticks();
+            if (tid == 0) {
+              ++stYields;
+              stSave += (uint64_t)(t1 - t0);
+              stUrgent += (uint64_t)(t2 - t1);
+              stRestore += (uint64_t)(t3 - t2);
+            }
+          }
+        }
+      }
+
+      E::compute(ring, s % E::NS, acc);
+      lds_sync();
+      ++s;
+    }
+    if (POLL != APK_POLL_OFF) {  // freshest landed sample of this tile
+      int last = S - 1;
+      while (last > 0 && !sampled(last)) --last;
+      if (S > 0) fLatest = uniform(flagring[last % E::NS][0]);
+    }
+
+    const uint64_t hp = store_tile<E>(acc, ring, P.C, P.N, row0, col0, P.task_hash != nullptr);
+    if (P.task_hash) {
+      const uint64_t h = block_sum_u64(hp, s_red);
+      if (tid == 0) P.task_hash[task] = h;
+    }
+    if (ORACLE && tid == 0) fetch_add_i32(&P.exec_count[task], 1);
+  }
+
+  if (P.stats && tid == 0) {
+    P.stats[(size_t)bid * 4 + 0] = stYields;
+    P.stats[(size_t)bid * 4 + 1] = stSave;
+    P.stats[(size_t)bid * 4 + 2] = stUrgent;
+    P.stats[(size_t)bid * 4 + 3] = stRestore;
+  }
+}
+
+template <class E>
+static int validate(const apk_yield_params* p, int poll, int oracle, int blocks) {
+  APK_REQUIRE(p != nullptr, "persistent_yield: params is NULL");
+  APK_REQUIRE(p->A && p->B && p->C && p->next_task, "persistent_yield: NULL GEMM pointer");
+  APK_REQUIRE(p->M > 0 && p->N > 0 && p->K > 0 && p->M % E::TM == 0 && p->N % E::TN == 0,
+              "persistent_yield: M=%d N=%d K=%d vs %dx%d tiles", p->M, p->N, p->K, E::TM, E::TN);
+  APK_REQUIRE(p->k_chunk > 0 && p->k_chunk % E::KS == 0 && p->K % p->k_chunk == 0,
+              "persistent_yield: k_chunk=%d must divide K=%d and be a multiple of %d",
+              p->k_chunk, p->K, E::KS);
+  APK_REQUIRE((size_t)p->M * p->K * 4 < (1ull << 31) && (size_t)p->K * p->N * 4 < (1ull << 31),
+              "persistent_yield: operands above 2 GiB are not supported");
+  APK_REQUIRE(blocks > 0, "persistent_yield: blocks=%d", blocks);
+  APK_REQUIRE(poll >= APK_POLL_OFF && poll <= APK_POLL_STAGE, "persistent_yield: poll=%d", poll);
+  APK_REQUIRE(p->num_events >= 0, "persistent_yield: num_events < 0");
+  if (poll != APK_POLL_OFF) {
+    APK_REQUIRE(p->flag != nullptr, "persistent_yield: polling needs a flag");
+    APK_REQUIRE(p->flag_copies >= 0 && p->flag_copies <= APK_FLAG_MAX_COPIES,
+                "persistent_yield: flag_copies=%d", p->flag_copies);
+    if (p->num_events > 0)
+      APK_REQUIRE(p->set_gt && p->obs_gt && p->claim && p->claim_site && p->u_gt &&
+                      p->u_end_max && p->uq_next,
+                  "persistent_yield: NULL event array");
+    if (p->flag_set) APK_REQUIRE(p->sched != nullptr, "persistent_yield: setter without schedule");
+    APK_REQUIRE(p->resume >= APK_RESUME_CKPT_FULL && p->resume <= APK_RESUME_RESTART,
+                "persistent_yield: resume=%d", p->resume);
+    if (p->resume != APK_RESUME_RESTART)
+      APK_REQUIRE(p->ckpt != nullptr, "persistent_yield: checkpointing needs ckpt storage");
+  }
+  if (p->Au) {
+    APK_REQUIRE(p->Bu && p->Cu && p->Mu > 0 && p->Nu > 0 && p->Ku > 0 &&
+                    p->Mu % E::TM == 0 && p->Nu % E::TN == 0 && p->Ku % E::KS == 0,
+                "persistent_yield: urgent job %dx%dx%d vs %dx%dx%d granularity", p->Mu,
+                p->Nu, p->Ku, E::TM, E::TN, E::KS);
+  }
+  if (oracle)
+    APK_REQUIRE(p->exec_count && (p->u_exec_count || !p->Au),
+                "persistent_yield: oracle needs count arrays");
+  return APK_OK;
+}
+
+template <class E, int POLL, bool ORACLE, bool SYS>
+static int launch_t(const apk_yield_params* p, int blocks, hipStream_t st) {
+  hipLaunchKernelGGL((k_persistent_yield<E, POLL, ORACLE, SYS>), dim3(blocks),
+                     dim3(E::THREADS), 0, st, *p);
+  APK_LAUNCHED();
+  return APK_OK;
+}
+
+template <class E, int POLL>
+static int launch_p(const apk_yield_params* p, int oracle, int blocks, hipStream_t st) {
+  const bool sys = p->flag_system != 0;
+  if (oracle) return sys ? launch_t<E, POLL, true, true>(p, blocks, st)
+                         : launch_t<E, POLL, true, false>(p, blocks, st);
+  return sys ? launch_t<E, POLL, false, true>(p, blocks, st)
+             : launch_t<E, POLL, false, false>(p, blocks, st);
+}
+
+template <class E>
+static int launch_e(int poll, int oracle, const apk_yield_params* p, int blocks,
+                    hipStream_t st) {
+  const int rc = validate<E>(p, poll, oracle, blocks);
+  if (rc != APK_OK) return rc;
+  switch (poll) {
+    case APK_POLL_OFF: return launch_p<E, APK_POLL_OFF>(p, oracle, blocks, st);
+    case APK_POLL_CHUNK: return launch_p<E, APK_POLL_CHUNK>(p, oracle, blocks, st);
+    default: return launch_p<E, APK_POLL_STAGE>(p, oracle, blocks, st);
+  }
+}
+
+}  // namespace apk
+
+extern "C" int apk_persistent_yield(int engine, int poll, int oracle,
+                                    const apk_yield_params* params, int blocks,
+                                    void* stream) {
+  using namespace apk;
+  switch (engine) {
+    case APK_ENGINE_VALU64:
+      return launch_e<EngValu64>(poll, oracle, params, blocks, as_stream(stream));
+    case APK_ENGINE_MFMA128:
+      return launch_e<EngMfma128>(poll, oracle, params, blocks, as_stream(stream));
+    default:
+      set_error("persistent_yield: unknown engine %d", engine);
+      return APK_EINVAL;
+  }
+}
+
+extern "C" long long apk_yield_ckpt_floats(int engine) {
+  using namespace apk;
+  switch (engine) {
+    case APK_ENGINE_VALU64: return Ckpt<EngValu64>::SLOT_FLOATS;
+    case APK_ENGINE_MFMA128: return Ckpt<EngMfma128>::SLOT_FLOATS;
+    default: return -1;
+  }
+}
+
+extern "C" int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_per_cu) {
+  using namespace apk;
+  APK_REQUIRE(blocks_per_cu != nullptr, "occupancy: out is NULL");
+  int n = 0;
+  auto q = [&](auto kern, int threads) -> int {
+    APK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, 0));
+    return APK_OK;
+  };
+  int rc;
+  switch (engine * 3 + poll) {
+    case 0: rc = q(k_persistent_yield<EngValu64, 0, false, false>, 256); break;
+    case 1: rc = q(k_persistent_yield<EngValu64, 1, false, false>, 256); break;
+    case 2: rc = q(k_persistent_yield<EngValu64, 2, false, false>, 256); break;
+    case 3: rc = q(k_persistent_yield<EngMfma128, 0, false, false>, 256); break;
+    case 4: rc = q(k_persistent_yield<EngMfma128, 1, false, false>, 256); break;
+    case 5: rc = q(k_persistent_yield<EngMfma128, 2, false, false>, 256); break;
+    default:
+      set_error("occupancy: engine %d poll %d", engine, poll);
+      return APK_EINVAL;
+  }
+  if (rc != APK_OK) return rc;
+  *blocks_per_cu = n;
+  return APK_OK;
+}

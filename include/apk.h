@@ -93,6 +93,126 @@ int apk_persistent_gemm(int engine, const float* A, const float* B, float* C,
                         unsigned int* next_task, apk_tile_record* log,
                         int blocks, void* stream);
 
+/* ------------------------------------------------------------------------
+ * Preemptible persistent GEMM (cooperative arm).
+ *
+ * Poll sites: APK_POLL_CHUNK polls at every poll_every-th k-chunk boundary of
+ * a tile (the tile-boundary yield points of src/yield.cu:125-136 once K is
+ * walked in chunks); APK_POLL_STAGE polls at every LDS k-stage (the
+ * mid-pipeline points of src/midyield.cu:246-290). The flag is sampled by a
+ * direct-to-LDS load that retires with the stage data, so a poll never stalls
+ * the pipeline; the value acted on is two stages old.
+ *
+ * On a new generation every block logs its observation time; blocks that pop
+ * an urgent tile from the event's mini-queue (src/yield.cu:155-183) yield:
+ * they drain their in-flight stage loads, checkpoint per `resume`, run urgent
+ * tiles through the same LDS ring until the mini-queue is empty, restore and
+ * continue the interrupted tile.
+ *   APK_RESUME_CKPT_FULL : accumulators + all live LDS stages -> HBM -> back
+ *   APK_RESUME_CKPT_ACC  : accumulators -> HBM -> back; live stages re-fetched
+ *   APK_RESUME_RESTART   : abandon the tile, restart it from k = 0 (the
+ *                          reference's semantics, src/midyield.cu:237-258)
+ * All three produce bit-identical C: the per-tile k order never changes.
+ */
+enum { APK_POLL_OFF = 0, APK_POLL_CHUNK = 1, APK_POLL_STAGE = 2 };
+/* The flag may be replicated so that no single address is polled by every
+ * CU: copy c lives at byte offset c * APK_FLAG_STRIDE. */
+#define APK_FLAG_STRIDE 4096
+#define APK_FLAG_MAX_COPIES 256
+enum { APK_RESUME_CKPT_FULL = 0, APK_RESUME_CKPT_ACC = 1, APK_RESUME_RESTART = 2 };
+
+typedef struct apk_yield_params {
+  /* background GEMM; tasks cycle the tile grid (src/urgent_baseline.cu:78-80) */
+  const float* A;
+  const float* B;
+  float* C;
+  int M, N, K, k_chunk;
+  unsigned int num_tasks;
+  unsigned int* next_task;     /* fetch-add counter, 0 at launch */
+  /* urgent job: Cu (Mu x Nu) = Au (Mu x Ku) . Bu (Ku x Nu), split into tiles
+   * that yielding blocks pop per event */
+  const float* Au;
+  const float* Bu;
+  float* Cu;
+  int Mu, Nu, Ku;
+  int* uq_next;                /* [events] mini-queue counters, 0 at launch */
+  /* generation flag and event bookkeeping (src/yield.cu:96-102); times are
+   * device wall-clock ticks */
+  const int* flag;             /* polled flag: 0 none, e events fired, -1 stop;
+                                  flag_copies ints APK_FLAG_STRIDE bytes apart */
+  int flag_copies;             /* copies of the flag (1..APK_FLAG_MAX_COPIES);
+                                  block b polls copy b % flag_copies */
+  int flag_system;             /* 1: flag is host-mapped memory (system scope) */
+  int* flag_set;               /* device setter target (block 0) with the same
+                                  copies; NULL = none */
+  const long long* sched;      /* [events] cumulative ticks after the setter's first poll */
+  int num_events;
+  long long stop_after;        /* setter stores -1 this many ticks after the
+                                  last scheduled event (0 = never) */
+  int poll_every;              /* chunks between polls (APK_POLL_CHUNK) */
+  long long* set_gt;           /* [events] */
+  long long* obs_gt;           /* [events * blocks] */
+  int* claim;                  /* [events] first popper + 1 */
+  int* claim_site;             /* [events] k-stage of the claimer's yield */
+  long long* u_gt;             /* [2 * events] urgent start / claimer end */
+  unsigned long long* u_end_max; /* [events] last urgent tile completion */
+  /* checkpoint */
+  int resume;                  /* APK_RESUME_* */
+  float* ckpt;                 /* blocks * apk_yield_ckpt_floats(engine) */
+  int poison;                  /* detector control: +1.0 on one staged B value
+                                  of every urgent tile (src/midyield.cu:146-147) */
+  /* verification and statistics (each may be NULL) */
+  unsigned long long* task_hash; /* [num_tasks] fingerprint of each completed task */
+  unsigned long long* u_hash;    /* [events * urgent tiles] */
+  unsigned long long* stats;     /* [blocks * 4]: yields, save, urgent, restore ticks */
+  /* exactly-once oracle (used by the oracle instantiation only) */
+  int* exec_count;             /* [num_tasks] */
+  int* u_exec_count;           /* [events] */
+} apk_yield_params;
+
+/* persistent_yield / persistent_midyield (src/yield.cu:95-204,
+ * src/midyield.cu:92-320) on a gfx950 tile engine. `oracle` selects the
+ * instantiation that counts executions. */
+int apk_persistent_yield(int engine, int poll, int oracle,
+                         const apk_yield_params* params, int blocks, void* stream);
+
+/* Floats of checkpoint storage one block needs (accumulators + LDS ring). */
+long long apk_yield_ckpt_floats(int engine);
+
+/* Resident blocks per CU of the preemptible kernel. */
+int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_per_cu);
+
+/* ------------------------------------------------------------------------
+ * Notification microbenchmark (visibility_poll, src/yield.cu:216-293): every
+ * block loops {work_iters dependent FMAs; optionally one 16-byte read of a
+ * DRAM-resident traffic buffer; barrier; thread 0 loads its flag copy with a
+ * synchronous agent-scope load; block 0 sets events on schedule and stores -1
+ * stop_after ticks after the last one; barrier; log a new generation}. The
+ * flag-load round trip of thread 0 is also timed (load_ticks). Dynamic LDS
+ * of lds_bytes pins residency to that of a tile kernel. */
+typedef struct apk_vis_params {
+  int* flag;                   /* flag_copies ints APK_FLAG_STRIDE apart */
+  int flag_copies;
+  const long long* sched;      /* [events] cumulative ticks */
+  int num_events;
+  long long stop_after;        /* ticks after the last event; must be > 0 */
+  long long max_ticks;         /* hard per-block deadline after its start; must be > 0 */
+  long long* set_gt;           /* [events] */
+  long long* obs_gt;           /* [events * blocks] */
+  int work_iters;
+  int loaded;                  /* 1: read traffic each iteration */
+  const float* traffic;        /* traffic_len float4 */
+  int traffic_len;
+  float* sink;                 /* [blocks * 256] */
+  long long* iter_count;       /* [blocks] iterations run */
+  long long* load_ticks;       /* [blocks * 2]: sum and max of flag-load ticks */
+} apk_vis_params;
+
+int apk_visibility(const apk_vis_params* params, int blocks, int lds_bytes, void* stream);
+
+/* Resident blocks per CU of the visibility kernel with lds_bytes of LDS. */
+int apk_visibility_occupancy(int lds_bytes, int* blocks_per_cu);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,61 @@
+"""Static check of compiled gfx950 kernels: no barrier inside a divergent loop.
+
+A loop whose latch is exec-masked (s_andn2_b64 exec, exec, ...) lets lanes of
+one wave leave it in different iterations. If such a loop contains s_barrier,
+part of a wave can arrive at barriers while other lanes of the same wave wait
+outside the loop -- the block livelocks or deadlocks even when every value
+was uniform at run time. LLVM annotates every basic block with its loop
+nesting ("in Loop: Header=BBx Depth=d"); this walks those annotations.
+"""
+import re
+
+
+def divergent_barrier_loops(asm_text):
+    """Return [(kernel, latch_block, loop_header)] for every violation."""
+    out = []
+    kernel = None
+    blocks = []
+    lines = asm_text.split('\n')
+    for i, l in enumerate(lines):
+        mk = re.match(r'^(_Z\w+):', l)
+        if mk:
+            out += _check(kernel, blocks)
+            kernel, blocks = mk.group(1), []
+            continue
+        _scan(lines, i, l, blocks)
+    out += _check(kernel, blocks)
+    return out
+
+
+def _scan(lines, i, l, blocks):
+    m = re.match(r'^(\.LBB(\d+_\d+)|; %bb\.\d+):?', l)
+    if m and not l.startswith(';;'):
+        cur = {'label': m.group(1), 'inner': None, 'loops': set(), 'lines': []}
+        blocks.append(cur)
+        ann = [l] + [x for x in lines[i + 1:i + 8] if x.lstrip().startswith(';') and 'Loop' in x]
+        best = -1
+        for a in ann:
+            for h, d in re.findall(r'Header=BB(\d+_\d+) Depth=(\d+)', a):
+                cur['loops'].add(h)
+                if int(d) > best:
+                    best, cur['inner'] = int(d), h
+            for h in re.findall(r'Parent Loop BB(\d+_\d+)', a):
+                cur['loops'].add(h)
+            md = re.search(r'This (?:Inner )?Loop Header: Depth=(\d+)', a)
+            if md and m.group(2):
+                cur['loops'].add(m.group(2))
+                if int(md.group(1)) > best:
+                    best, cur['inner'] = int(md.group(1)), m.group(2)
+    elif blocks:
+        blocks[-1]['lines'].append(l)
+
+
+def _check(kernel, blocks):
+    out = []
+    for b in blocks:
+        if any('s_andn2_b64 exec, exec' in l for l in b['lines']) and b['inner']:
+            h = b['inner']
+            body = [x for x in blocks if h in x['loops']]
+            if any(any('s_barrier' in l for l in x['lines']) for x in body):
+                out.append((kernel, b['label'], 'BB' + h))
+    return out

@@ -53,3 +53,46 @@ def test_null_pointers_rejected():
     lib = apk_amd.load()
     rc = lib.apk_persistent_gemm(0, None, None, None, 64, 64, 64, 64, None, None, 1, None)
     assert rc == apk_amd.APK_EINVAL
+
+
+def test_yield_params_layout_matches_header(tmp_path):
+    """The ctypes mirror of apk_yield_params has the C compiler's layout."""
+    src = tmp_path / "sz.c"
+    fields = [f[0] for f in apk_amd.YieldParams._fields_]
+    body = "".join(f'printf("%zu ", offsetof(apk_yield_params, {f}));' for f in fields)
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "apk.h"\n'
+                   'int main(){' + body + 'printf("%zu\\n", sizeof(apk_yield_params));return 0;}\n')
+    exe = tmp_path / "sz"
+    subprocess.check_call(["gcc", "-I", apk_amd.os.path.join(apk_amd.ROOT, "include"),
+                           str(src), "-o", str(exe)])
+    got = [int(x) for x in subprocess.check_output([str(exe)]).split()]
+    want = [getattr(apk_amd.YieldParams, f).offset for f in fields] + [ctypes.sizeof(apk_amd.YieldParams)]
+    assert got == want
+
+
+def test_yield_rejects_bad_args():
+    lib = apk_amd.load()
+    p = apk_amd.YieldParams()
+    fake = 0x1000
+    p.A = p.B = p.C = p.next_task = fake
+    p.M, p.N, p.K, p.k_chunk = 128, 128, 64, 48
+    rc = lib.apk_persistent_yield(apk_amd.ENGINE_MFMA128, apk_amd.POLL_STAGE, 0, ctypes.byref(p), 1, None)
+    assert rc == apk_amd.APK_EINVAL and b"k_chunk" in lib.apk_last_error()
+    p.k_chunk = 32
+    rc = lib.apk_persistent_yield(apk_amd.ENGINE_MFMA128, apk_amd.POLL_STAGE, 0, ctypes.byref(p), 1, None)
+    assert rc == apk_amd.APK_EINVAL and b"flag" in lib.apk_last_error()
+    p.flag = fake
+    p.resume = apk_amd.RESUME_CKPT_FULL
+    rc = lib.apk_persistent_yield(apk_amd.ENGINE_MFMA128, apk_amd.POLL_STAGE, 0, ctypes.byref(p), 1, None)
+    assert rc == apk_amd.APK_EINVAL and b"ckpt" in lib.apk_last_error()
+    p.resume = apk_amd.RESUME_RESTART
+    p.num_events = 3
+    rc = lib.apk_persistent_yield(apk_amd.ENGINE_MFMA128, apk_amd.POLL_STAGE, 0, ctypes.byref(p), 1, None)
+    assert rc == apk_amd.APK_EINVAL and b"event array" in lib.apk_last_error()
+    p.num_events = 0
+    p.Au = fake
+    p.Bu = p.Cu = fake
+    p.Mu, p.Nu, p.Ku = 100, 128, 32
+    rc = lib.apk_persistent_yield(apk_amd.ENGINE_MFMA128, apk_amd.POLL_STAGE, 0, ctypes.byref(p), 1, None)
+    assert rc == apk_amd.APK_EINVAL and b"urgent" in lib.apk_last_error()
+    assert apk_amd.ckpt_floats(apk_amd.ENGINE_MFMA128) == 64 * 256 + 96 * 1024 // 4
