@@ -80,6 +80,27 @@ __device__ __forceinline__ i32x4 make_rsrc(const void* base, uint32_t bytes) {
   return r;
 }
 
+// Compiler-visible buffer loads/stores (tracked by the wait-insertion pass,
+// unlike the direct-to-LDS asm below): wave-uniform base in the resource,
+// per-lane byte offset in a VGPR, a uniform byte offset in an SGPR.
+typedef __amdgpu_buffer_rsrc_t buf_rsrc;
+__device__ __forceinline__ buf_rsrc make_buf_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           0x00020000);
+}
+__device__ __forceinline__ void buf_store_f4(float4 v, buf_rsrc r, int voff, int soff) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 u = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
+                   __float_as_uint(v.w)};
+  __builtin_amdgcn_raw_buffer_store_b128(u, r, voff, soff, 0);
+}
+__device__ __forceinline__ float4 buf_load_f4(buf_rsrc r, int voff, int soff) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 u = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+  return make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z),
+                     __uint_as_float(u.w));
+}
+
 // One 16-byte-per-lane buffer load written straight into LDS: lane l's 16
 // bytes land at lds_base + 16*l (lds_base is wave-uniform, passed in M0).
 //

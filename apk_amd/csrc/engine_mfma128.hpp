@@ -91,29 +91,49 @@ struct EngMfma128 {
     }
   }
 
-  static __device__ __forceinline__ void compute(const char* ring, int slot,
-                                                 Acc& acc) {
+  // Operands of k-group g (8 k values): one 16-byte A read per 32-row
+  // block (the quad 2g+h of the lane's row), four B dwords per 32-column
+  // block.
+  struct Frag {
+    f32x4 a4[2];
+    float bv[2][4];
+  };
+  static __device__ __forceinline__ void load_frag(const char* abase, int g, Frag& f) {
     const int w = threadIdx.x >> 6, l = lane_id();
     const int wm = w & 1, wn = w >> 1;
     const int lr = l & 31, h = l >> 5;
-    const char* abase = ring + slot * STAGE;
     const float* bbase = (const float*)(abase + A_STAGE);
 #pragma unroll
-    for (int g = 0; g < KS / 8; ++g) {
-      f32x4 a4[2];
-      float bv[2][4];
+    for (int rb = 0; rb < 2; ++rb) {
+      const int row = wm * 64 + rb * 32 + lr;
+      const int q = (2 * g + h) ^ (row & 7);
+      f.a4[rb] = *(const f32x4*)(abase + row * 128 + q * 16);
+    }
 #pragma unroll
-      for (int rb = 0; rb < 2; ++rb) {
-        const int row = wm * 64 + rb * 32 + lr;
-        const int slot = (2 * g + h) ^ (row & 7);
-        a4[rb] = *(const f32x4*)(abase + row * 128 + slot * 16);
-      }
+    for (int cb = 0; cb < 2; ++cb) {
+      const int col = wn * 64 + cb * 32 + lr;
 #pragma unroll
-      for (int cb = 0; cb < 2; ++cb) {
-        const int col = wn * 64 + cb * 32 + lr;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) bv[cb][s] = bbase[(8 * g + 4 * h + s) * TN + col];
-      }
+      for (int s = 0; s < 4; ++s) f.bv[cb][s] = bbase[(8 * g + 4 * h + s) * TN + col];
+    }
+  }
+
+  // One k-stage of MFMAs out of ring slot `slot`. The operands of group g+1
+  // are read from LDS while group g's 16 MFMAs run. Two hooks let the stage
+  // loops fold their per-stage work under it: `pre` runs after the first
+  // group's operand reads are issued (the preempt-flag check: its LDS read
+  // overlaps theirs); if it returns false the stage is abandoned before any
+  // accumulator changes and compute returns false. `mid` runs once the first
+  // group's MFMAs are issued (the next stage's direct-to-LDS loads, issued
+  // while the matrix cores are busy).
+  template <class Pre, class Mid>
+  static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
+                                                 Pre&& pre, Mid&& mid) {
+    const char* abase = ring + slot * STAGE;
+    constexpr int G = KS / 8;
+    Frag f[2];
+    auto group = [&](int g) {
+      if (g + 1 < G) load_frag(abase, g + 1, f[(g + 1) & 1]);
+      const Frag& c = f[g & 1];
 #pragma unroll
       for (int s = 0; s < 4; ++s)
 #pragma unroll
@@ -121,8 +141,21 @@ struct EngMfma128 {
 #pragma unroll
           for (int cb = 0; cb < 2; ++cb)
             acc.c[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                a4[rb][s], bv[cb][s], acc.c[rb][cb], 0, 0, 0);
-    }
+                c.a4[rb][s], c.bv[cb][s], acc.c[rb][cb], 0, 0, 0);
+    };
+    // Group 0 is peeled so that the hooks sit outside the unrolled loop.
+    load_frag(abase, 0, f[0]);
+    if (!pre()) return false;
+    group(0);
+    __builtin_amdgcn_sched_barrier(0);
+    mid();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int g = 1; g < G; ++g) group(g);
+    return true;
+  }
+  static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {
+    compute(ring, slot, acc, [] { return true; }, [] {});
   }
 
   // Output element (tile-relative row, col) of accumulator register e.

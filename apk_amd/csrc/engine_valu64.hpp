@@ -82,12 +82,16 @@ struct EngValu64 {
     }
   }
 
-  static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {
+  // One k-stage out of ring slot `slot`. `pre` runs first (flag check;
+  // returning false abandons the stage before any accumulator changes),
+  // `mid` after the first k step (the next stage's direct-to-LDS loads).
+  template <class Pre, class Mid>
+  static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
+                                                 Pre&& pre, Mid&& mid) {
     const char* abase = ring + slot * STAGE;
     const float* bs = (const float*)(abase + A_STAGE);
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-#pragma unroll
-    for (int kk = 0; kk < KS; ++kk) {
+    auto step = [&](int kk) {
       float a[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -101,7 +105,17 @@ struct EngValu64 {
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc.v[i][j] = fmaf(a[i], bb[j], acc.v[i][j]);
-    }
+    };
+    // k step 0 is peeled so that the hooks sit outside the unrolled loop.
+    if (!pre()) return false;
+    step(0);
+    mid();
+#pragma unroll
+    for (int kk = 1; kk < KS; ++kk) step(kk);
+    return true;
+  }
+  static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {
+    compute(ring, slot, acc, [] { return true; }, [] {});
   }
 
   // Output element (tile-relative row, col) of accumulator register e.

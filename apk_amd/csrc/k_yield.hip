@@ -5,13 +5,14 @@
 // direct-to-LDS pipeline:
 //  * workers pop output tiles from an HBM fetch-add queue (tasks cycle the
 //    tile grid) and walk each tile's K in LDS k-stages;
-//  * the generation flag is sampled by a direct-to-LDS load issued just
-//    before each stage's data loads; it lands with that stage, so reading it
-//    costs one LDS read and never a stall (the value is two stages old);
+//  * the generation flag is sampled by a direct-to-LDS load issued right
+//    behind the data loads of a poll site's stage; the site's ordinary
+//    "stage landed" wait retires it, so reading it costs one LDS read and
+//    never a stall (the sample is one stage old);
 //  * at poll sites (every poll_every chunks, or every stage) a new generation
 //    is logged by every block; blocks that pop an urgent tile from the
-//    event's mini-queue yield: drain, checkpoint (accumulators and live LDS
-//    stages to HBM), run urgent tiles through the same ring, restore,
+//    event's mini-queue yield: drain, checkpoint (accumulators and the two
+//    resident LDS stages to HBM), run urgent tiles through the same ring, restore,
 //    continue -- the tile's k order is untouched, so C is bit-identical to an
 //    unpreempted run;
 //  * block 0 optionally acts as the device setter of a pre-scheduled event
@@ -29,12 +30,11 @@ namespace apk {
 template <class E, int POLL, bool ORACLE, bool SYS>
 __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield_params P) {
   __shared__ __attribute__((aligned(16))) char ring[E::LDS_BYTES];
-  __shared__ int flagring[E::NS][E::THREADS / 64];  // sample preceding stage s: [s % NS][wave]
+  __shared__ int flagring[E::NS];  // flag sample issued with stage t: [t % NS]
   __shared__ unsigned s_u32;
   __shared__ uint64_t s_red[E::THREADS / 64];
 
   const int tid = threadIdx.x, bid = blockIdx.x, G = gridDim.x;
-  const int wave = tid >> 6;
   const int tilesN = P.N / E::TN;
   const int totalTiles = (P.M / E::TM) * tilesN;
   const int S = P.K / E::KS;
@@ -49,11 +49,10 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   const int copies = P.flag_copies > 0 ? P.flag_copies : 1;
   const i32x4 flag_rsrc =
       make_rsrc((const char*)P.flag + (size_t)(bid % copies) * APK_FLAG_STRIDE, 4);
-  const i32x4 dummy_rsrc = make_rsrc(P.A, 4);
   float* ckslot = P.ckpt ? P.ckpt + (size_t)bid * Ckpt<E>::SLOT_FLOATS : nullptr;
   const bool isSetter = P.flag_set != nullptr && P.sched != nullptr && bid == 0;
 
-  if (tid < E::NS * (E::THREADS / 64)) (&flagring[0][0])[tid] = 0;
+  if (tid < E::NS) flagring[tid] = 0;
   __syncthreads();
 
   int lastSeen = 0;     // uniform: every thread derives it from the same samples
@@ -62,18 +61,19 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   int64_t gBase = 0;
   uint64_t stYields = 0, stSave = 0, stUrgent = 0, stRestore = 0;
 
-  // Stages that are poll sites carry a flag sample issued just in front of
-  // their data loads (all waves, same op count).
-  auto sampled = [&](int s) { return POLL != APK_POLL_OFF && s % pollStride == 0; };
-  auto issue_stage = [&](const typename E::Ctx& c, int row0, int col0, int s) {
-    if (sampled(s)) sample_flag<SYS>(flag_rsrc, dummy_rsrc, &flagring[s % E::NS][wave]);
-    E::issue(ring, c, s % E::NS, row0, col0, s);
-  };
-  // Operations issued after stage s's loads by the `ahead` later stages.
-  auto ops_after = [&](int s, int ahead) {
-    int n = 0;
-    for (int j = 1; j <= ahead; ++j) n += E::LOADS + (sampled(s + j) ? 1 : 0);
-    return n;
+  // Poll sites are the stages s with s % pollStride == 0, tracked with a
+  // countdown (`toPoll` stages until the next site) rather than divisions.
+  // The sample a site s reads is issued in front of the data loads of stage
+  // s+1, i.e. right behind stage s's own loads, so the ordinary "stage s
+  // landed" wait retires it too. For a site at the tile's last stage the
+  // sample is issued alone, in place of stage S.
+  auto issue_stage = [&](const typename E::Ctx& c, int row0, int col0, int t, int tslot,
+                         bool carry, int& lastSlot) {
+    if (POLL != APK_POLL_OFF && carry) {
+      sample_flag<SYS>(flag_rsrc, &flagring[tslot]);
+      lastSlot = tslot;
+    }
+    if (t < S) E::issue(ring, c, tslot, row0, col0, t);
   };
   auto set_flag = [&](int v) {
     for (int c = 0; c < copies; ++c)
@@ -95,24 +95,29 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     return (int)bcast(v);
   };
 
-  // One urgent tile through the ring (non-preemptible).
-  auto urgent_tile = [&](int uidx, int ev) {
+  // One urgent tile through the ring (non-preemptible). `ua` is the
+  // background accumulator, already checkpointed (or to be restarted), so
+  // the urgent job needs no registers of its own.
+  auto urgent_tile = [&](typename E::Acc& ua, int uidx, int ev) {
     const int ur0 = (uidx / uTilesN) * E::TM, uc0 = (uidx % uTilesN) * E::TN;
-    typename E::Acc ua;
     E::zero(ua);
-    if (Su > 0) E::issue(ring, uctx, 0, ur0, uc0, 0);
+    E::issue(ring, uctx, 0, ur0, uc0, 0);
     if (Su > 1) E::issue(ring, uctx, 1, ur0, uc0, 1);
+    int slot = 0;
     for (int t = 0; t < Su; ++t) {
-      if (t + kPrefetch < Su) E::issue(ring, uctx, (t + kPrefetch) % E::NS, ur0, uc0, t + kPrefetch);
-      wait_stage<E, 0>(Su - 1 - t < kPrefetch ? Su - 1 - t : kPrefetch);
+      wait_landed<E>(t + 1 < Su);
       lds_sync();
       if (P.poison && t == 0) {
         if (tid == 0) *(float*)(ring + E::A_STAGE) += 1.0f;  // staged B[0][uc0]
         lds_sync();
       }
-      E::compute(ring, t % E::NS, ua);
-      lds_sync();
+      const int ahead = slot_after_next(slot);
+      E::compute(ring, slot, ua, [] { return true; }, [&] {
+        if (t + 2 < Su) E::issue(ring, uctx, ahead, ur0, uc0, t + 2);
+      });
+      slot = next_slot(slot);
     }
+    lds_sync();
     const uint64_t hp = store_tile<E>(ua, ring, P.Cu, P.Nu, ur0, uc0, P.u_hash != nullptr);
     if (P.u_hash) {
       const uint64_t h = block_sum_u64(hp, s_red);
@@ -140,18 +145,34 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     const int col0 = (tile % tilesN) * E::TN;
     typename E::Acc acc;
     E::zero(acc);
-    if (S > 0) issue_stage(ctx, row0, col0, 0);
-    if (S > 1) issue_stage(ctx, row0, col0, 1);
+    int lastSlot = -1;
+    issue_stage(ctx, row0, col0, 0, 0, false, lastSlot);
+    issue_stage(ctx, row0, col0, 1, 1, true, lastSlot);  // stage 0 is a poll site
 
-    int s = 0;
+    int s = 0, slot = 0, toPoll = 0;
     while (s < S) {
-      if (s + kPrefetch < S) issue_stage(ctx, row0, col0, s + kPrefetch);
-      wait_ops<E>(ops_after(s, S - 1 - s < kPrefetch ? S - 1 - s : kPrefetch));
+      wait_landed<E>(s + 1 < S);
       lds_sync();
 
-      if (sampled(s)) {
-        int f = uniform(flagring[s % E::NS][0]);  // sample taken just before stage s was issued
+      const int ahead = slot_after_next(slot);
+      const bool carry = (toPoll == 1) || (toPoll == 0 && pollStride == 1);  // s+1 is a site
+      const bool site = POLL != APK_POLL_OFF && toPoll == 0;
+      bool restart = false;
+
+      // The site's flag sample (issued in front of stage s+1's loads, so
+      // landed by the wait above) is read under stage s's first operand
+      // reads. Everything past "no new generation" is the rare path: event
+      // log, urgent pop, and the yield itself -- drain, checkpoint, urgent
+      // tiles through the ring, restore. Restored accumulators and ring are
+      // bit-identical to what was saved, so the stage then simply computes
+      // (the operands already read are the same bytes). Only RESTART
+      // abandons the stage.
+      auto at_site = [&]() -> bool {
+        if (!site) return true;
+        int f = uniform(flagring[next_slot(slot)]);
         fLatest = f;
+        if (f == lastSeen && !isSetter) return true;
+
         if (isSetter && tid == 0 && f >= 0) {
           const int64_t now = wall_ticks();
           if (gBase == 0) gBase = now;
@@ -167,80 +188,82 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
           }
         }
         if (f > P.num_events) f = P.num_events;  // never index past the event arrays
-        if (f > lastSeen) {
-          const int64_t g = wall_ticks();
-          if (tid == 0)
-            for (int e = lastSeen; e < f; ++e) P.obs_gt[(size_t)e * G + bid] = g;
-          const int ev = f - 1;
-          lastSeen = f;
-          int uidx = U > 0 ? pop_urgent(ev) : U;
-          if (uidx < U) {
-            // ---- yield: this block hands its CU to the urgent job ----
-            wait_vmcnt<0>();
-            lds_sync();  // every wave's in-flight stage loads have landed
-            const int64_t t0 = wall_ticks();
-            const int live = (S - s) < E::NS ? (S - s) : E::NS;  // stages s.. not yet computed
-            if (P.resume != APK_RESUME_RESTART) {
-              Ckpt<E>::save_acc(acc, ckslot);
-              if (P.resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, ckslot, s % E::NS, live);
-            }
-            lds_sync();  // ring reads done before the urgent tile overwrites it
-            const int64_t t1 = wall_ticks();
-            if (uidx == 0 && tid == 0) {
-              P.claim[ev] = bid + 1;
-              P.claim_site[ev] = s;
-              P.u_gt[2 * (size_t)ev] = t1;
-            }
-            while (uidx < U) {
-              urgent_tile(uidx, ev);
-              uidx = pop_urgent(ev);
-            }
-            const int64_t t2 = wall_ticks();
-            if (tid == 0) {
-              atomic_max_u64(&P.u_end_max[ev], (unsigned long long)t2);
-              P.u_gt[2 * (size_t)ev + 1] = t2;
-            }
-            if (P.resume == APK_RESUME_RESTART) {
-              E::zero(acc);
-              s = 0;
-              issue_stage(ctx, row0, col0, 0);
-              if (S > 1) issue_stage(ctx, row0, col0, 1);
-              if (tid == 0) {
-                ++stYields;
-                stSave += (uint64_t)(t1 - t0);
-                stUrgent += (uint64_t)(t2 - t1);
-              }
-              lds_sync();  // reconverge before the back-edge (see the task loop)
-              continue;
-            }
-            Ckpt<E>::load_acc(acc, ckslot);
-            if (P.resume == APK_RESUME_CKPT_FULL) {
-              Ckpt<E>::load_ring(ring, ckslot, s % E::NS, live);
-            } else {
-              for (int k = 0; k < live; ++k) E::issue(ring, ctx, (s + k) % E::NS, row0, col0, s + k);
-              wait_vmcnt<0>();
-            }
-            __syncthreads();  // restored ring visible to all waves
-            const int64_t t3 = wall_ticks();
-            if (tid == 0) {
-              ++stYields;
-              stSave += (uint64_t)(t1 - t0);
-              stUrgent += (uint64_t)(t2 - t1);
-              stRestore += (uint64_t)(t3 - t2);
-            }
-          }
-        }
-      }
+        if (f <= lastSeen) return true;
+        const int64_t g = wall_ticks();
+        if (tid == 0)
+          for (int e = lastSeen; e < f; ++e) P.obs_gt[(size_t)e * G + bid] = g;
+        const int ev = f - 1;
+        lastSeen = f;
+        int uidx = U > 0 ? pop_urgent(ev) : U;
+        if (uidx >= U) return true;
 
-      E::compute(ring, s % E::NS, acc);
-      lds_sync();
+        // ---- yield: this block hands its CU to the urgent job ----
+        wait_vmcnt<0>();
+        lds_sync();  // stage s+1's loads have landed in every wave
+        const int64_t t0 = wall_ticks();
+        const int live = (S - s) < 2 ? (S - s) : 2;  // stages s, s+1: resident, not computed
+        if (P.resume != APK_RESUME_RESTART) {
+          Ckpt<E>::save_acc(acc, ckslot);
+          if (P.resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, ckslot, slot, live);
+        }
+        lds_sync();  // ring reads done before the urgent tile overwrites it
+        const int64_t t1 = wall_ticks();
+        if (uidx == 0 && tid == 0) {
+          P.claim[ev] = bid + 1;
+          P.claim_site[ev] = s;
+          P.u_gt[2 * (size_t)ev] = t1;
+        }
+        while (uidx < U) {
+          urgent_tile(acc, uidx, ev);
+          uidx = pop_urgent(ev);
+        }
+        const int64_t t2 = wall_ticks();
+        if (tid == 0) {
+          atomic_max_u64(&P.u_end_max[ev], (unsigned long long)t2);
+          P.u_gt[2 * (size_t)ev + 1] = t2;
+          ++stYields;
+          stSave += (uint64_t)(t1 - t0);
+          stUrgent += (uint64_t)(t2 - t1);
+        }
+        if (P.resume == APK_RESUME_RESTART) {
+          restart = true;
+          return false;
+        }
+        Ckpt<E>::load_acc(acc, ckslot);
+        if (P.resume == APK_RESUME_CKPT_FULL) {
+          Ckpt<E>::load_ring(ring, ckslot, slot, live);
+        } else {
+          E::issue(ring, ctx, slot, row0, col0, s);
+          if (live > 1) E::issue(ring, ctx, next_slot(slot), row0, col0, s + 1);
+          wait_vmcnt<0>();
+        }
+        __syncthreads();  // restored ring visible to all waves
+        if (tid == 0) stRestore += (uint64_t)(wall_ticks() - t2);
+        return true;
+      };
+      // Stage s+2 (and the sample for a site at s+1) goes out under stage
+      // s's matrix work; its slot held stage s-1, which every wave finished
+      // before the barrier above.
+      E::compute(ring, slot, acc, at_site, [&] {
+        if (s + 2 <= S) issue_stage(ctx, row0, col0, s + 2, ahead, carry, lastSlot);
+      });
+      if (restart) {  // RESTART: the tile starts over from stage 0
+        E::zero(acc);
+        s = 0;
+        slot = 0;
+        toPoll = 0;
+        lastSlot = -1;
+        issue_stage(ctx, row0, col0, 0, 0, false, lastSlot);
+        issue_stage(ctx, row0, col0, 1, 1, true, lastSlot);
+        lds_sync();  // reconverge before the back-edge (see the task loop)
+        continue;
+      }
+      toPoll = (toPoll == 0 ? pollStride : toPoll) - 1;
+      slot = next_slot(slot);
       ++s;
     }
-    if (POLL != APK_POLL_OFF) {  // freshest landed sample of this tile
-      int last = S - 1;
-      while (last > 0 && !sampled(last)) --last;
-      if (S > 0) fLatest = uniform(flagring[last % E::NS][0]);
-    }
+    lds_sync();  // every wave done with the ring; every sample has landed
+    if (POLL != APK_POLL_OFF && lastSlot >= 0) fLatest = uniform(flagring[lastSlot]);
 
     const uint64_t hp = store_tile<E>(acc, ring, P.C, P.N, row0, col0, P.task_hash != nullptr);
     if (P.task_hash) {

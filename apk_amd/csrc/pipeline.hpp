@@ -7,84 +7,70 @@
 
 namespace apk {
 
-// Prefetch depth of every ring here: NS = 3 slots, P = 2 stages in flight.
-constexpr int kPrefetch = 2;
-
-// Wait until k-stage s has landed when `ahead` (0..2) later stages were
-// issued behind it, each stage being E::LOADS + EXTRA vector-memory
-// operations per wave (EXTRA = 1 when a flag sample rides with the stage).
-// vmcnt retires in issue order, so <= ahead*(LOADS+EXTRA) outstanding
-// operations means stage s is in LDS. More operations issued later (stores,
-// atomics) only make the wait stricter, never wrong.
-template <class E, int EXTRA>
-__device__ __forceinline__ void wait_stage(int ahead) {
-  static_assert(E::NS == kPrefetch + 1, "ring of 3");
-  if (ahead >= 2) wait_vmcnt<2 * (E::LOADS + EXTRA)>();
-  else if (ahead == 1) wait_vmcnt<E::LOADS + EXTRA>();
-  else wait_vmcnt<0>();
-}
-
-// Wait until at most n vector-memory operations of this wave are
-// outstanding, for the n a ring can produce: 0, L, L+1, 2L, 2L+1, 2L+2 (L =
-// E::LOADS per stage, +1 per stage that carries a flag sample). Any other n
-// waits for everything, which is always safe.
+// ---------------------------------------------------------------------------
+// The ring protocol of every stage loop here (NS = 3 slots, one barrier per
+// k-stage):
+//   prologue  issue(0), issue(1)
+//   stage s   wait until stage s has landed (stage s+1 may stay in flight);
+//             lds_sync: stage s is visible to every wave, and every wave has
+//             finished computing stage s-1, so its slot, (s+2) % 3, is free;
+//             compute(s), with issue(s+2) folded in after its first reads.
+//   end       lds_sync before the ring is used for anything else.
+// When stage s is waited for, only the loads of stage s+1 (and nothing a
+// wave must read) have been issued after it, and vmcnt retires in issue
+// order, so "stage s landed" is vmcnt <= LOADS.
 template <class E>
-__device__ __forceinline__ void wait_ops(int n) {
-  constexpr int L = E::LOADS;
-  if (n == 2 * L + 2) wait_vmcnt<2 * L + 2>();
-  else if (n == 2 * L + 1) wait_vmcnt<2 * L + 1>();
-  else if (n == 2 * L) wait_vmcnt<2 * L>();
-  else if (n == L + 1) wait_vmcnt<L + 1>();
-  else if (n == L) wait_vmcnt<L>();
+__device__ __forceinline__ void wait_landed(bool next_in_flight) {
+  static_assert(E::NS == 3, "ring of 3");
+  if (next_in_flight) wait_vmcnt<E::LOADS>();
   else wait_vmcnt<0>();
 }
 
-// Non-preemptible K loop over stages [0, S) of one tile: prologue of two
-// stages, then issue s+2 / wait s / compute s. hook(s) runs uniformly at the
-// top of stage s.
+__device__ __forceinline__ int next_slot(int slot) { return slot == 2 ? 0 : slot + 1; }
+__device__ __forceinline__ int slot_after_next(int slot) { return slot == 0 ? 2 : slot - 1; }
+
+// Non-preemptible K loop over stages [0, S) of one tile. hook(s) runs
+// uniformly at the top of stage s.
 template <class E, class Hook>
 __device__ __forceinline__ void run_stages(char* ring, const typename E::Ctx& c,
                                            typename E::Acc& acc, int row0, int col0,
                                            int S, Hook&& hook) {
-  if (S > 0) E::issue(ring, c, 0, row0, col0, 0);
+  E::issue(ring, c, 0, row0, col0, 0);
   if (S > 1) E::issue(ring, c, 1, row0, col0, 1);
+  int slot = 0;
   for (int s = 0; s < S; ++s) {
     hook(s);
-    if (s + kPrefetch < S) E::issue(ring, c, (s + kPrefetch) % E::NS, row0, col0, s + kPrefetch);
-    wait_stage<E, 0>(S - 1 - s < kPrefetch ? S - 1 - s : kPrefetch);
+    wait_landed<E>(s + 1 < S);
     lds_sync();
-    E::compute(ring, s % E::NS, acc);
-    lds_sync();
+    const int ahead = slot_after_next(slot);
+    E::compute(ring, slot, acc, [] { return true; }, [&] {
+      if (s + 2 < S) E::issue(ring, c, ahead, row0, col0, s + 2);
+    });
+    slot = next_slot(slot);
   }
+  lds_sync();
 }
 
 // ---------------------------------------------------------------------------
-// Flag sampling. One dword is loaded from the flag straight into LDS by a
-// buffer load, so the sample rides the same in-order vmcnt stream as the
-// stage data and is read from LDS once a later stage wait has retired it: no
-// wave ever stalls on the flag's cross-XCD round trip. Only wave 0's lane 0
-// samples the real flag (agent scope: sc1, or system scope sc0 sc1 for a
-// host-mapped flag); lanes 0 of waves 1..3 load a cached dword so that every
-// wave has the same number of operations per stage.
+// Flag sampling. Lane 0 of wave 0 loads the flag dword straight into LDS
+// with a buffer load, so the sample rides the same in-order vmcnt stream as
+// the stage data and lands no later than the stage wait that follows it: no
+// wave ever stalls on the flag's cross-XCD round trip. Agent scope is sc1;
+// a host-mapped flag is read at system scope (sc0 sc1). The other waves read
+// the sample from LDS after the next barrier.
 template <bool SYSTEM>
-__device__ __forceinline__ void sample_flag(i32x4 flag_rsrc, i32x4 dummy_rsrc,
-                                            int* lds_dst_wave) {
+__device__ __forceinline__ void sample_flag(i32x4 flag_rsrc, int* lds_dst) {
   const uint32_t lds_addr = (uint32_t)(uintptr_t)(
-      (__attribute__((address_space(3))) const void*)lds_dst_wave);
+      (__attribute__((address_space(3))) const void*)lds_dst);
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr);
   const uint32_t zero = 0;
-  if (lane_id() == 0) {
-    if ((threadIdx.x >> 6) == 0) {
-      if (SYSTEM)
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen sc0 sc1 lds"
-                     : : "s"(m0), "v"(zero), "s"(flag_rsrc) : "memory");
-      else
-        asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen sc1 lds"
-                     : : "s"(m0), "v"(zero), "s"(flag_rsrc) : "memory");
-    } else {
-      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-                   : : "s"(m0), "v"(zero), "s"(dummy_rsrc) : "memory");
-    }
+  if (threadIdx.x == 0) {
+    if (SYSTEM)
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen sc0 sc1 lds"
+                   : : "s"(m0), "v"(zero), "s"(flag_rsrc) : "memory");
+    else
+      asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen sc1 lds"
+                   : : "s"(m0), "v"(zero), "s"(flag_rsrc) : "memory");
   }
 }
 
@@ -150,39 +136,53 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* red) {
 // Checkpoint slot layout (per slot, floats):
 //   [0, ACC_PER_THREAD*THREADS)        accumulators: float4 j of thread t at
 //                                      (j*THREADS + t)*4 -> coalesced 16 B/lane
-//   [ACC.., ACC.. + NS*STAGE/4)        the LDS ring, byte for byte
+//   [ACC.., ACC.. + 2*STAGE/4)         the resident stages s, s+1 of the
+//                                      ring (positions 0, 1), byte for byte
 template <class E>
 struct Ckpt {
   static constexpr int ACC_FLOATS = E::ACC_PER_THREAD * E::THREADS;
-  static constexpr int RING_FLOATS = E::LDS_BYTES / 4;
+  static constexpr int RING_FLOATS = 2 * E::STAGE / 4;
   static constexpr int SLOT_FLOATS = ACC_FLOATS + RING_FLOATS;
 
+  // Buffer stores/loads: one lane offset register, the float4 index in the
+  // scalar offset, so the checkpoint adds no live address registers.
   static __device__ __forceinline__ void save_acc(const typename E::Acc& a, float* slot) {
+    const buf_rsrc r = make_buf_rsrc(slot, ACC_FLOATS * 4);
+    const int vo = (int)threadIdx.x * 16;
 #pragma unroll
     for (int j = 0; j < E::ACC_PER_THREAD / 4; ++j) {
-      float4 v = {E::get(a, 4 * j), E::get(a, 4 * j + 1), E::get(a, 4 * j + 2),
-                  E::get(a, 4 * j + 3)};
-      *(float4*)(slot + ((size_t)j * E::THREADS + threadIdx.x) * 4) = v;
+      const float4 v = {E::get(a, 4 * j), E::get(a, 4 * j + 1), E::get(a, 4 * j + 2),
+                        E::get(a, 4 * j + 3)};
+      buf_store_f4(v, r, vo, j * E::THREADS * 16);
     }
   }
   static __device__ __forceinline__ void load_acc(typename E::Acc& a, const float* slot) {
+    const buf_rsrc r = make_buf_rsrc(slot, ACC_FLOATS * 4);
+    const int vo = (int)threadIdx.x * 16;
 #pragma unroll
     for (int j = 0; j < E::ACC_PER_THREAD / 4; ++j) {
-      const float4 v = *(const float4*)(slot + ((size_t)j * E::THREADS + threadIdx.x) * 4);
+      const float4 v = buf_load_f4(r, vo, j * E::THREADS * 16);
       E::set(a, 4 * j, v.x);
       E::set(a, 4 * j + 1, v.y);
       E::set(a, 4 * j + 2, v.z);
       E::set(a, 4 * j + 3, v.w);
     }
+    // Retire the loads here, on the rare restore path. Otherwise the
+    // compiler's wait insertion sees loads still pending into the
+    // accumulator registers where the restore path rejoins the stage loop and
+    // puts vmcnt waits at the head of the shared compute block -- which then
+    // drain the prefetched stages on every k-stage of every tile.
+    wait_vmcnt<0>();
   }
-  // Copy ring slots [first, first+n) (mod NS) to / from the checkpoint.
+  // Copy n (<= 2) ring slots first, first+1 (mod NS) to / from checkpoint
+  // positions 0, 1.
   static __device__ __forceinline__ void save_ring(const char* ring, float* slot,
                                                    int first, int n) {
     char* dst = (char*)(slot + ACC_FLOATS);
     for (int k = 0; k < n; ++k) {
       const int b = (first + k) % E::NS;
       for (int i = threadIdx.x * 16; i < E::STAGE; i += E::THREADS * 16)
-        *(float4*)(dst + b * E::STAGE + i) = *(const float4*)(ring + b * E::STAGE + i);
+        *(float4*)(dst + k * E::STAGE + i) = *(const float4*)(ring + b * E::STAGE + i);
     }
   }
   static __device__ __forceinline__ void load_ring(char* ring, const float* slot,
@@ -191,7 +191,7 @@ struct Ckpt {
     for (int k = 0; k < n; ++k) {
       const int b = (first + k) % E::NS;
       for (int i = threadIdx.x * 16; i < E::STAGE; i += E::THREADS * 16)
-        *(float4*)(ring + b * E::STAGE + i) = *(const float4*)(src + b * E::STAGE + i);
+        *(float4*)(ring + b * E::STAGE + i) = *(const float4*)(src + k * E::STAGE + i);
     }
   }
 };

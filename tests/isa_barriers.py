@@ -59,3 +59,38 @@ def _check(kernel, blocks):
             if any(any('s_barrier' in l for l in x['lines']) for x in body):
                 out.append((kernel, b['label'], 'BB' + h))
     return out
+
+
+def vm_waits_in_compute_blocks(asm_text, min_math=32):
+    """Return [(kernel, block, wait)] for compiler-visible vmcnt waits inside
+    basic blocks that carry the k-stage math (>= min_math MFMA/FMA ops).
+
+    The stage loops keep two stages of direct-to-LDS loads in flight and wait
+    for them explicitly before the barrier; a vmcnt wait inside the compute
+    block itself drains the prefetch on every stage.
+    """
+    out = []
+    kernel, label, lines = None, None, []
+
+    def flush():
+        math = sum(1 for l in lines if re.search(r'\bv_(mfma|fmac_f32|fma_f32)', l))
+        if math >= min_math:
+            for l in lines:
+                if re.search(r's_waitcnt\b.*vmcnt', l):
+                    out.append((kernel, label, l.strip()))
+
+    for l in asm_text.split('\n'):
+        mk = re.match(r'^(_Z\w+):', l)
+        mb = re.match(r'^(\.LBB\d+_\d+|; %bb\.\d+)', l)
+        if mk or mb:
+            flush()
+            lines = []
+            if mk:
+                kernel, label = mk.group(1), 'entry'
+            else:
+                label = mb.group(1)
+            continue
+        if l.startswith('\t') and not l.lstrip().startswith(';'):
+            lines.append(l)
+    flush()
+    return out

@@ -95,4 +95,6 @@ def test_yield_rejects_bad_args():
     p.Mu, p.Nu, p.Ku = 100, 128, 32
     rc = lib.apk_persistent_yield(apk_amd.ENGINE_MFMA128, apk_amd.POLL_STAGE, 0, ctypes.byref(p), 1, None)
     assert rc == apk_amd.APK_EINVAL and b"urgent" in lib.apk_last_error()
-    assert apk_amd.ckpt_floats(apk_amd.ENGINE_MFMA128) == 64 * 256 + 96 * 1024 // 4
+    # accumulators (64 floats x 256 threads) + the two resident 32 KiB stages
+    assert apk_amd.ckpt_floats(apk_amd.ENGINE_MFMA128) == 64 * 256 + 2 * 32 * 1024 // 4
+    assert apk_amd.ckpt_floats(apk_amd.ENGINE_VALU64) == 16 * 256 + 2 * 16 * 1024 // 4

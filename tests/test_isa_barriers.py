@@ -1,19 +1,24 @@
-"""Every gfx950 kernel of the library is free of barriers inside divergent
-loops (see tests/isa_barriers.py). Compiles each HIP source to assembly."""
+"""Static checks of the gfx950 assembly of every kernel of the library (see
+tests/isa_barriers.py): no barrier inside a divergent loop, and no vmcnt
+wait inside a k-stage compute block. Compiles each HIP source once."""
 import glob
 import os
 import subprocess
 
 import pytest
 
-from isa_barriers import divergent_barrier_loops
+from isa_barriers import divergent_barrier_loops, vm_waits_in_compute_blocks
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SOURCES = sorted(glob.glob(os.path.join(ROOT, "apk_amd", "csrc", "*.hip")))
 
 
-@pytest.mark.parametrize("src", SOURCES, ids=[os.path.basename(s) for s in SOURCES])
-def test_no_barrier_in_divergent_loop(src, tmp_path):
+_ASM = {}
+
+
+def _asm(src, tmp_path):
+    if src in _ASM:
+        return _ASM[src]
     out = tmp_path / "k.s"
     subprocess.check_call(
         ["/opt/rocm/bin/hipcc", "-std=c++17", "-O3", "--offload-arch=gfx950", "-fPIC",
@@ -21,8 +26,20 @@ def test_no_barrier_in_divergent_loop(src, tmp_path):
          "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "apk_amd", "csrc"),
          "-S", "--cuda-device-only", src, "-o", str(out)],
         stderr=subprocess.DEVNULL)
-    bad = divergent_barrier_loops(out.read_text())
+    _ASM[src] = out.read_text()
+    return _ASM[src]
+
+
+@pytest.mark.parametrize("src", SOURCES, ids=[os.path.basename(s) for s in SOURCES])
+def test_no_barrier_in_divergent_loop(src, tmp_path):
+    bad = divergent_barrier_loops(_asm(src, tmp_path))
     assert not bad, bad
+
+
+@pytest.mark.parametrize("src", SOURCES, ids=[os.path.basename(s) for s in SOURCES])
+def test_no_vm_wait_in_compute_block(src, tmp_path):
+    bad = vm_waits_in_compute_blocks(_asm(src, tmp_path))
+    assert not bad, bad[:8]
 
 
 def test_checker_catches_the_pattern():
@@ -39,3 +56,11 @@ def test_checker_catches_the_pattern():
     assert divergent_barrier_loops(asm) == [("_Z1kv", ".LBB0_1", "BB0_1")]
     clean = asm.replace("\ts_barrier\n", "")
     assert divergent_barrier_loops(clean) == []
+
+
+def test_vm_wait_checker_catches_the_pattern():
+    body = ["\tv_mfma_f32_32x32x2_f32 a[0:15], v1, v2, a[0:15]"] * 40
+    asm = "\n".join(["_Z1kv:", ".LBB0_1:", "\ts_waitcnt vmcnt(4)"] + body + ["\ts_endpgm"])
+    assert divergent_barrier_loops(asm) == []
+    assert vm_waits_in_compute_blocks(asm) == [("_Z1kv", ".LBB0_1", "s_waitcnt vmcnt(4)")]
+    assert vm_waits_in_compute_blocks(asm.replace("\ts_waitcnt vmcnt(4)\n", "")) == []
