@@ -100,15 +100,17 @@ int apk_persistent_gemm(int engine, const float* A, const float* B, float* C,
  * a tile (the tile-boundary yield points of src/yield.cu:125-136 once K is
  * walked in chunks); APK_POLL_STAGE polls at every LDS k-stage (the
  * mid-pipeline points of src/midyield.cu:246-290). The flag is sampled by a
- * direct-to-LDS load that retires with the stage data, so a poll never stalls
- * the pipeline; the value acted on is two stages old.
+ * direct-to-LDS load issued right behind a stage's data loads and retired by
+ * the same stage wait, so a poll never stalls the pipeline; the value acted
+ * on is one k-stage old.
  *
  * On a new generation every block logs its observation time; blocks that pop
  * an urgent tile from the event's mini-queue (src/yield.cu:155-183) yield:
  * they drain their in-flight stage loads, checkpoint per `resume`, run urgent
  * tiles through the same LDS ring until the mini-queue is empty, restore and
- * continue the interrupted tile.
- *   APK_RESUME_CKPT_FULL : accumulators + all live LDS stages -> HBM -> back
+ * continue the interrupted tile. At a site before stage s, stages s and s+1
+ * are resident in LDS and not yet computed (the "live" stages).
+ *   APK_RESUME_CKPT_FULL : accumulators + the live LDS stages -> HBM -> back
  *   APK_RESUME_CKPT_ACC  : accumulators -> HBM -> back; live stages re-fetched
  *   APK_RESUME_RESTART   : abandon the tile, restart it from k = 0 (the
  *                          reference's semantics, src/midyield.cu:237-258)
@@ -176,7 +178,8 @@ typedef struct apk_yield_params {
 int apk_persistent_yield(int engine, int poll, int oracle,
                          const apk_yield_params* params, int blocks, void* stream);
 
-/* Floats of checkpoint storage one block needs (accumulators + LDS ring). */
+/* Floats of checkpoint storage one block needs (accumulators + two LDS
+ * stages). */
 long long apk_yield_ckpt_floats(int engine);
 
 /* Resident blocks per CU of the preemptible kernel. */
