@@ -46,6 +46,7 @@ class EngineGeometry(ctypes.Structure):
 POLL_OFF, POLL_CHUNK, POLL_STAGE = 0, 1, 2
 RESUME_CKPT_FULL, RESUME_CKPT_ACC, RESUME_RESTART = 0, 1, 2
 FLAG_STRIDE, FLAG_MAX_COPIES = 4096, 256
+STATS_PER_BLOCK = 8
 
 
 class YieldParams(ctypes.Structure):
@@ -67,6 +68,8 @@ class YieldParams(ctypes.Structure):
         ("resume", ctypes.c_int), ("ckpt", ctypes.c_void_p), ("poison", ctypes.c_int),
         ("task_hash", ctypes.c_void_p), ("u_hash", ctypes.c_void_p), ("stats", ctypes.c_void_p),
         ("exec_count", ctypes.c_void_p), ("u_exec_count", ctypes.c_void_p),
+        ("cu_event_stride", ctypes.c_longlong), ("naive", ctypes.c_int),
+        ("run_gt", ctypes.c_void_p), ("exit_count", ctypes.c_void_p),
     ]
 
 

@@ -53,13 +53,14 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   const bool isSetter = P.flag_set != nullptr && P.sched != nullptr && bid == 0;
 
   if (tid < E::NS) flagring[tid] = 0;
+  if (P.run_gt && bid == 0 && tid == 0) P.run_gt[0] = wall_ticks();
   __syncthreads();
 
   int lastSeen = 0;     // uniform: every thread derives it from the same samples
   int fLatest = 0;      // freshest landed sample, for the task-boundary stop check
   int nextEv = 0;       // setter state (thread 0 of block 0)
   int64_t gBase = 0;
-  uint64_t stYields = 0, stSave = 0, stUrgent = 0, stRestore = 0;
+  uint64_t stYields = 0, stSave = 0, stUrgent = 0, stRestore = 0, stInflight = 0;
 
   // Poll sites are the stages s with s % pollStride == 0, tracked with a
   // countdown (`toPoll` stages until the next site) rather than divisions.
@@ -118,7 +119,8 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
       slot = next_slot(slot);
     }
     lds_sync();
-    const uint64_t hp = store_tile<E>(ua, ring, P.Cu, P.Nu, ur0, uc0, P.u_hash != nullptr);
+    float* cu = P.Cu + (size_t)ev * (size_t)P.cu_event_stride;
+    const uint64_t hp = store_tile<E>(ua, ring, cu, P.Nu, ur0, uc0, P.u_hash != nullptr);
     if (P.u_hash) {
       const uint64_t h = block_sum_u64(hp, s_red);
       if (tid == 0) P.u_hash[(size_t)ev * U + uidx] = h;
@@ -198,8 +200,8 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
         if (uidx >= U) return true;
 
         // ---- yield: this block hands its CU to the urgent job ----
-        wait_vmcnt<0>();
-        lds_sync();  // stage s+1's loads have landed in every wave
+        if (!P.naive) wait_vmcnt<0>();  // drain: stage s+1 has landed
+        lds_sync();
         const int64_t t0 = wall_ticks();
         const int live = (S - s) < 2 ? (S - s) : 2;  // stages s, s+1: resident, not computed
         if (P.resume != APK_RESUME_RESTART) {
@@ -222,6 +224,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
           atomic_max_u64(&P.u_end_max[ev], (unsigned long long)t2);
           P.u_gt[2 * (size_t)ev + 1] = t2;
           ++stYields;
+          stInflight += live > 1 ? 1 : 0;  // stage s+1 was issued, not waited for
           stSave += (uint64_t)(t1 - t0);
           stUrgent += (uint64_t)(t2 - t1);
         }
@@ -273,11 +276,16 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     if (ORACLE && tid == 0) fetch_add_i32(&P.exec_count[task], 1);
   }
 
+  if (P.run_gt && tid == 0 && fetch_add_u32(P.exit_count, 1u) == (unsigned)G - 1)
+    P.run_gt[1] = wall_ticks();
   if (P.stats && tid == 0) {
-    P.stats[(size_t)bid * 4 + 0] = stYields;
-    P.stats[(size_t)bid * 4 + 1] = stSave;
-    P.stats[(size_t)bid * 4 + 2] = stUrgent;
-    P.stats[(size_t)bid * 4 + 3] = stRestore;
+    unsigned long long* st = P.stats + (size_t)bid * APK_STATS_PER_BLOCK;
+    st[0] = stYields;
+    st[1] = stSave;
+    st[2] = stUrgent;
+    st[3] = stRestore;
+    st[4] = stInflight;
+    st[5] = st[6] = st[7] = 0;
   }
 }
 
@@ -318,6 +326,10 @@ static int validate(const apk_yield_params* p, int poll, int oracle, int blocks)
   if (oracle)
     APK_REQUIRE(p->exec_count && (p->u_exec_count || !p->Au),
                 "persistent_yield: oracle needs count arrays");
+  APK_REQUIRE(p->cu_event_stride >= 0 && (p->cu_event_stride == 0 ||
+                                          p->cu_event_stride >= (long long)p->Mu * p->Nu),
+              "persistent_yield: cu_event_stride=%lld", p->cu_event_stride);
+  APK_REQUIRE(!p->run_gt || p->exit_count, "persistent_yield: run_gt needs exit_count");
   return APK_OK;
 }
 

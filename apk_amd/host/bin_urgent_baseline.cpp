@@ -1,0 +1,284 @@
+// urgent_baseline -- how long an urgent GEMM waits behind a saturating
+// persistent GEMM when nothing yields (the no-preemption baseline).
+//
+// Measurement surface of the reference's bin/urgent_baseline
+// (src/urgent_baseline.cu:144-378): flags --k 64 --tiles-m 48 --tiles-n 48
+// --bg-tasks 20000 --trials 500 --mode sat|sat-1|1persm --blocks 0
+// --reserve -1 --urgent-blocks 1 --csv, the same stdout summary lines and
+// the CSV "trial,delay_us,consumed_at_arrival,remaining_at_arrival,e2e_us,
+// exec_us,gap_us,drain_us". Per trial the background persistent GEMM is
+// launched on one stream; after a delay (uniform in 0.2..0.8 of the measured
+// drain, mt19937(seed)) the urgent job is submitted on a second stream, and
+// the host times arrival -> completion (e2e). Device timeline: gap = urgent
+// start - background exit, exec = urgent duration, drain = background run.
+//
+// MI355X differences:
+//  * both streams have the default priority (stream priorities are not used
+//    on this pool); the urgent kernel is still only dispatched once CUs free
+//    up, which is exactly what this baseline measures;
+//  * the background is the preemptible kernel with polling off (tasks cycle
+//    the tile grid, src/urgent_baseline.cu:78-80), the urgent job is
+//    apk_persistent_gemm with --urgent-blocks workers over its own tiles.
+// Additions: --engine valu64|mfma128, --gemm-k K (background depth, walked
+// in --k chunks), --urgent-m/-n/-k (urgent GEMM shape; default
+// urgent-blocks tiles of depth --gemm-k, as the reference), --arrival
+// uniform|exp with --mean-gap-us (exponential delays, redrawn until they fall
+// inside the drain), --seed, --verify-rows.
+#include <omp.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <random>
+#include <string>
+#include <thread>
+#include <vector>
+
+#include "host_common.hpp"
+#include "yield_rig.hpp"
+
+using namespace host;
+
+int main(int argc, char** argv) {
+  const int kChunk = (int)parse_arg(argc, argv, "--k", 64);
+  const int tilesM = (int)parse_arg(argc, argv, "--tiles-m", 48);
+  const int tilesN = (int)parse_arg(argc, argv, "--tiles-n", 48);
+  const int bgTasks = (int)parse_arg(argc, argv, "--bg-tasks", 20000);
+  const int trials = (int)parse_arg(argc, argv, "--trials", 500);
+  const std::string mode = parse_str(argc, argv, "--mode", "sat");
+  int blocks = (int)parse_arg(argc, argv, "--blocks", 0);
+  const int reserve = (int)parse_arg(argc, argv, "--reserve", -1);
+  const int urgentBlocks = (int)parse_arg(argc, argv, "--urgent-blocks", 1);
+  const char* csvPath = parse_str(argc, argv, "--csv", "");
+  const std::string engName = parse_str(argc, argv, "--engine", "valu64");
+  const int gemmK = (int)parse_arg(argc, argv, "--gemm-k", kChunk);
+  const std::string arrival = parse_str(argc, argv, "--arrival", "uniform");
+  const double meanGapUs = parse_arg(argc, argv, "--mean-gap-us", 2000);
+  const unsigned seed = (unsigned)parse_arg(argc, argv, "--seed", 21);
+  const int verifyRows = (int)parse_arg(argc, argv, "--verify-rows", 0);
+
+  const int engine = engName == "mfma128" ? APK_ENGINE_MFMA128
+                     : engName == "valu64" ? APK_ENGINE_VALU64
+                                           : -1;
+  if (engine < 0) {
+    fprintf(stderr, "unknown --engine %s (valu64|mfma128)\n", engName.c_str());
+    return 1;
+  }
+  apk_engine_geometry geo;
+  APK_CHECK(apk_engine_geometry_of(engine, &geo));
+  if (kChunk <= 0 || kChunk % geo.k_stage != 0 || gemmK % kChunk != 0) {
+    fprintf(stderr, "--k must be a multiple of %d and divide --gemm-k\n", geo.k_stage);
+    return 1;
+  }
+  if (arrival != "uniform" && arrival != "exp") {
+    fprintf(stderr, "unknown --arrival %s (uniform|exp)\n", arrival.c_str());
+    return 1;
+  }
+  const int urgentM = (int)parse_arg(argc, argv, "--urgent-m", geo.tile_m);
+  const int urgentN = (int)parse_arg(argc, argv, "--urgent-n", urgentBlocks * geo.tile_n);
+  const int urgentK = (int)parse_arg(argc, argv, "--urgent-k", gemmK);
+  if (urgentM % geo.tile_m || urgentN % geo.tile_n || urgentK % geo.k_stage || urgentM <= 0 ||
+      urgentN <= 0 || urgentK <= 0) {
+    fprintf(stderr, "urgent job %dx%dx%d is not a whole number of %dx%dx%d tiles\n", urgentM,
+            urgentN, urgentK, geo.tile_m, geo.tile_n, geo.k_stage);
+    return 1;
+  }
+  const int uTiles = (urgentM / geo.tile_m) * (urgentN / geo.tile_n);
+
+  const Device dev = device_query();
+  int maxPerCU = 0;
+  APK_CHECK(apk_persistent_yield_occupancy(engine, APK_POLL_OFF, &maxPerCU));
+  const int sat = dev.info.cu_count * maxPerCU;
+  if (blocks <= 0) {
+    if (reserve >= 0) blocks = sat - reserve;
+    else if (mode == "sat") blocks = sat;
+    else if (mode == "sat-1") blocks = sat - 1;
+    else if (mode == "1persm") blocks = dev.info.cu_count;
+    else {
+      fprintf(stderr, "unknown --mode %s\n", mode.c_str());
+      return 1;
+    }
+  }
+  if (blocks <= 0 || blocks > sat) {
+    fprintf(stderr, "ERROR: %d blocks outside 1..%d residency slots\n", blocks, sat);
+    return 1;
+  }
+
+  const int M = tilesM * geo.tile_m, N = tilesN * geo.tile_n, K = gemmK;
+  printf("GPU: %s | %d CUs | %d resident blocks/CU max -> %d slots\n", dev.info.arch,
+         dev.info.cu_count, maxPerCU, sat);
+  printf("mode=%s: %d blocks | reserve=%d urgent-blocks=%d | K=%d (k-chunk %d) | "
+         "bg-tasks=%d | trials=%d | engine %s | urgent %dx%dx%d (%d tiles)\n",
+         mode.c_str(), blocks, reserve, urgentBlocks, K, kChunk, bgTasks, trials,
+         engName.c_str(), urgentM, urgentN, urgentK, uTiles);
+  printf("stream priorities: none (both streams at the default priority)\n");
+
+  std::vector<float> hA((size_t)M * K), hB((size_t)K * N);
+  fill_uniform_pm1(seed, hA, hB);
+  std::vector<float> hAu((size_t)urgentM * urgentK), hBu((size_t)urgentK * urgentN);
+  fill_uniform_pm1(seed + 1, hAu, hBu);
+
+  RigShape rs;
+  rs.engine = engine;
+  rs.M = M;
+  rs.N = N;
+  rs.K = K;
+  rs.kChunk = kChunk;
+  rs.blocks = blocks;
+  rs.events = 1;
+  rs.runTimes = true;
+  YieldRig rig(rs, hA, hB, {}, {});
+
+  float *dAu, *dBu, *dCu;
+  unsigned* dUNext;
+  apk_tile_record* dULog;
+  const int uChunks = 1;
+  HIP_CHECK(hipMalloc(&dAu, hAu.size() * 4));
+  HIP_CHECK(hipMalloc(&dBu, hBu.size() * 4));
+  HIP_CHECK(hipMalloc(&dCu, (size_t)urgentM * urgentN * 4));
+  HIP_CHECK(hipMalloc(&dUNext, sizeof(unsigned)));
+  HIP_CHECK(hipMalloc(&dULog, (size_t)uTiles * uChunks * sizeof(apk_tile_record)));
+  HIP_CHECK(hipMemcpy(dAu, hAu.data(), hAu.size() * 4, hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemcpy(dBu, hBu.data(), hBu.size() * 4, hipMemcpyHostToDevice));
+  unsigned* hConsumed;  // pinned, for the mid-flight queue snapshot
+  HIP_CHECK(hipHostMalloc((void**)&hConsumed, sizeof(unsigned), hipHostMallocDefault));
+
+  hipStream_t bgStream, uStream;
+  HIP_CHECK(hipStreamCreateWithFlags(&bgStream, hipStreamNonBlocking));
+  HIP_CHECK(hipStreamCreateWithFlags(&uStream, hipStreamNonBlocking));
+
+  auto launch_bg = [&]() {
+    rig.launch(APK_POLL_OFF, 1, APK_RESUME_RESTART, 0, (unsigned)bgTasks, false, 0, false,
+               bgStream);
+  };
+  auto launch_urgent = [&]() {
+    HIP_CHECK(hipMemsetAsync(dUNext, 0, sizeof(unsigned), uStream));
+    APK_CHECK(apk_persistent_gemm(engine, dAu, dBu, dCu, urgentM, urgentN, urgentK, urgentK,
+                                  dUNext, dULog, urgentBlocks, uStream));
+  };
+  // Urgent job timeline from its per-tile records: earliest start, latest end.
+  auto urgent_window = [&]() {
+    std::vector<apk_tile_record> rec((size_t)uTiles * uChunks);
+    HIP_CHECK(hipMemcpy(rec.data(), dULog, rec.size() * sizeof(apk_tile_record),
+                        hipMemcpyDeviceToHost));
+    long long s = rec[0].start, e = rec[0].end;
+    for (const auto& r : rec) {
+      s = std::min<long long>(s, r.start);
+      e = std::max<long long>(e, r.end);
+    }
+    return std::make_pair(s, e);
+  };
+  const double tickUs = 1.0 / dev.wall_mhz;
+
+  // --- Correctness gate (once, before any timing): both kernels vs float64.
+  {
+    printf("verifying bg + urgent kernels against float64 host reference...\n");
+    rig.reset(true);
+    HIP_CHECK(hipMemset(dCu, 0xFF, (size_t)urgentM * urgentN * 4));
+    HIP_CHECK(hipDeviceSynchronize());
+    launch_bg();
+    launch_urgent();
+    HIP_CHECK(hipDeviceSynchronize());
+    const std::vector<float> hC = rig.readC();
+    std::vector<float> hCu((size_t)urgentM * urgentN);
+    HIP_CHECK(hipMemcpy(hCu.data(), dCu, hCu.size() * 4, hipMemcpyDeviceToHost));
+    const int covered = std::min(bgTasks, tilesM * tilesN);
+    const int coveredRows = (covered / tilesN) * geo.tile_m;
+    const int rows = verifyRows > 0 ? std::min(verifyRows, coveredRows) : coveredRows;
+    const int threads = (int)std::max(1u, std::thread::hardware_concurrency());
+    std::vector<double> ref((size_t)rows * N);
+#pragma omp parallel for num_threads(threads) schedule(dynamic, 8)
+    for (int r = 0; r < rows; ++r) gemm_f64_rows(hA.data(), hB.data(), &ref[(size_t)r * N], N, K, r, 1);
+    std::vector<double> uref((size_t)urgentM * urgentN);
+    gemm_f64(hAu.data(), hBu.data(), uref.data(), urgentM, urgentN, urgentK, threads);
+    const double tol = K > 256 ? 1e-3 : 1e-4;  // elementwise gate; rel-Frobenius is the bar
+    const CheckResult cb = check(hC.data(), ref.data(), (int64_t)rows * N, tol, tol);
+    const CheckResult cu = check(hCu.data(), uref.data(), (int64_t)uref.size(), tol, tol);
+    if (cb.nans || cb.bad || cu.nans || cu.bad || cb.rel_frob > 1e-5 || cu.rel_frob > 1e-5) {
+      fprintf(stderr, "FAIL: bg %lld NaN %lld bad (rel-Frob %.2e); urgent %lld NaN %lld bad "
+              "(rel-Frob %.2e)\n", (long long)cb.nans, (long long)cb.bad, cb.rel_frob,
+              (long long)cu.nans, (long long)cu.bad, cu.rel_frob);
+      return 1;
+    }
+    printf("PASS: %d bg rows + %d urgent tiles, max rel err %.3e / %.3e, rel-Frobenius "
+           "%.2e / %.2e\n", rows, uTiles, cb.max_rel, cu.max_rel, cb.rel_frob, cu.rel_frob);
+  }
+
+  // --- Drain estimate (bg alone, device timeline), used to place arrivals.
+  rig.reset(false);
+  launch_bg();
+  HIP_CHECK(hipStreamSynchronize(bgStream));
+  auto [bs0, be0] = rig.readRunGT();
+  const double drainEstUs = (be0 - bs0) * tickUs;
+  printf("bg drain, no urgent: %.0f us for %d tasks on %d blocks\n", drainEstUs, bgTasks,
+         blocks);
+
+  // --- Trials.
+  std::mt19937 rng(seed);
+  std::uniform_real_distribution<double> frac(0.2, 0.8);
+  std::exponential_distribution<double> expo(1.0 / std::max(1.0, meanGapUs));
+  struct Row {
+    double delayUs, e2eUs, execUs, gapUs, drainUs;
+    unsigned consumed;
+  };
+  std::vector<Row> rows;
+  rows.reserve(trials);
+  for (int t = 0; t < trials; ++t) {
+    rig.reset(false);
+    double delayUs;
+    if (arrival == "uniform") {
+      delayUs = frac(rng) * drainEstUs;
+    } else {
+      do delayUs = expo(rng);
+      while (delayUs >= 0.95 * drainEstUs);
+    }
+    const int64_t t0 = now_ns();
+    launch_bg();
+    spin_until_ns(t0 + (int64_t)(delayUs * 1e3));
+    const int64_t tArrive = now_ns();
+    HIP_CHECK(hipMemcpyAsync(hConsumed, rig.dNextTask(), sizeof(unsigned),
+                             hipMemcpyDeviceToHost, uStream));
+    launch_urgent();
+    HIP_CHECK(hipStreamSynchronize(uStream));
+    const int64_t tDone = now_ns();
+    HIP_CHECK(hipStreamSynchronize(bgStream));
+    auto [bS, bE] = rig.readRunGT();
+    auto [uS, uE] = urgent_window();
+    rows.push_back({delayUs, (tDone - tArrive) / 1e3, (uE - uS) * tickUs, (uS - bE) * tickUs,
+                    (bE - bS) * tickUs, std::min(*hConsumed, (unsigned)bgTasks)});
+  }
+
+  std::vector<double> e2e, gap, exec, drain;
+  for (const Row& r : rows) {
+    e2e.push_back(r.e2eUs);
+    gap.push_back(r.gapUs);
+    exec.push_back(r.execUs);
+    drain.push_back(r.drainUs);
+  }
+  printf("\n--- %s: %d trials ---\n", mode.c_str(), trials);
+  printf("urgent e2e (us):  p50 %.1f | p90 %.1f | p99 %.1f | max %.1f\n",
+         percentile(e2e, 0.50), percentile(e2e, 0.90), percentile(e2e, 0.99),
+         *std::max_element(e2e.begin(), e2e.end()));
+  printf("gap uStart-bgEnd (us): p50 %.1f | p10 %.1f | p90 %.1f\n", percentile(gap, 0.50),
+         percentile(gap, 0.10), percentile(gap, 0.90));
+  printf("urgent exec (us): p50 %.2f | p99 %.2f\n", percentile(exec, 0.50),
+         percentile(exec, 0.99));
+  printf("bg drain (us):    p50 %.0f\n", percentile(drain, 0.50));
+
+  if (csvPath[0]) {
+    FILE* csv = fopen(csvPath, "w");
+    if (csv) {
+      fprintf(csv, "trial,delay_us,consumed_at_arrival,remaining_at_arrival,e2e_us,exec_us,"
+                   "gap_us,drain_us\n");
+      for (int t = 0; t < trials; ++t)
+        fprintf(csv, "%d,%.1f,%u,%d,%.1f,%.2f,%.1f,%.1f\n", t, rows[t].delayUs,
+                rows[t].consumed, bgTasks - (int)rows[t].consumed, rows[t].e2eUs,
+                rows[t].execUs, rows[t].gapUs, rows[t].drainUs);
+      fclose(csv);
+      printf("raw trial records: %s\n", csvPath);
+    } else {
+      fprintf(stderr, "warning: could not open %s\n", csvPath);
+    }
+  }
+  return 0;
+}

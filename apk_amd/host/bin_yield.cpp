@@ -364,7 +364,7 @@ int main(int argc, char** argv) {
     for (size_t t = 0; t < hNow.size(); ++t)
       if (hNow[t] != hRef[t]) ++hashBad;
     uint64_t yields = 0;
-    for (int b = 0; b < blocks; ++b) yields += r.stats[(size_t)b * 4];
+    for (int b = 0; b < blocks; ++b) yields += r.stats[(size_t)b * APK_STATS_PER_BLOCK];
     printf("yields taken: %llu | C bit-identical to the unpreempted run: %s | task "
            "fingerprints differing: %lld\n",
            (unsigned long long)yields, bitsSame ? "yes" : "NO", (long long)hashBad);
@@ -520,10 +520,10 @@ int main(int argc, char** argv) {
   if (csv) fclose(csv);
   uint64_t yields = 0, tSave = 0, tUrg = 0, tRest = 0;
   for (int b = 0; b < blocks; ++b) {
-    yields += r.stats[(size_t)b * 4];
-    tSave += r.stats[(size_t)b * 4 + 1];
-    tUrg += r.stats[(size_t)b * 4 + 2];
-    tRest += r.stats[(size_t)b * 4 + 3];
+    yields += r.stats[(size_t)b * APK_STATS_PER_BLOCK];
+    tSave += r.stats[(size_t)b * APK_STATS_PER_BLOCK + 1];
+    tUrg += r.stats[(size_t)b * APK_STATS_PER_BLOCK + 2];
+    tRest += r.stats[(size_t)b * APK_STATS_PER_BLOCK + 3];
   }
   printf("\n--- latency (%s-set, poll-every=%d, %d blocks): %zu events (%d warmup discarded, "
          "%d anomalies, %d unset) ---\n", setBy.c_str(), pollEvery, blocks, lat.size(),

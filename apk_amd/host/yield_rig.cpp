@@ -30,7 +30,7 @@ YieldRig::YieldRig(const RigShape& s, const std::vector<float>& A,
   if (U_ > 0) {
     dAu_ = dalloc<float>(Au.size());
     dBu_ = dalloc<float>(Bu.size());
-    dCu_ = dalloc<float>((size_t)s.Mu * s.Nu);
+    dCu_ = dalloc<float>((size_t)s.Mu * s.Nu * (s.cuPerEvent ? E : 1));
     HIP_CHECK(hipMemcpy(dAu_, Au.data(), Au.size() * 4, hipMemcpyHostToDevice));
     HIP_CHECK(hipMemcpy(dBu_, Bu.data(), Bu.size() * 4, hipMemcpyHostToDevice));
   }
@@ -54,10 +54,14 @@ YieldRig::YieldRig(const RigShape& s, const std::vector<float>& A,
   dCkpt_ = dalloc<float>((size_t)s.blocks * apk_yield_ckpt_floats(s.engine));
   if (s.hashTasks) dTaskHash_ = dalloc<unsigned long long>(s.hashTasks);
   if (U_ > 0) dUHash_ = dalloc<unsigned long long>((size_t)E * U_);
-  dStats_ = dalloc<unsigned long long>((size_t)s.blocks * 4);
+  dStats_ = dalloc<unsigned long long>((size_t)s.blocks * APK_STATS_PER_BLOCK);
   if (s.oracleTasks) {
     dExec_ = dalloc<int>(s.oracleTasks);
     dUExec_ = dalloc<int>(E);
+  }
+  if (s.runTimes) {
+    dRunGT_ = dalloc<long long>(2);
+    dExit_ = dalloc<unsigned>(1);
   }
 }
 
@@ -79,20 +83,40 @@ void YieldRig::reset(bool nanFill) {
   HIP_CHECK(hipMemset(dSite_, 0xFF, E * sizeof(int)));
   HIP_CHECK(hipMemset(dUq_, 0, E * sizeof(int)));
   HIP_CHECK(hipMemset(dUEnd_, 0, E * sizeof(unsigned long long)));
-  HIP_CHECK(hipMemset(dStats_, 0, (size_t)s_.blocks * 4 * sizeof(unsigned long long)));
+  HIP_CHECK(hipMemset(dStats_, 0, (size_t)s_.blocks * APK_STATS_PER_BLOCK * 8));
   if (dTaskHash_) HIP_CHECK(hipMemset(dTaskHash_, 0, (size_t)s_.hashTasks * 8));
   if (dUHash_) HIP_CHECK(hipMemset(dUHash_, 0, (size_t)E * U_ * 8));
   if (dExec_) {
     HIP_CHECK(hipMemset(dExec_, 0, (size_t)s_.oracleTasks * sizeof(int)));
     HIP_CHECK(hipMemset(dUExec_, 0, E * sizeof(int)));
   }
+  if (dRunGT_) {
+    HIP_CHECK(hipMemset(dRunGT_, 0, 2 * sizeof(long long)));
+    HIP_CHECK(hipMemset(dExit_, 0, sizeof(unsigned)));
+  }
   if (nanFill) {
     HIP_CHECK(hipMemset(dC_, 0xFF, (size_t)s_.M * s_.N * 4));
-    if (dCu_) HIP_CHECK(hipMemset(dCu_, 0xFF, (size_t)s_.Mu * s_.Nu * 4));
+    if (dCu_)
+      HIP_CHECK(hipMemset(dCu_, 0xFF, (size_t)s_.Mu * s_.Nu * 4 * (s_.cuPerEvent ? E : 1)));
   }
   // Null-stream fills do not order against non-blocking streams
   // (src/yield.cu:681-684): hard sync before any launch.
   HIP_CHECK(hipDeviceSynchronize());
+}
+
+void YieldRig::reserveTasks(unsigned hashTasks, unsigned oracleTasks) {
+  HIP_CHECK(hipDeviceSynchronize());
+  if (hashTasks > s_.hashTasks) {
+    if (dTaskHash_) HIP_CHECK(hipFree(dTaskHash_));
+    dTaskHash_ = dalloc<unsigned long long>(hashTasks);
+    s_.hashTasks = hashTasks;
+  }
+  if (oracleTasks > s_.oracleTasks) {
+    if (dExec_) HIP_CHECK(hipFree(dExec_));
+    dExec_ = dalloc<int>(oracleTasks);
+    if (!dUExec_) dUExec_ = dalloc<int>(s_.events > 0 ? s_.events : 1);
+    s_.oracleTasks = oracleTasks;
+  }
 }
 
 void YieldRig::setSchedule(const std::vector<long long>& cumNs, double wallMHz) {
@@ -105,7 +129,7 @@ void YieldRig::setSchedule(const std::vector<long long>& cumNs, double wallMHz) 
 
 void YieldRig::launch(int poll, int pollEvery, int resume, int poison, unsigned numTasks,
                       bool devSetter, int nEvents, bool oracle, hipStream_t stream,
-                      long long stopAfterTicks) {
+                      long long stopAfterTicks, int naive) {
   apk_yield_params p;
   memset(&p, 0, sizeof p);
   p.A = dA_;
@@ -146,6 +170,10 @@ void YieldRig::launch(int poll, int pollEvery, int resume, int poison, unsigned 
   p.task_hash = (dTaskHash_ && numTasks <= s_.hashTasks) ? dTaskHash_ : nullptr;
   p.u_hash = dUHash_;
   p.stats = dStats_;
+  p.cu_event_stride = s_.cuPerEvent ? (long long)s_.Mu * s_.Nu : 0;
+  p.naive = naive;
+  p.run_gt = dRunGT_;
+  p.exit_count = dExit_;
   if (oracle) {
     if (!dExec_ || numTasks > s_.oracleTasks) {
       fprintf(stderr, "oracle launch needs %u task counters (have %u)\n", numTasks,
@@ -184,13 +212,26 @@ EventResult YieldRig::readEvents(int nEvents) const {
   r.site = d2h(dSite_, E);
   r.uEnd = d2h(dUEnd_, E);
   if (dUHash_) r.uHash = d2h(dUHash_, E * U_);
-  r.stats = d2h(dStats_, (size_t)s_.blocks * 4);
+  r.stats = d2h(dStats_, (size_t)s_.blocks * APK_STATS_PER_BLOCK);
   return r;
 }
 
 std::vector<float> YieldRig::readC() const { return d2h(dC_, (size_t)s_.M * s_.N); }
 std::vector<float> YieldRig::readCu() const {
   return d2h(dCu_, dCu_ ? (size_t)s_.Mu * s_.Nu : 0);
+}
+std::vector<float> YieldRig::readCuEvent(int e) const {
+  const size_t n = (size_t)s_.Mu * s_.Nu;
+  std::vector<float> h(dCu_ ? n : 0);
+  if (dCu_)
+    HIP_CHECK(hipMemcpy(h.data(), dCu_ + (s_.cuPerEvent ? (size_t)e * n : 0), n * 4,
+                        hipMemcpyDeviceToHost));
+  return h;
+}
+std::pair<long long, long long> YieldRig::readRunGT() const {
+  long long t[2] = {0, 0};
+  if (dRunGT_) HIP_CHECK(hipMemcpy(t, dRunGT_, sizeof t, hipMemcpyDeviceToHost));
+  return {t[0], t[1]};
 }
 std::vector<unsigned long long> YieldRig::readTaskHash(unsigned n) const {
   return d2h(dTaskHash_, dTaskHash_ ? std::min(n, s_.hashTasks) : 0);

@@ -4,6 +4,7 @@
 // src/midyield.cu:410-469) gathered in one place.
 #pragma once
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "host_common.hpp"
@@ -20,6 +21,8 @@ struct RigShape {
   unsigned oracleTasks = 0;    // capacity of the exactly-once counts (0 = none)
   bool hostFlag = false;       // flag in host-mapped memory (host-set events)
   int flagCopies = 1;          // replicas of the flag, APK_FLAG_STRIDE apart
+  bool cuPerEvent = false;     // one urgent output per event (CuAll)
+  bool runTimes = false;       // record the run's start / last-exit ticks
 };
 
 struct EventResult {
@@ -27,7 +30,7 @@ struct EventResult {
   std::vector<int> claim, site;
   std::vector<unsigned long long> uEnd;
   std::vector<unsigned long long> uHash;
-  std::vector<unsigned long long> stats;      // blocks x 4
+  std::vector<unsigned long long> stats;      // blocks x APK_STATS_PER_BLOCK
 };
 
 class YieldRig {
@@ -43,6 +46,9 @@ class YieldRig {
   // Zero the queue, flag and event arrays (before any launch); fill C / Cu
   // with NaN when nanFill. Synchronizes the device.
   void reset(bool nanFill);
+  // (Re)allocate the per-task fingerprint and exactly-once arrays for up to
+  // n tasks each (0 = keep the current capacity).
+  void reserveTasks(unsigned hashTasks, unsigned oracleTasks);
   // Upload a cumulative schedule (ns) as device ticks.
   void setSchedule(const std::vector<long long>& cumNs, double wallMHz);
 
@@ -50,19 +56,22 @@ class YieldRig {
   // the device setter for `nEvents` events, oracle instantiation.
   void launch(int poll, int pollEvery, int resume, int poison, unsigned numTasks,
               bool devSetter, int nEvents, bool oracle, hipStream_t stream,
-              long long stopAfterTicks = 0);
+              long long stopAfterTicks = 0, int naive = 0);
 
   // Host-mapped flag (host-set mode): relaxed store visible to the GPU.
   void hostSetFlag(int v);
 
   EventResult readEvents(int nEvents) const;
   std::vector<float> readC() const;
-  std::vector<float> readCu() const;
+  std::vector<float> readCu() const;           // event 0's (or the shared) output
+  std::vector<float> readCuEvent(int e) const; // cuPerEvent
+  std::pair<long long, long long> readRunGT() const;  // runTimes: start, last exit
   std::vector<unsigned long long> readTaskHash(unsigned n) const;
   std::vector<int> readExec(unsigned n) const;
   std::vector<int> readUExec(int n) const;
 
   float* dC() const { return dC_; }
+  unsigned* dNextTask() const { return dNext_; }
   int* dFlag() const { return dFlag_; }
 
  private:
@@ -80,6 +89,8 @@ class YieldRig {
   float* dCkpt_ = nullptr;
   unsigned long long *dTaskHash_ = nullptr, *dUHash_ = nullptr, *dStats_ = nullptr;
   int *dExec_ = nullptr, *dUExec_ = nullptr;
+  long long* dRunGT_ = nullptr;
+  unsigned* dExit_ = nullptr;
 };
 
 // Per-event summary of an observation matrix (src/yield.cu:889-928).

@@ -121,6 +121,7 @@ enum { APK_POLL_OFF = 0, APK_POLL_CHUNK = 1, APK_POLL_STAGE = 2 };
  * CU: copy c lives at byte offset c * APK_FLAG_STRIDE. */
 #define APK_FLAG_STRIDE 4096
 #define APK_FLAG_MAX_COPIES 256
+#define APK_STATS_PER_BLOCK 8
 enum { APK_RESUME_CKPT_FULL = 0, APK_RESUME_CKPT_ACC = 1, APK_RESUME_RESTART = 2 };
 
 typedef struct apk_yield_params {
@@ -166,10 +167,25 @@ typedef struct apk_yield_params {
   /* verification and statistics (each may be NULL) */
   unsigned long long* task_hash; /* [num_tasks] fingerprint of each completed task */
   unsigned long long* u_hash;    /* [events * urgent tiles] */
-  unsigned long long* stats;     /* [blocks * 4]: yields, save, urgent, restore ticks */
+  unsigned long long* stats;     /* [blocks * APK_STATS_PER_BLOCK]: yields, save,
+                                    urgent, restore ticks, yields that drained a
+                                    stage still in flight, 3 reserved */
   /* exactly-once oracle (used by the oracle instantiation only) */
   int* exec_count;             /* [num_tasks] */
   int* u_exec_count;           /* [events] */
+  /* per-event urgent outputs: event e writes its tiles at Cu + e *
+   * cu_event_stride floats (0 = every event overwrites Cu); the reference's
+   * CuAll (src/midyield.cu:410-416) */
+  long long cu_event_stride;
+  /* 1 = skip the drain (vmcnt 0) before the checkpoint -- the reference's
+   * "naive" discipline (src/midyield.cu:180-200) as a control experiment:
+   * a live stage still in flight is checkpointed stale. 0 = drain. */
+  int naive;
+  /* run timeline (src/urgent_baseline.cu:66-88), may be NULL: run_gt[0] =
+   * block 0's start, run_gt[1] = exit of the last block; exit_count must be
+   * 0 at launch */
+  long long* run_gt;
+  unsigned int* exit_count;
 } apk_yield_params;
 
 /* persistent_yield / persistent_midyield (src/yield.cu:95-204,

@@ -1,6 +1,7 @@
 """C ABI surface on the CPU: the library loads, exports every function that
 include/apk.h declares, and rejects bad arguments before touching a GPU."""
 import ctypes
+import re
 import subprocess
 
 import pytest
@@ -98,3 +99,11 @@ def test_yield_rejects_bad_args():
     # accumulators (64 floats x 256 threads) + the two resident 32 KiB stages
     assert apk_amd.ckpt_floats(apk_amd.ENGINE_MFMA128) == 64 * 256 + 2 * 32 * 1024 // 4
     assert apk_amd.ckpt_floats(apk_amd.ENGINE_VALU64) == 16 * 256 + 2 * 16 * 1024 // 4
+
+
+def test_python_constants_match_header():
+    text = open(apk_amd.HEADER).read()
+    defines = dict(re.findall(r"#define (APK_\w+) (\d+)", text))
+    assert int(defines["APK_FLAG_STRIDE"]) == apk_amd.FLAG_STRIDE
+    assert int(defines["APK_FLAG_MAX_COPIES"]) == apk_amd.FLAG_MAX_COPIES
+    assert int(defines["APK_STATS_PER_BLOCK"]) == apk_amd.STATS_PER_BLOCK

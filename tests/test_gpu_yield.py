@@ -58,7 +58,7 @@ class Job:
         self.ckpt = T.zeros(blocks * apk.ckpt_floats(engine), dtype=T.float32, device="cuda")
         self.task_hash = T.zeros(self.num_tasks, dtype=i64, device="cuda")
         self.u_hash = T.zeros(E * max(self.U, 1), dtype=i64, device="cuda")
-        self.stats = T.zeros(blocks * 4, dtype=i64, device="cuda")
+        self.stats = T.zeros(blocks * apk.STATS_PER_BLOCK, dtype=i64, device="cuda")
         self.exec_count = T.zeros(self.num_tasks, dtype=i32, device="cuda")
         self.u_exec = T.zeros(E, dtype=i32, device="cuda")
 
@@ -104,7 +104,7 @@ class Job:
             "set_gt": self.set_gt.cpu().numpy()[:ev], "claim": self.claim.cpu().numpy()[:ev],
             "site": self.site.cpu().numpy()[:ev],
             "obs": self.obs.cpu().numpy()[:ev * self.blocks].reshape(max(ev, 0), self.blocks),
-            "stats": self.stats.cpu().numpy().reshape(self.blocks, 4),
+            "stats": self.stats.cpu().numpy().reshape(self.blocks, self.apk.STATS_PER_BLOCK),
             "exec": self.exec_count.cpu().numpy(), "u_exec": self.u_exec.cpu().numpy()[:ev],
         }
 
