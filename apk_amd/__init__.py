@@ -17,8 +17,8 @@ BIN_DIR = os.path.join(_HERE, "bin")
 HEADER = os.path.join(ROOT, "include", "apk.h")
 
 APK_OK, APK_EINVAL, APK_EHIP, APK_ERANGE = 0, 1, 2, 3
-ENGINE_VALU64, ENGINE_MFMA128 = 0, 1
-ENGINES = {"valu64": ENGINE_VALU64, "mfma128": ENGINE_MFMA128}
+ENGINE_VALU64, ENGINE_MFMA128, ENGINE_BF16X256 = 0, 1, 2
+ENGINES = {"valu64": ENGINE_VALU64, "mfma128": ENGINE_MFMA128, "bf16x256": ENGINE_BF16X256}
 
 
 class ApkError(RuntimeError):
@@ -40,7 +40,8 @@ class DeviceInfo(ctypes.Structure):
 class EngineGeometry(ctypes.Structure):
     _fields_ = [("tile_m", ctypes.c_int), ("tile_n", ctypes.c_int),
                 ("k_stage", ctypes.c_int), ("threads", ctypes.c_int),
-                ("lds_bytes", ctypes.c_int)]
+                ("lds_bytes", ctypes.c_int), ("elem_bytes", ctypes.c_int),
+                ("b_transposed", ctypes.c_int)]
 
 
 POLL_OFF, POLL_CHUNK, POLL_STAGE = 0, 1, 2

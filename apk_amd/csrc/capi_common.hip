@@ -2,6 +2,7 @@
 #include <stdarg.h>
 #include <string.h>
 #include "capi.hpp"
+#include "engine_bf16x256.hpp"
 #include "engine_mfma128.hpp"
 #include "engine_valu64.hpp"
 
@@ -41,11 +42,15 @@ extern "C" int apk_engine_geometry_of(int engine, apk_engine_geometry* out) {
   switch (engine) {
     case APK_ENGINE_VALU64:
       *out = {apk::EngValu64::TM, apk::EngValu64::TN, apk::EngValu64::KS,
-              apk::EngValu64::THREADS, apk::EngValu64::LDS_BYTES};
+              apk::EngValu64::THREADS, apk::EngValu64::LDS_BYTES, 4, 0};
       return APK_OK;
     case APK_ENGINE_MFMA128:
       *out = {apk::EngMfma128::TM, apk::EngMfma128::TN, apk::EngMfma128::KS,
-              apk::EngMfma128::THREADS, apk::EngMfma128::LDS_BYTES};
+              apk::EngMfma128::THREADS, apk::EngMfma128::LDS_BYTES, 4, 0};
+      return APK_OK;
+    case APK_ENGINE_BF16X256:
+      *out = {apk::EngBf16x256::TM, apk::EngBf16x256::TN, apk::EngBf16x256::KS,
+              apk::EngBf16x256::THREADS, apk::EngBf16x256::LDS_BYTES, 2, 1};
       return APK_OK;
     default:
       apk::set_error("unknown engine %d", engine);

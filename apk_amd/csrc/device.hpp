@@ -101,6 +101,16 @@ __device__ __forceinline__ float4 buf_load_f4(buf_rsrc r, int voff, int soff) {
                      __uint_as_float(u.w));
 }
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// splitmix64 finaliser: the mixing step of the tile fingerprints.
+__device__ __forceinline__ uint64_t mix64(uint64_t z) {
+  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
+  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
+  return z ^ (z >> 31);
+}
+
 // One 16-byte-per-lane buffer load written straight into LDS: lane l's 16
 // bytes land at lds_base + 16*l (lds_base is wave-uniform, passed in M0).
 //

@@ -1,0 +1,206 @@
+// engine_bf16x256.hpp -- 256x256 output tile of a bf16 GEMM with fp32
+// accumulation on the gfx950 matrix cores (v_mfma_f32_32x32x16_bf16), fed by
+// a 3-stage LDS ring of buffer_load_dwordx4 ... lds (direct-to-LDS).
+//
+// Operands: A is M x K row-major bf16; B is passed transposed, Bt = N x K
+// row-major bf16 (C = A . Bt^T), so that both operands are k-contiguous in
+// memory, in LDS and in the MFMA operand registers (8 consecutive k per lane
+// = one 16-byte LDS read). C is M x N row-major fp32.
+//
+// Block: 256 threads = 4 wave64s in a 2x2 arrangement; each wave owns a
+// 128x128 sub-tile held as 4x4 32x32 accumulators (256 fp32 per lane, in the
+// accumulation registers).
+// Stage: k depth KS=32 -> A stage 256 rows x 64 B (16 KiB) + Bt stage 256
+// rows x 64 B (16 KiB); 3 stages = 96 KiB of the 160 KiB LDS (1 block/CU).
+//
+// LDS layout (both operands): row r of a stage is 64 B = four 16-byte
+// chunks; chunk q is stored at slot q ^ ((r >> 1) & 3). A 32-row operand read
+// (lanes 0-31 chunk 2j, lanes 32-63 chunk 2j+1) then touches every 16-byte
+// bank group once per eight consecutive rows.
+//
+// k order: a k-stage is two MFMA k-steps of 16, in ascending k; every
+// output's sum is formed in the same order whatever worker computes it and
+// however often it is checkpointed and resumed.
+//
+// Epilogue: the fp32 tile (256 KiB) does not fit LDS; every lane stores its
+// accumulators straight to C (each store instruction writes two 128-byte row
+// segments) and folds them into the tile fingerprint.
+#pragma once
+#include "device.hpp"
+
+namespace apk {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+struct EngBf16x256 {
+  static constexpr int TM = 256, TN = 256, KS = 32, NS = 3, THREADS = 256;
+  static constexpr int ROW_BYTES = KS * 2;                  // 64 B
+  static constexpr int A_STAGE = TM * ROW_BYTES;            // 16 KiB
+  static constexpr int B_STAGE = TN * ROW_BYTES;            // 16 KiB
+  static constexpr int STAGE = A_STAGE + B_STAGE;           // 32 KiB
+  static constexpr int LDS_BYTES = NS * STAGE;              // 96 KiB
+  static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 4 per thread
+  static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 4 per thread
+  static constexpr int LOADS = LOADS_A + LOADS_B;
+  static constexpr int ACC_PER_THREAD = 256;                // floats
+  static constexpr int ELEM_BYTES = 2;                      // bf16 operands
+  static constexpr bool DIRECT_STORE = true;
+
+  struct Acc {
+    f32x16 c[4][4];
+  };
+
+  struct Ctx {
+    i32x4 ra, rb;
+    int K;
+  };
+
+  static __device__ __forceinline__ Ctx make_ctx(const void* A, const void* Bt, int M, int N,
+                                                 int K) {
+    Ctx c;
+    c.ra = make_rsrc(A, (uint32_t)((size_t)M * K * 2));
+    c.rb = make_rsrc(Bt, (uint32_t)((size_t)N * K * 2));
+    c.K = K;
+    return c;
+  }
+
+  static __device__ __forceinline__ void zero(Acc& a) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a.c[i][j][r] = 0.0f;
+  }
+
+  static __device__ __forceinline__ int swz(int r) { return (r >> 1) & 3; }
+
+  // Issue the direct-to-LDS loads of k-stage `s` of the tile at (row0, col0)
+  // into ring slot `slot`: one 1 KiB piece (16 rows) per wave per load.
+  static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot, int row0,
+                                               int col0, int s) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int k0 = s * KS;
+    char* abase = ring + slot * STAGE;
+    char* bbase = abase + A_STAGE;
+    const int r16 = l >> 2, p = l & 3;
+#pragma unroll
+    for (int i = 0; i < LOADS_A; ++i) {
+      const int ci = i * 4 + w;
+      const int r = ci * 16 + r16;
+      const int q = p ^ swz(r);
+      const uint32_t off = (uint32_t)(((row0 + r) * c.K + k0 + 8 * q) * 2);
+      load_lds_x4(c.ra, abase + ci * 1024, off);
+    }
+#pragma unroll
+    for (int i = 0; i < LOADS_B; ++i) {
+      const int ci = i * 4 + w;
+      const int r = ci * 16 + r16;
+      const int q = p ^ swz(r);
+      const uint32_t off = (uint32_t)(((col0 + r) * c.K + k0 + 8 * q) * 2);
+      load_lds_x4(c.rb, bbase + ci * 1024, off);
+    }
+  }
+
+  // Operands of k-step j (16 k values): one 16-byte read per 32-row block of
+  // A and per 32-column block of Bt.
+  struct Frag {
+    bf16x8 a[4], b[4];
+  };
+  static __device__ __forceinline__ void load_frag(const char* abase, int j, Frag& f) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w & 1, wn = w >> 1;
+    const int lr = l & 31, q = 2 * j + (l >> 5);
+    const char* bbase = abase + A_STAGE;
+#pragma unroll
+    for (int rb = 0; rb < 4; ++rb) {
+      const int row = wm * 128 + rb * 32 + lr;
+      f.a[rb] = *(const bf16x8*)(abase + row * ROW_BYTES + ((q ^ swz(row)) << 4));
+    }
+#pragma unroll
+    for (int cb = 0; cb < 4; ++cb) {
+      const int col = wn * 128 + cb * 32 + lr;
+      f.b[cb] = *(const bf16x8*)(bbase + col * ROW_BYTES + ((q ^ swz(col)) << 4));
+    }
+  }
+
+  // One k-stage out of ring slot `slot`; `pre` runs first (returning false
+  // abandons the stage before any accumulator changes), `mid` after the
+  // first k-step's MFMAs are issued.
+  template <class Pre, class Mid>
+  static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
+                                                 Pre&& pre, Mid&& mid) {
+    const char* abase = ring + slot * STAGE;
+    constexpr int J = KS / 16;
+    Frag f[2];
+    auto step = [&](int j) {
+      if (j + 1 < J) load_frag(abase, j + 1, f[(j + 1) & 1]);
+      const Frag& c = f[j & 1];
+#pragma unroll
+      for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+        for (int cb = 0; cb < 4; ++cb)
+          acc.c[rb][cb] =
+              __builtin_amdgcn_mfma_f32_32x32x16_bf16(c.a[rb], c.b[cb], acc.c[rb][cb], 0, 0, 0);
+    };
+    // pre() runs before any operand is in registers: a yield inside it
+    // (checkpoint, urgent tiles, restore) then needs only the accumulators
+    // live, which keeps the kernel within the register file.
+    if (!pre()) return false;
+    load_frag(abase, 0, f[0]);
+    step(0);
+    __builtin_amdgcn_sched_barrier(0);
+    mid();
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int j = 1; j < J; ++j) step(j);
+    return true;
+  }
+  static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {
+    compute(ring, slot, acc, [] { return true; }, [] {});
+  }
+
+  // Output element (tile-relative row, col) of accumulator register e.
+  static __device__ __forceinline__ void coord(int e, int& r, int& c) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w & 1, wn = w >> 1, rb = e >> 6, cb = (e >> 4) & 3, i = e & 15;
+    r = wm * 128 + rb * 32 + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+    c = wn * 128 + cb * 32 + (l & 31);
+  }
+  static __device__ __forceinline__ float get(const Acc& a, int e) {
+    return a.c[e >> 6][(e >> 4) & 3][e & 15];
+  }
+  static __device__ __forceinline__ void set(Acc& a, int e, float v) {
+    a.c[e >> 6][(e >> 4) & 3][e & 15] = v;
+  }
+
+  // Epilogue straight from the accumulators. The fingerprint (wrapping sum
+  // of mix64(bits + (e << 32)), e = row * TN + col inside the tile; this
+  // thread's part is returned when want_hash) is taken from the values read
+  // back from C, so that no loop ever indexes the accumulators dynamically
+  // (that would move all 256 of them to scratch memory).
+  static __device__ __forceinline__ uint64_t store_direct(const Acc& acc, float* C, int ldc,
+                                                          int row0, int col0, bool want_hash) {
+#pragma unroll
+    for (int e = 0; e < ACC_PER_THREAD; ++e) {
+      int r, c;
+      coord(e, r, c);
+      C[(size_t)(row0 + r) * ldc + col0 + c] = get(acc, e);
+    }
+    uint64_t h = 0;
+    if (want_hash) {
+      // A thread's loads after its own stores to the same addresses return
+      // the stored values (program order per address).
+#pragma unroll 4
+      for (int e = 0; e < ACC_PER_THREAD; ++e) {
+        int r, c;
+        coord(e, r, c);
+        const float v = C[(size_t)(row0 + r) * ldc + col0 + c];
+        h += mix64((uint64_t)__float_as_uint(v) + ((uint64_t)(r * TN + c) << 32));
+      }
+    }
+    return h;
+  }
+};
+
+}  // namespace apk

@@ -24,9 +24,6 @@
 
 namespace apk {
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
 struct EngMfma128 {
   static constexpr int TM = 128, TN = 128, KS = 32, NS = 3, THREADS = 256;
   static constexpr int A_STAGE = TM * KS * 4;               // bytes
@@ -37,6 +34,8 @@ struct EngMfma128 {
   static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 4 per thread
   static constexpr int LOADS = LOADS_A + LOADS_B;           // per stage
   static constexpr int ACC_PER_THREAD = 64;                 // floats
+  static constexpr int ELEM_BYTES = 4;                      // fp32 operands
+  static constexpr bool DIRECT_STORE = false;
 
   struct Acc {
     f32x16 c[2][2];
@@ -47,7 +46,7 @@ struct EngMfma128 {
     int K, N;
   };
 
-  static __device__ __forceinline__ Ctx make_ctx(const float* A, const float* B,
+  static __device__ __forceinline__ Ctx make_ctx(const void* A, const void* B,
                                                  int M, int N, int K) {
     Ctx c;
     c.ra = make_rsrc(A, (uint32_t)((size_t)M * K * 4));

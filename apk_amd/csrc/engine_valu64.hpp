@@ -30,6 +30,8 @@ struct EngValu64 {
   static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 2
   static constexpr int LOADS = LOADS_A + LOADS_B;
   static constexpr int ACC_PER_THREAD = 16;                 // floats
+  static constexpr int ELEM_BYTES = 4;                      // fp32 operands
+  static constexpr bool DIRECT_STORE = false;
 
   struct Acc {
     float v[4][4];
@@ -40,7 +42,7 @@ struct EngValu64 {
     int K, N;
   };
 
-  static __device__ __forceinline__ Ctx make_ctx(const float* A, const float* B,
+  static __device__ __forceinline__ Ctx make_ctx(const void* A, const void* B,
                                                  int M, int N, int K) {
     Ctx c;
     c.ra = make_rsrc(A, (uint32_t)((size_t)M * K * 4));

@@ -8,6 +8,7 @@
 // preemptible variants poll, and here they are where per-chunk timing
 // records are taken.
 #include "capi.hpp"
+#include "engine_bf16x256.hpp"
 #include "engine_mfma128.hpp"
 #include "engine_valu64.hpp"
 #include "pipeline.hpp"
@@ -16,7 +17,7 @@ namespace apk {
 
 template <class E>
 __global__ void __launch_bounds__(E::THREADS)
-    k_persistent_gemm(const float* __restrict__ A, const float* __restrict__ B,
+    k_persistent_gemm(const void* __restrict__ A, const void* __restrict__ B,
                       float* __restrict__ C, int M, int N, int K, int kChunk,
                       unsigned* next_task, apk_tile_record* log) {
   __shared__ __attribute__((aligned(16))) char ring[E::LDS_BYTES];
@@ -70,7 +71,7 @@ __global__ void __launch_bounds__(E::THREADS)
 }
 
 template <class E>
-static int launch_persistent_gemm(const float* A, const float* B, float* C,
+static int launch_persistent_gemm(const void* A, const void* B, float* C,
                                   int M, int N, int K, int kChunk,
                                   unsigned* next, apk_tile_record* log,
                                   int blocks, hipStream_t st) {
@@ -82,7 +83,8 @@ static int launch_persistent_gemm(const float* A, const float* B, float* C,
   APK_REQUIRE(kChunk > 0 && kChunk % E::KS == 0 && K % kChunk == 0,
               "persistent_gemm: k_chunk=%d must divide K=%d and be a multiple "
               "of %d", kChunk, K, E::KS);
-  APK_REQUIRE((size_t)M * K * 4 < (1ull << 31) && (size_t)K * N * 4 < (1ull << 31) &&
+  APK_REQUIRE((size_t)M * K * E::ELEM_BYTES < (1ull << 31) &&
+                  (size_t)K * N * E::ELEM_BYTES < (1ull << 31) &&
                   (size_t)M * N < (1ull << 31),
               "persistent_gemm: operands above 2 GiB are not supported");
   APK_REQUIRE(blocks > 0, "persistent_gemm: blocks=%d", blocks);
@@ -104,7 +106,7 @@ static int occupancy_of(int* out) {
 
 }  // namespace apk
 
-extern "C" int apk_persistent_gemm(int engine, const float* A, const float* B,
+extern "C" int apk_persistent_gemm(int engine, const void* A, const void* B,
                                    float* C, int M, int N, int K, int k_chunk,
                                    unsigned int* next_task, apk_tile_record* log,
                                    int blocks, void* stream) {
@@ -118,6 +120,10 @@ extern "C" int apk_persistent_gemm(int engine, const float* A, const float* B,
       return launch_persistent_gemm<EngMfma128>(A, B, C, M, N, K, k_chunk,
                                                 next_task, log, blocks,
                                                 as_stream(stream));
+    case APK_ENGINE_BF16X256:
+      return launch_persistent_gemm<EngBf16x256>(A, B, C, M, N, K, k_chunk,
+                                                 next_task, log, blocks,
+                                                 as_stream(stream));
     default:
       set_error("persistent_gemm: unknown engine %d", engine);
       return APK_EINVAL;
@@ -129,6 +135,7 @@ extern "C" int apk_persistent_gemm_occupancy(int engine, int* blocks_per_cu) {
   switch (engine) {
     case APK_ENGINE_VALU64: return occupancy_of<EngValu64>(blocks_per_cu);
     case APK_ENGINE_MFMA128: return occupancy_of<EngMfma128>(blocks_per_cu);
+    case APK_ENGINE_BF16X256: return occupancy_of<EngBf16x256>(blocks_per_cu);
     default:
       set_error("occupancy: unknown engine %d", engine);
       return APK_EINVAL;

@@ -21,6 +21,7 @@
 // from LDS after a barrier (the snapshot discipline of src/midyield.cu:
 // 177-200), so a block never splits across barriers.
 #include "capi.hpp"
+#include "engine_bf16x256.hpp"
 #include "engine_mfma128.hpp"
 #include "engine_valu64.hpp"
 #include "pipeline.hpp"
@@ -298,7 +299,8 @@ static int validate(const apk_yield_params* p, int poll, int oracle, int blocks)
   APK_REQUIRE(p->k_chunk > 0 && p->k_chunk % E::KS == 0 && p->K % p->k_chunk == 0,
               "persistent_yield: k_chunk=%d must divide K=%d and be a multiple of %d",
               p->k_chunk, p->K, E::KS);
-  APK_REQUIRE((size_t)p->M * p->K * 4 < (1ull << 31) && (size_t)p->K * p->N * 4 < (1ull << 31),
+  APK_REQUIRE((size_t)p->M * p->K * E::ELEM_BYTES < (1ull << 31) &&
+                  (size_t)p->K * p->N * E::ELEM_BYTES < (1ull << 31),
               "persistent_yield: operands above 2 GiB are not supported");
   APK_REQUIRE(blocks > 0, "persistent_yield: blocks=%d", blocks);
   APK_REQUIRE(poll >= APK_POLL_OFF && poll <= APK_POLL_STAGE, "persistent_yield: poll=%d", poll);
@@ -373,6 +375,8 @@ extern "C" int apk_persistent_yield(int engine, int poll, int oracle,
       return launch_e<EngValu64>(poll, oracle, params, blocks, as_stream(stream));
     case APK_ENGINE_MFMA128:
       return launch_e<EngMfma128>(poll, oracle, params, blocks, as_stream(stream));
+    case APK_ENGINE_BF16X256:
+      return launch_e<EngBf16x256>(poll, oracle, params, blocks, as_stream(stream));
     default:
       set_error("persistent_yield: unknown engine %d", engine);
       return APK_EINVAL;
@@ -384,6 +388,7 @@ extern "C" long long apk_yield_ckpt_floats(int engine) {
   switch (engine) {
     case APK_ENGINE_VALU64: return Ckpt<EngValu64>::SLOT_FLOATS;
     case APK_ENGINE_MFMA128: return Ckpt<EngMfma128>::SLOT_FLOATS;
+    case APK_ENGINE_BF16X256: return Ckpt<EngBf16x256>::SLOT_FLOATS;
     default: return -1;
   }
 }
@@ -404,6 +409,9 @@ extern "C" int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_
     case 3: rc = q(k_persistent_yield<EngMfma128, 0, false, false>, 256); break;
     case 4: rc = q(k_persistent_yield<EngMfma128, 1, false, false>, 256); break;
     case 5: rc = q(k_persistent_yield<EngMfma128, 2, false, false>, 256); break;
+    case 6: rc = q(k_persistent_yield<EngBf16x256, 0, false, false>, 256); break;
+    case 7: rc = q(k_persistent_yield<EngBf16x256, 1, false, false>, 256); break;
+    case 8: rc = q(k_persistent_yield<EngBf16x256, 2, false, false>, 256); break;
     default:
       set_error("occupancy: engine %d poll %d", engine, poll);
       return APK_EINVAL;

@@ -76,14 +76,9 @@ __device__ __forceinline__ void sample_flag(i32x4 flag_rsrc, int* lds_dst) {
 
 // ---------------------------------------------------------------------------
 // Bit-exact tile fingerprint: wrapping sum over the tile's elements of
-// splitmix64(bits + (e << 32)), e = row*TN + col inside the tile. Sum order
-// does not matter, so each thread hashes its own accumulators and the block
+// mix64(bits + (e << 32)), e = row*TN + col inside the tile. Sum order does
+// not matter, so each thread hashes its own accumulators and the block
 // reduces. The CPU oracle computes the same definition.
-__device__ __forceinline__ uint64_t mix64(uint64_t z) {
-  z = (z ^ (z >> 30)) * 0xbf58476d1ce4e5b9ull;
-  z = (z ^ (z >> 27)) * 0x94d049bb133111ebull;
-  return z ^ (z >> 31);
-}
 
 // Epilogue through LDS: the tile is staged row-major in LDS, then every
 // thread moves 16-byte pieces to C (coalesced rows) and, when asked, folds
@@ -93,25 +88,29 @@ template <class E>
 __device__ __forceinline__ uint64_t store_tile(const typename E::Acc& acc, char* lds,
                                                float* C, int ldc, int row0, int col0,
                                                bool want_hash) {
-  E::stage_tile(acc, lds);
-  lds_sync();
-  uint64_t h = 0;
-  const float4* t = (const float4*)lds;
-  constexpr int Q = E::TN / 4;  // float4 per row
-  for (int i = threadIdx.x; i < E::TM * Q; i += E::THREADS) {
-    const int r = i / Q, c4 = (i % Q) * 4;
-    const float4 v = t[i];
-    *(float4*)(C + (size_t)(row0 + r) * ldc + col0 + c4) = v;
-    if (want_hash) {
-      const uint64_t e = (uint64_t)(r * E::TN + c4);
-      h += mix64((uint64_t)__float_as_uint(v.x) + (e << 32));
-      h += mix64((uint64_t)__float_as_uint(v.y) + ((e + 1) << 32));
-      h += mix64((uint64_t)__float_as_uint(v.z) + ((e + 2) << 32));
-      h += mix64((uint64_t)__float_as_uint(v.w) + ((e + 3) << 32));
+  if constexpr (E::DIRECT_STORE) {
+    return E::store_direct(acc, C, ldc, row0, col0, want_hash);
+  } else {
+    E::stage_tile(acc, lds);
+    lds_sync();
+    uint64_t h = 0;
+    const float4* t = (const float4*)lds;
+    constexpr int Q = E::TN / 4;  // float4 per row
+    for (int i = threadIdx.x; i < E::TM * Q; i += E::THREADS) {
+      const int r = i / Q, c4 = (i % Q) * 4;
+      const float4 v = t[i];
+      *(float4*)(C + (size_t)(row0 + r) * ldc + col0 + c4) = v;
+      if (want_hash) {
+        const uint64_t e = (uint64_t)(r * E::TN + c4);
+        h += mix64((uint64_t)__float_as_uint(v.x) + (e << 32));
+        h += mix64((uint64_t)__float_as_uint(v.y) + ((e + 1) << 32));
+        h += mix64((uint64_t)__float_as_uint(v.z) + ((e + 2) << 32));
+        h += mix64((uint64_t)__float_as_uint(v.w) + ((e + 3) << 32));
+      }
     }
+    lds_sync();  // LDS reads done before the ring is refilled
+    return h;
   }
-  lds_sync();  // LDS reads done before the ring is refilled
-  return h;
 }
 
 // Sum a per-thread uint64 over the block; valid in thread 0. `red` holds

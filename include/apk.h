@@ -27,13 +27,24 @@ enum {
 };
 
 /* Tile engines (compute of one output tile).
- *  VALU64  : 64x64 fp32 tile, 256 threads, one fmaf chain per output in the
- *            reference's k order (src/tile.cuh:62-107) -- bit-identical to a
- *            correctly rounded sequential fmaf over k.
- *  MFMA128 : 128x128 fp32 tile on v_mfma_f32_32x32x2_f32 (fp32 matrix cores),
- *            256 threads, 3-stage LDS ring fed by buffer_load ... lds.
+ *  VALU64   : 64x64 fp32 tile, 256 threads, one fmaf chain per output in the
+ *             reference's k order (src/tile.cuh:62-107) -- bit-identical to a
+ *             correctly rounded sequential fmaf over k.
+ *  MFMA128  : 128x128 fp32 tile on v_mfma_f32_32x32x2_f32 (fp32 matrix
+ *             cores), 256 threads, 3-stage LDS ring fed by buffer_load ... lds.
+ *  BF16X256 : 256x256 tile of a bf16 GEMM with fp32 accumulation on
+ *             v_mfma_f32_32x32x16_bf16 (replaces the reference's fp16 wmma
+ *             tile, src/tcyield.cu:91-356). Operands are bf16 (uint16 bit
+ *             patterns): A is M x K row-major and B is passed TRANSPOSED, as
+ *             Bt = N x K row-major (C = A . Bt^T); C is fp32 M x N.
+ * For the fp32 engines A is M x K and B is K x N, row-major fp32.
  */
-enum { APK_ENGINE_VALU64 = 0, APK_ENGINE_MFMA128 = 1, APK_ENGINE_COUNT = 2 };
+enum {
+  APK_ENGINE_VALU64 = 0,
+  APK_ENGINE_MFMA128 = 1,
+  APK_ENGINE_BF16X256 = 2,
+  APK_ENGINE_COUNT = 3
+};
 
 /* Per-step timing record; layout of TileRecord (src/tile.cuh:37-42). start
  * and end are device wall-clock ticks (s_memrealtime, rate in
@@ -61,6 +72,8 @@ typedef struct apk_engine_geometry {
   int k_stage;            /* k depth of one LDS stage */
   int threads;            /* block size */
   int lds_bytes;          /* static LDS per block */
+  int elem_bytes;         /* operand element size: 4 = fp32, 2 = bf16 */
+  int b_transposed;       /* 1: B is passed as Bt (N x K row-major) */
 } apk_engine_geometry;
 
 /* Text of the last error raised in this thread. */
@@ -88,7 +101,7 @@ int apk_persistent_gemm_occupancy(int engine, int* blocks_per_cu);
  * (tile, chunk): log[tile * (K/k_chunk) + chunk]. k_chunk == K reproduces the
  * reference exactly. Requires M % tile_m == 0, N % tile_n == 0,
  * K % k_chunk == 0, k_chunk % k_stage == 0. */
-int apk_persistent_gemm(int engine, const float* A, const float* B, float* C,
+int apk_persistent_gemm(int engine, const void* A, const void* B, float* C,
                         int M, int N, int K, int k_chunk,
                         unsigned int* next_task, apk_tile_record* log,
                         int blocks, void* stream);
@@ -126,16 +139,16 @@ enum { APK_RESUME_CKPT_FULL = 0, APK_RESUME_CKPT_ACC = 1, APK_RESUME_RESTART = 2
 
 typedef struct apk_yield_params {
   /* background GEMM; tasks cycle the tile grid (src/urgent_baseline.cu:78-80) */
-  const float* A;
-  const float* B;
+  const void* A;               /* element type and B layout per engine (above) */
+  const void* B;
   float* C;
   int M, N, K, k_chunk;
   unsigned int num_tasks;
   unsigned int* next_task;     /* fetch-add counter, 0 at launch */
   /* urgent job: Cu (Mu x Nu) = Au (Mu x Ku) . Bu (Ku x Nu), split into tiles
    * that yielding blocks pop per event */
-  const float* Au;
-  const float* Bu;
+  const void* Au;
+  const void* Bu;
   float* Cu;
   int Mu, Nu, Ku;
   int* uq_next;                /* [events] mini-queue counters, 0 at launch */

@@ -27,8 +27,13 @@ def test_library_exports_every_header_symbol():
 def test_engine_geometry():
     g = apk_amd.geometry(apk_amd.ENGINE_VALU64)
     assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (64, 64, 32, 256)
+    assert (g.elem_bytes, g.b_transposed) == (4, 0)
     g = apk_amd.geometry(apk_amd.ENGINE_MFMA128)
     assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (128, 128, 32, 256)
+    assert g.lds_bytes <= 160 * 1024
+    g = apk_amd.geometry(apk_amd.ENGINE_BF16X256)
+    assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (256, 256, 32, 256)
+    assert (g.elem_bytes, g.b_transposed) == (2, 1)
     assert g.lds_bytes <= 160 * 1024
     with pytest.raises(apk_amd.ApkError):
         apk_amd.geometry(99)
@@ -40,6 +45,8 @@ def test_engine_geometry():
     (apk_amd.ENGINE_MFMA128, 128, 128, 64, 48, 4, "k_chunk"),
     (apk_amd.ENGINE_VALU64, 64, 64, 64, 64, 0, "blocks"),
     (apk_amd.ENGINE_VALU64, 0, 64, 64, 64, 1, "empty"),
+    (apk_amd.ENGINE_BF16X256, 256, 128, 64, 64, 4, "multiples"),
+    (apk_amd.ENGINE_BF16X256, 256, 256, 64, 48, 4, "k_chunk"),
     (7, 64, 64, 64, 64, 1, "engine"),
 ])
 def test_persistent_gemm_rejects_bad_args(engine, M, N, K, kc, blocks, frag):
@@ -99,6 +106,7 @@ def test_yield_rejects_bad_args():
     # accumulators (64 floats x 256 threads) + the two resident 32 KiB stages
     assert apk_amd.ckpt_floats(apk_amd.ENGINE_MFMA128) == 64 * 256 + 2 * 32 * 1024 // 4
     assert apk_amd.ckpt_floats(apk_amd.ENGINE_VALU64) == 16 * 256 + 2 * 16 * 1024 // 4
+    assert apk_amd.ckpt_floats(apk_amd.ENGINE_BF16X256) == 256 * 256 + 2 * 32 * 1024 // 4
 
 
 def test_python_constants_match_header():
