@@ -48,6 +48,7 @@ POLL_OFF, POLL_CHUNK, POLL_STAGE = 0, 1, 2
 RESUME_CKPT_FULL, RESUME_CKPT_ACC, RESUME_RESTART = 0, 1, 2
 FLAG_STRIDE, FLAG_MAX_COPIES = 4096, 256
 STATS_PER_BLOCK = 8
+QUEUE_WORDS, QUEUE_XCDS = 16, 8
 
 
 class YieldParams(ctypes.Structure):

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "apk.h"
+
 namespace apk {
 
 // ---------------------------------------------------------------------------
@@ -42,6 +44,12 @@ __device__ __forceinline__ void atomic_max_u64(unsigned long long* p,
 // src/tile.cuh:44-48).
 __device__ __forceinline__ int64_t wall_ticks() { return (int64_t)wall_clock64(); }
 __device__ __forceinline__ unsigned hw_slot() { return __smid(); }
+// The XCD (XCC) the executing wave runs on, 0..7 on MI355X: hardware
+// register XCC_ID (20), bits [3:0] -> s_getreg_b32 immediate
+// size-1 = 3 << 11 | offset 0 << 6 | 20.
+__device__ __forceinline__ unsigned xcc_id() {
+  return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & (APK_QUEUE_XCDS - 1);
+}
 
 // ---------------------------------------------------------------------------
 // Barriers. __syncthreads() carries a workgroup release/acquire fence, which

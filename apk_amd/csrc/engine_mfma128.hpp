@@ -9,10 +9,15 @@
 //
 // LDS layouts (bank-conflict-free for the MFMA operand reads):
 //  A stage: 128 rows x 128 B. 16-byte quad q of row r is stored at slot
-//           q ^ (r & 7), so eight consecutive rows reading the same quad hit
-//           eight different 16-byte bank groups.
-//  B stage: 32 rows x 512 B, natural order; an operand read is 32
-//           consecutive dwords of one row per half-wave.
+//           q ^ aswz(r), aswz(r) = (r ^ (r >> 3)) & 7: 8 (or 16) consecutive
+//           rows reading the same quad hit 8 (16) different 16-byte bank
+//           groups, whether the LDS serves 128 B or 256 B per cycle.
+//  B stage: 32 rows x 512 B; 16-byte chunk c of row k is stored at slot
+//           c ^ (((k >> 2) & 1) << 3). An operand read is 32 consecutive
+//           dwords of row k for the lower half-wave and of row k+4 for the
+//           upper one; the XOR moves the upper half by 128 B, so the two
+//           halves never share a bank even when all 64 lanes are served in
+//           one cycle.
 //
 // k order inside a stage: k-group g (8 values) is consumed in 4 MFMA steps;
 // in step s the lower half-wave supplies k = 8g+s and the upper half-wave
@@ -40,6 +45,9 @@ struct EngMfma128 {
   struct Acc {
     f32x16 c[2][2];
   };
+
+  static __device__ __forceinline__ int aswz(int r) { return (r ^ (r >> 3)) & 7; }
+  static __device__ __forceinline__ int bswz(int k) { return ((k >> 2) & 1) << 3; }
 
   struct Ctx {
     i32x4 ra, rb;
@@ -77,7 +85,7 @@ struct EngMfma128 {
     for (int i = 0; i < LOADS_A; ++i) {
       const int ci = i * 4 + w;          // 1 KiB piece = 8 rows of 128 B
       const int r = ci * 8 + (l >> 3);
-      const int q = (l & 7) ^ (r & 7);   // global quad landing in slot l&7
+      const int q = (l & 7) ^ aswz(r);   // global quad landing in slot l&7
       const uint32_t off = (uint32_t)(((row0 + r) * c.K + k0 + 4 * q) * 4);
       load_lds_x4(c.ra, abase + ci * 1024, off);
     }
@@ -85,7 +93,8 @@ struct EngMfma128 {
     for (int i = 0; i < LOADS_B; ++i) {
       const int ci = i * 4 + w;          // 1 KiB piece = 2 rows of 512 B
       const int r = ci * 2 + (l >> 5);
-      const uint32_t off = (uint32_t)(((k0 + r) * c.N + col0 + 4 * (l & 31)) * 4);
+      const int cq = (l & 31) ^ bswz(r); // global chunk landing in slot l&31
+      const uint32_t off = (uint32_t)(((k0 + r) * c.N + col0 + 4 * cq) * 4);
       load_lds_x4(c.rb, bbase + ci * 1024, off);
     }
   }
@@ -105,14 +114,16 @@ struct EngMfma128 {
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
       const int row = wm * 64 + rb * 32 + lr;
-      const int q = (2 * g + h) ^ (row & 7);
+      const int q = (2 * g + h) ^ aswz(row);
       f.a4[rb] = *(const f32x4*)(abase + row * 128 + q * 16);
     }
+    // Row k = 8g + 4h + s has bswz(k) = h << 3 for every s.
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
       const int col = wn * 64 + cb * 32 + lr;
+      const int cpos = (((col >> 2) ^ (h << 3)) << 2) | (col & 3);
 #pragma unroll
-      for (int s = 0; s < 4; ++s) f.bv[cb][s] = bbase[(8 * g + 4 * h + s) * TN + col];
+      for (int s = 0; s < 4; ++s) f.bv[cb][s] = bbase[(8 * g + 4 * h + s) * TN + cpos];
     }
   }
 

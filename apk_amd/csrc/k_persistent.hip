@@ -25,6 +25,8 @@ __global__ void __launch_bounds__(E::THREADS)
 
   const int tilesN = N / E::TN;
   const unsigned numTasks = (unsigned)((M / E::TM) * tilesN);
+  const TaskQueue tq(next_task, M / E::TM, tilesN, numTasks);
+  const int home = (int)xcc_id();
   const int nChunks = K / kChunk;
   const int spc = kChunk / E::KS;  // k-stages per chunk
   const typename E::Ctx ctx = E::make_ctx(A, B, M, N, K);
@@ -33,7 +35,7 @@ __global__ void __launch_bounds__(E::THREADS)
     // Reconverge before the thread-0 pop (no thread-0 region of the previous
     // iteration may be threaded into this one across the back-edge).
     lds_sync();
-    if (threadIdx.x == 0) s_task = fetch_add_u32(next_task, 1u);
+    if (threadIdx.x == 0) s_task = tq.pop(home);
     __syncthreads();
     const unsigned task = uniform(s_task);
     __syncthreads();  // every thread has read s_task before it is rewritten

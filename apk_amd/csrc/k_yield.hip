@@ -38,6 +38,8 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   const int tid = threadIdx.x, bid = blockIdx.x, G = gridDim.x;
   const int tilesN = P.N / E::TN;
   const int totalTiles = (P.M / E::TM) * tilesN;
+  const TaskQueue tq(P.next_task, P.M / E::TM, tilesN, P.num_tasks);
+  const int home = (int)xcc_id();
   const int S = P.K / E::KS;
   const int spc = P.k_chunk / E::KS;
   const int pollStride =
@@ -137,7 +139,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     // loop iterations (lanes 1..63 spinning on a stale task at the barrier
     // below while lane 0 waits outside the loop to pop the next one).
     lds_sync();
-    if (tid == 0) s_u32 = fetch_add_u32(P.next_task, 1u);
+    if (tid == 0) s_u32 = tq.pop(home);
     __syncthreads();
     const unsigned task = uniform(s_u32);
     __syncthreads();
@@ -303,6 +305,7 @@ static int validate(const apk_yield_params* p, int poll, int oracle, int blocks)
                   (size_t)p->K * p->N * E::ELEM_BYTES < (1ull << 31),
               "persistent_yield: operands above 2 GiB are not supported");
   APK_REQUIRE(blocks > 0, "persistent_yield: blocks=%d", blocks);
+  APK_REQUIRE(p->num_tasks < (1u << 31), "persistent_yield: num_tasks=%u", p->num_tasks);
   APK_REQUIRE(poll >= APK_POLL_OFF && poll <= APK_POLL_STAGE, "persistent_yield: poll=%d", poll);
   APK_REQUIRE(p->num_events >= 0, "persistent_yield: num_events < 0");
   if (poll != APK_POLL_OFF) {

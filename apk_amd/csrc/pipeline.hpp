@@ -8,6 +8,53 @@
 namespace apk {
 
 // ---------------------------------------------------------------------------
+// XCD-aware work queue. The tile grid (tilesM x tilesN) is walked in a
+// grouped order G: bands of GM tile rows, column by column inside a band, so
+// that consecutive positions form GM x n blocks of the grid. Positions
+// [q*T/8, (q+1)*T/8) of G are XCD q's list; pass p of the task space maps
+// position i of list q to task p*T + G(i). A worker pops its own XCD's list
+// (counter ctr[q]) and, once that is exhausted, the other lists in turn, so
+// every task id below num_tasks is handed out exactly once and task u always
+// computes tile u % T.
+struct TaskQueue {
+  static constexpr int GM = 4;
+  unsigned* ctr;
+  int tilesM, tilesN, T;
+  unsigned numTasks, passes;
+
+  __device__ __forceinline__ TaskQueue(unsigned* c, int tm, int tn, unsigned n)
+      : ctr(c), tilesM(tm), tilesN(tn), T(tm * tn), numTasks(n),
+        passes((n + (unsigned)(tm * tn) - 1) / (unsigned)(tm * tn)) {}
+
+  __device__ __forceinline__ int grouped(int i) const {
+    const int band = i / (GM * tilesN);
+    const int rows = min(GM, tilesM - band * GM);
+    const int r = i - band * GM * tilesN;
+    return (band * GM + r % rows) * tilesN + r / rows;
+  }
+  __device__ __forceinline__ int list_begin(int q) const {
+    return (int)(((long long)q * T) / APK_QUEUE_XCDS);
+  }
+  // Thread-0 only. Returns the next task id, or 0xffffffff when every list
+  // is exhausted.
+  __device__ __forceinline__ unsigned pop(int home) const {
+    for (int k = 0; k < APK_QUEUE_XCDS; ++k) {
+      const int q = (home + k) & (APK_QUEUE_XCDS - 1);
+      const int b = list_begin(q), n = list_begin(q + 1) - b;
+      if (n == 0) continue;
+      const unsigned total = (unsigned)n * passes;
+      for (;;) {
+        const unsigned j = fetch_add_u32(&ctr[q], 1u);
+        if (j >= total) break;
+        const unsigned u = (j / (unsigned)n) * (unsigned)T + (unsigned)grouped(b + (int)(j % (unsigned)n));
+        if (u < numTasks) return u;
+      }
+    }
+    return 0xffffffffu;
+  }
+};
+
+// ---------------------------------------------------------------------------
 // The ring protocol of every stage loop here (NS = 3 slots, one barrier per
 // k-stage):
 //   prologue  issue(0), issue(1)

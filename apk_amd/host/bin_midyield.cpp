@@ -205,10 +205,10 @@ int main(int argc, char** argv) {
     HIP_CHECK(hipMalloc(&dAu, hAu.size() * 4));
     HIP_CHECK(hipMalloc(&dBu, hBu.size() * 4));
     HIP_CHECK(hipMalloc(&dCu, uRefGpu.size() * 4));
-    HIP_CHECK(hipMalloc(&dNx, 4));
+    HIP_CHECK(hipMalloc(&dNx, APK_QUEUE_WORDS * sizeof(unsigned)));
     HIP_CHECK(hipMemcpy(dAu, hAu.data(), hAu.size() * 4, hipMemcpyHostToDevice));
     HIP_CHECK(hipMemcpy(dBu, hBu.data(), hBu.size() * 4, hipMemcpyHostToDevice));
-    HIP_CHECK(hipMemset(dNx, 0, 4));
+    HIP_CHECK(hipMemset(dNx, 0, APK_QUEUE_WORDS * sizeof(unsigned)));
     APK_CHECK(apk_persistent_gemm(engine, dAu, dBu, dCu, Mu, Nu, Ku, Ku, dNx, nullptr,
                                   std::min(U, blocks), kStream));
     HIP_CHECK(hipStreamSynchronize(kStream));

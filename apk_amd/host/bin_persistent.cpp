@@ -93,7 +93,7 @@ int main(int argc, char** argv) {
   HIP_CHECK(hipMalloc(&dA, hA.size() * sizeof(float)));
   HIP_CHECK(hipMalloc(&dB, hB.size() * sizeof(float)));
   HIP_CHECK(hipMalloc(&dC, (size_t)M * N * sizeof(float)));
-  HIP_CHECK(hipMalloc(&dNext, sizeof(unsigned)));
+  HIP_CHECK(hipMalloc(&dNext, APK_QUEUE_WORDS * sizeof(unsigned)));
   HIP_CHECK(hipMalloc(&dLog, (size_t)numRecs * sizeof(apk_tile_record)));
   HIP_CHECK(hipMemcpy(dA, hA.data(), hA.size() * sizeof(float), hipMemcpyHostToDevice));
   HIP_CHECK(hipMemcpy(dB, hB.data(), hB.size() * sizeof(float), hipMemcpyHostToDevice));
@@ -107,7 +107,7 @@ int main(int argc, char** argv) {
     // fails loudly (src/persistent.cu:156-160).
     HIP_CHECK(hipMemset(dC, 0xFF, (size_t)M * N * sizeof(float)));
     HIP_CHECK(hipMemset(dLog, 0xFF, (size_t)numRecs * sizeof(apk_tile_record)));
-    HIP_CHECK(hipMemset(dNext, 0, sizeof(unsigned)));
+    HIP_CHECK(hipMemset(dNext, 0, APK_QUEUE_WORDS * sizeof(unsigned)));
     HIP_CHECK(hipDeviceSynchronize());
     HIP_CHECK(hipEventRecord(e0, 0));
     APK_CHECK(apk_persistent_gemm(engine, dA, dB, dC, M, N, K, kChunk, dNext, dLog,

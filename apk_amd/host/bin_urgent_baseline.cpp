@@ -136,12 +136,13 @@ int main(int argc, char** argv) {
   HIP_CHECK(hipMalloc(&dAu, hAu.size() * 4));
   HIP_CHECK(hipMalloc(&dBu, hBu.size() * 4));
   HIP_CHECK(hipMalloc(&dCu, (size_t)urgentM * urgentN * 4));
-  HIP_CHECK(hipMalloc(&dUNext, sizeof(unsigned)));
+  HIP_CHECK(hipMalloc(&dUNext, APK_QUEUE_WORDS * sizeof(unsigned)));
   HIP_CHECK(hipMalloc(&dULog, (size_t)uTiles * uChunks * sizeof(apk_tile_record)));
   HIP_CHECK(hipMemcpy(dAu, hAu.data(), hAu.size() * 4, hipMemcpyHostToDevice));
   HIP_CHECK(hipMemcpy(dBu, hBu.data(), hBu.size() * 4, hipMemcpyHostToDevice));
-  unsigned* hConsumed;  // pinned, for the mid-flight queue snapshot
-  HIP_CHECK(hipHostMalloc((void**)&hConsumed, sizeof(unsigned), hipHostMallocDefault));
+  unsigned* hConsumed;  // pinned, for the mid-flight queue snapshot (per-XCD counters)
+  HIP_CHECK(hipHostMalloc((void**)&hConsumed, APK_QUEUE_WORDS * sizeof(unsigned),
+                          hipHostMallocDefault));
 
   hipStream_t bgStream, uStream;
   HIP_CHECK(hipStreamCreateWithFlags(&bgStream, hipStreamNonBlocking));
@@ -152,7 +153,7 @@ int main(int argc, char** argv) {
                bgStream);
   };
   auto launch_urgent = [&]() {
-    HIP_CHECK(hipMemsetAsync(dUNext, 0, sizeof(unsigned), uStream));
+    HIP_CHECK(hipMemsetAsync(dUNext, 0, APK_QUEUE_WORDS * sizeof(unsigned), uStream));
     APK_CHECK(apk_persistent_gemm(engine, dAu, dBu, dCu, urgentM, urgentN, urgentK, urgentK,
                                   dUNext, dULog, urgentBlocks, uStream));
   };
@@ -236,7 +237,7 @@ int main(int argc, char** argv) {
     launch_bg();
     spin_until_ns(t0 + (int64_t)(delayUs * 1e3));
     const int64_t tArrive = now_ns();
-    HIP_CHECK(hipMemcpyAsync(hConsumed, rig.dNextTask(), sizeof(unsigned),
+    HIP_CHECK(hipMemcpyAsync(hConsumed, rig.dNextTask(), APK_QUEUE_XCDS * sizeof(unsigned),
                              hipMemcpyDeviceToHost, uStream));
     launch_urgent();
     HIP_CHECK(hipStreamSynchronize(uStream));
@@ -244,8 +245,10 @@ int main(int argc, char** argv) {
     HIP_CHECK(hipStreamSynchronize(bgStream));
     auto [bS, bE] = rig.readRunGT();
     auto [uS, uE] = urgent_window();
+    unsigned consumed = 0;  // pops handed out at arrival, summed over the XCD lists
+    for (int q = 0; q < APK_QUEUE_XCDS; ++q) consumed += hConsumed[q];
     rows.push_back({delayUs, (tDone - tArrive) / 1e3, (uE - uS) * tickUs, (uS - bE) * tickUs,
-                    (bE - bS) * tickUs, std::min(*hConsumed, (unsigned)bgTasks)});
+                    (bE - bS) * tickUs, std::min(consumed, (unsigned)bgTasks)});
   }
 
   std::vector<double> e2e, gap, exec, drain;

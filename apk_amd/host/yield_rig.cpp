@@ -34,7 +34,7 @@ YieldRig::YieldRig(const RigShape& s, const std::vector<float>& A,
     HIP_CHECK(hipMemcpy(dAu_, Au.data(), Au.size() * 4, hipMemcpyHostToDevice));
     HIP_CHECK(hipMemcpy(dBu_, Bu.data(), Bu.size() * 4, hipMemcpyHostToDevice));
   }
-  dNext_ = dalloc<unsigned>(1);
+  dNext_ = dalloc<unsigned>(APK_QUEUE_WORDS);
   const size_t flagBytes = (size_t)APK_FLAG_MAX_COPIES * APK_FLAG_STRIDE;
   if (s.hostFlag) {
     HIP_CHECK(hipHostMalloc((void**)&hFlag_, flagBytes, hipHostMallocCoherent | hipHostMallocMapped));
@@ -73,7 +73,7 @@ YieldRig::~YieldRig() {
 void YieldRig::reset(bool nanFill) {
   const int E = s_.events > 0 ? s_.events : 1;
   HIP_CHECK(hipDeviceSynchronize());
-  HIP_CHECK(hipMemset(dNext_, 0, sizeof(unsigned)));
+  HIP_CHECK(hipMemset(dNext_, 0, APK_QUEUE_WORDS * sizeof(unsigned)));
   if (hFlag_) hostSetFlag(0);
   else HIP_CHECK(hipMemset(dFlag_, 0, (size_t)APK_FLAG_MAX_COPIES * APK_FLAG_STRIDE));
   HIP_CHECK(hipMemset(dSet_, 0, E * sizeof(long long)));

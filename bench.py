@@ -118,7 +118,7 @@ def main():
     dB = torch.rand((K, N), generator=gen, device="cuda", dtype=torch.float32) * 2 - 1
     dC = torch.empty((M, N), device="cuda", dtype=torch.float32)
     total = args.warmup + args.steps
-    counters = torch.zeros(total, dtype=torch.int32, device="cuda")
+    counters = torch.zeros((total, apk_amd.QUEUE_WORDS), dtype=torch.int32, device="cuda")
     stream = torch.cuda.current_stream()
     starts = [torch.cuda.Event(enable_timing=True) for _ in range(total)]
     ends = [torch.cuda.Event(enable_timing=True) for _ in range(total)]
@@ -129,7 +129,7 @@ def main():
     def step(i):
         starts[i].record(stream)
         apk_amd.persistent_gemm(eng, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(),
-                                M, N, K, kc, counters[i:].data_ptr(), None, blocks,
+                                M, N, K, kc, counters[i].data_ptr(), None, blocks,
                                 stream.cuda_stream)
         ends[i].record(stream)
 

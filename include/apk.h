@@ -92,8 +92,8 @@ int apk_engine_geometry_of(int engine, apk_engine_geometry* out);
 int apk_persistent_gemm_occupancy(int engine, int* blocks_per_cu);
 
 /* persistent_gemm (src/persistent.cu:51-79): a persistent grid of `blocks`
- * workers pops output tiles from the fetch-add counter *next_task (must be 0
- * at launch) until tilesM*tilesN tiles are taken. Each tile computes
+ * workers pops output tiles from the work queue next_task (APK_QUEUE_WORDS
+ * counters, 0 at launch) until all tilesM*tilesN tiles are taken. Each tile computes
  * C[tile] = A[rows, 0:K] . B[0:K, cols] with A MxK, B KxN, C MxN row-major
  * fp32 (lda = K, ldb = N, ldc = N). The reference's task is one tile with
  * per-task K; here K may be split into K/k_chunk chunks walked in order by
@@ -135,6 +135,15 @@ enum { APK_POLL_OFF = 0, APK_POLL_CHUNK = 1, APK_POLL_STAGE = 2 };
 #define APK_FLAG_STRIDE 4096
 #define APK_FLAG_MAX_COPIES 256
 #define APK_STATS_PER_BLOCK 8
+
+/* Work queue: every persistent kernel pops tasks from APK_QUEUE_WORDS
+ * unsigned counters (zero at launch). The tiles are split into
+ * APK_QUEUE_XCDS lists, one per XCD, each a compact 2-D region of the tile
+ * grid; a worker pops from its own XCD's list first (so concurrently running
+ * tiles share A and B panels in that XCD's L2) and steals from the others
+ * when it is empty. Task u always computes tile u mod (tilesM * tilesN). */
+#define APK_QUEUE_WORDS 16
+#define APK_QUEUE_XCDS 8
 enum { APK_RESUME_CKPT_FULL = 0, APK_RESUME_CKPT_ACC = 1, APK_RESUME_RESTART = 2 };
 
 typedef struct apk_yield_params {
@@ -143,8 +152,8 @@ typedef struct apk_yield_params {
   const void* B;
   float* C;
   int M, N, K, k_chunk;
-  unsigned int num_tasks;
-  unsigned int* next_task;     /* fetch-add counter, 0 at launch */
+  unsigned int num_tasks;      /* < 2^31 */
+  unsigned int* next_task;     /* APK_QUEUE_WORDS counters, 0 at launch */
   /* urgent job: Cu (Mu x Nu) = Au (Mu x Ku) . Bu (Ku x Nu), split into tiles
    * that yielding blocks pop per event */
   const void* Au;

@@ -24,7 +24,7 @@ def run_persistent(torch, apk, engine, A, B, k_chunk, blocks=None, with_log=True
         blocks = apk.device_info().cu_count * apk.occupancy(engine)
     dA, dB = dev(torch, A), dev(torch, B)
     dC = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda") if C is None else C
-    nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+    nxt = torch.zeros(apk.QUEUE_WORDS, dtype=torch.int32, device="cuda")
     nrec = (M // g.tile_m) * (N // g.tile_n) * (K // k_chunk)
     log = torch.full((nrec * 3,), -1, dtype=torch.int64, device="cuda") if with_log else None
     stream = torch.cuda.current_stream().cuda_stream
@@ -39,4 +39,18 @@ def run_persistent(torch, apk, engine, A, B, k_chunk, blocks=None, with_log=True
         recs = {"start": raw[:, 0], "end": raw[:, 1],
                 "smid": (raw[:, 2] & 0xffffffff).astype(np.int64).astype(np.int32),
                 "block": (raw[:, 2] >> 32).astype(np.int32)}
-    return out, recs, int(nxt.cpu().numpy()[0])
+    return out, recs, nxt.cpu().numpy()
+
+
+def assert_queue_drained(ctr, tasks, blocks, xcds=8):
+    """Counters of the XCD-aware queue after a run with tasks == tiles: list
+    q holds positions [q*T/8, (q+1)*T/8) and every one was handed out; every
+    worker ends with one failed pop on each non-empty list."""
+    T = tasks
+    for q in range(xcds):
+        n = (q + 1) * T // xcds - q * T // xcds
+        if n:
+            assert ctr[q] >= n + blocks, (q, ctr[q], n, blocks)
+        else:
+            assert ctr[q] == 0, (q, ctr[q])
+    assert not ctr[xcds:].any()

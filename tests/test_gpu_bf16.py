@@ -18,7 +18,7 @@ import numpy as np
 import pytest
 
 import oracle
-from gpu_util import dev, say
+from gpu_util import assert_queue_drained, dev, say
 
 pytestmark = pytest.mark.gpu
 
@@ -39,11 +39,11 @@ def run_bf16(torch, apk, A_bits, Bt_bits, k_chunk, blocks=None):
         blocks = apk.device_info().cu_count * apk.occupancy(eng)
     dA, dB = dev(torch, A_bits.view(np.int16)), dev(torch, Bt_bits.view(np.int16))
     dC = torch.full((M, N), float("nan"), dtype=torch.float32, device="cuda")
-    nxt = torch.zeros(1, dtype=torch.int32, device="cuda")
+    nxt = torch.zeros(apk.QUEUE_WORDS, dtype=torch.int32, device="cuda")
     apk.persistent_gemm(eng, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(), M, N, K, k_chunk,
                         nxt.data_ptr(), None, blocks, torch.cuda.current_stream().cuda_stream)
     torch.cuda.synchronize()
-    return dC.cpu().numpy(), int(nxt.cpu().numpy()[0])
+    return dC.cpu().numpy(), nxt.cpu().numpy()
 
 
 def test_bf16_layout_exact_small_integers(torch_gpu, apk):
@@ -54,7 +54,7 @@ def test_bf16_layout_exact_small_integers(torch_gpu, apk):
     Bt_bits, Bt = bits_of_small_ints(rng, (N, K))
     C, nxt = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=K, blocks=3)
     ref = (A.astype(np.int64) @ Bt.astype(np.int64).T).astype(np.float32)
-    assert nxt == (M // 256) * (N // 256) + 3
+    assert_queue_drained(nxt, (M // 256) * (N // 256), blocks=3)
     assert np.array_equal(C, ref)
 
 
@@ -107,7 +107,7 @@ class Bf16Job:
         E = max(events, 1)
         i32, i64 = T.int32, T.int64
         z = lambda n, t: T.zeros(n, dtype=t, device="cuda")
-        self.nxt, self.uq = z(1, i32), z(E, i32)
+        self.nxt, self.uq = z(apk.QUEUE_WORDS, i32), z(E, i32)
         self.flag = z(apk.FLAG_MAX_COPIES * apk.FLAG_STRIDE // 4, i32)
         self.sched, self.set_gt, self.obs = z(E, i64), z(E, i64), z(E * blocks, i64)
         self.claim, self.site, self.u_gt, self.u_end = z(E, i32), z(E, i32), z(2 * E, i64), z(E, i64)

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 
 import oracle
-from gpu_util import run_persistent, say
+from gpu_util import assert_queue_drained, run_persistent, say
 
 pytestmark = pytest.mark.gpu
 
@@ -33,7 +33,7 @@ def test_cfg1_valu64_bit_exact(torch_gpu, apk):
     assert bad == 0 and nans == 0
     assert oracle.rel_frobenius(C, ref) <= FROB_F32
     assert (recs["block"] >= 0).all() and (recs["end"] >= recs["start"]).all()
-    assert nxt >= 256
+    assert nxt[:8].sum() >= 256
 
 
 def test_valu64_chunked_bit_exact_reference_seed(torch_gpu, apk):
@@ -70,7 +70,7 @@ def test_mfma128_single_tile_and_idle_workers(torch_gpu, apk):
     C, _, nxt = run_persistent(torch_gpu, apk, apk.ENGINE_MFMA128, A, B, 32, blocks=64)
     ref = oracle.gemm_f64(A, B)
     assert oracle.rel_frobenius(C, ref) <= FROB_F32
-    assert nxt == 1 + 64   # one tile taken, every worker popped once more and left
+    assert_queue_drained(nxt, 1, 64)  # one tile taken; every worker's last pop failed
 
 
 def test_cfg2_full_size_sampled_rows(torch_gpu, apk):

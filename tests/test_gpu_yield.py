@@ -45,7 +45,7 @@ class Job:
         self.dCu = T.empty((Mu, Nu), dtype=T.float32, device="cuda")
         E = max(events, 1)
         i32, i64 = T.int32, T.int64
-        self.nxt = T.zeros(1, dtype=i32, device="cuda")
+        self.nxt = T.zeros(apk.QUEUE_WORDS, dtype=i32, device="cuda")
         self.flag = T.zeros(apk.FLAG_MAX_COPIES * apk.FLAG_STRIDE // 4, dtype=i32, device="cuda")
         self.sched = T.zeros(E, dtype=i64, device="cuda")
         self.set_gt = T.zeros(E, dtype=i64, device="cuda")
