@@ -119,6 +119,26 @@ __device__ __forceinline__ uint64_t mix64(uint64_t z) {
   return z ^ (z >> 31);
 }
 
+// 32-bit LDS byte address of a pointer into __shared__ memory.
+__device__ __forceinline__ uint32_t lds_addr_of(const void* p) {
+  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const void*)p);
+}
+// Index of the executing wave in its block, as a scalar.
+__device__ __forceinline__ int wave_id() {
+  return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+}
+// Direct-to-LDS 16-byte-per-lane buffer load with every address part but
+// the lane offset kept scalar: lane l's bytes land at LDS address lds + 16*l
+// (lds in M0), read from base + soff + voff. The stage loops issue eight of
+// these per k-stage between MFMAs, so each costs three scalar instructions.
+__device__ __forceinline__ void dma_x4(i32x4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc),
+                 "s"(__builtin_amdgcn_readfirstlane(soff))
+               : "memory");
+}
+
 // One 16-byte-per-lane buffer load written straight into LDS: lane l's 16
 // bytes land at lds_base + 16*l (lds_base is wave-uniform, passed in M0).
 //

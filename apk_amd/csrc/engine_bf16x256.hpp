@@ -78,31 +78,40 @@ struct EngBf16x256 {
 
   static __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
 
-  // Issue the direct-to-LDS loads of k-stage `s` of the tile at (row0, col0)
-  // into ring slot `slot`: one 1 KiB piece (16 rows) per wave per load.
+  // Direct-to-LDS loads of one k-stage: load i (0..LOADS-1) fills the
+  // 1 KiB piece i*4 + wave of the A stage (i < 4) or of the Bt stage, i.e.
+  // 16 rows, row 64*i + 16*wave + lane/4, chunk slot lane%4. The swizzle of
+  // a row does not depend on its bit 6, so each lane's offset is fixed per
+  // tile (Lane) and load i and stage s only add scalar offsets.
+  struct Lane {
+    uint32_t a, b;
+  };
+  static __device__ __forceinline__ Lane lane_offsets(const Ctx& c, int row0, int col0) {
+    const int w = wave_id(), l = lane_id();
+    const int r = w * 16 + (l >> 2);
+    const int q = (l & 3) ^ swz(r);
+    return Lane{(uint32_t)(((row0 + r) * c.K + 8 * q) * 2),
+                (uint32_t)(((col0 + r) * c.K + 8 * q) * 2)};
+  }
+  static __device__ __forceinline__ void issue_one(uint32_t ring_lds, const Ctx& c,
+                                                   const Lane& ln, int slot, int s, int i) {
+    const int w = wave_id();
+    const uint32_t stage = ring_lds + (uint32_t)(slot * STAGE);
+    const uint32_t kb = (uint32_t)(s * KS * 2);
+    if (i < LOADS_A)
+      dma_x4(c.ra, stage + (uint32_t)((i * 4 + w) * 1024), ln.a,
+             kb + (uint32_t)(i * 64) * (uint32_t)c.K * 2u);
+    else
+      dma_x4(c.rb, stage + A_STAGE + (uint32_t)(((i - LOADS_A) * 4 + w) * 1024), ln.b,
+             kb + (uint32_t)((i - LOADS_A) * 64) * (uint32_t)c.K * 2u);
+  }
+  // All loads of stage s of the tile at (row0, col0) into ring slot `slot`.
   static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot, int row0,
                                                int col0, int s) {
-    const int w = threadIdx.x >> 6, l = lane_id();
-    const int k0 = s * KS;
-    char* abase = ring + slot * STAGE;
-    char* bbase = abase + A_STAGE;
-    const int r16 = l >> 2, p = l & 3;
+    const Lane ln = lane_offsets(c, row0, col0);
+    const uint32_t rl = lds_addr_of(ring);
 #pragma unroll
-    for (int i = 0; i < LOADS_A; ++i) {
-      const int ci = i * 4 + w;
-      const int r = ci * 16 + r16;
-      const int q = p ^ swz(r);
-      const uint32_t off = (uint32_t)(((row0 + r) * c.K + k0 + 8 * q) * 2);
-      load_lds_x4(c.ra, abase + ci * 1024, off);
-    }
-#pragma unroll
-    for (int i = 0; i < LOADS_B; ++i) {
-      const int ci = i * 4 + w;
-      const int r = ci * 16 + r16;
-      const int q = p ^ swz(r);
-      const uint32_t off = (uint32_t)(((col0 + r) * c.K + k0 + 8 * q) * 2);
-      load_lds_x4(c.rb, bbase + ci * 1024, off);
-    }
+    for (int i = 0; i < LOADS; ++i) issue_one(rl, c, ln, slot, s, i);
   }
 
   // Operands of k-step j (16 k values): one 16-byte read per 32-row block of
@@ -127,40 +136,43 @@ struct EngBf16x256 {
     }
   }
 
-  // One k-stage out of ring slot `slot`; `pre` runs first (returning false
-  // abandons the stage before any accumulator changes), `mid` after the
-  // first k-step's MFMAs are issued.
+  static constexpr int J = KS / 16;  // MFMA k-steps per stage
+
+  // One k-stage out of ring slot `slot`. `pre` runs first (returning false
+  // abandons the stage before any accumulator changes); `mid(i)`, i = 0..
+  // LOADS-1, runs after MFMA 2i+1 of the first k-step -- the stage loops
+  // issue the next stage's direct-to-LDS load i there, one per two MFMAs,
+  // so the loads never hold up the matrix cores.
   template <class Pre, class Mid>
   static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
                                                  Pre&& pre, Mid&& mid) {
     const char* abase = ring + slot * STAGE;
-    constexpr int J = KS / 16;
     Frag f[2];
-    auto step = [&](int j) {
-      if (j + 1 < J) load_frag(abase, j + 1, f[(j + 1) & 1]);
-      const Frag& c = f[j & 1];
-#pragma unroll
-      for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-        for (int cb = 0; cb < 4; ++cb)
-          acc.c[rb][cb] =
-              __builtin_amdgcn_mfma_f32_32x32x16_bf16(c.a[rb], c.b[cb], acc.c[rb][cb], 0, 0, 0);
-    };
     // pre() runs before any operand is in registers: a yield inside it
     // (checkpoint, urgent tiles, restore) then needs only the accumulators
     // live, which keeps the kernel within the register file.
     if (!pre()) return false;
     load_frag(abase, 0, f[0]);
-    step(0);
-    __builtin_amdgcn_sched_barrier(0);
-    mid();
-    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int j = 1; j < J; ++j) step(j);
+    for (int j = 0; j < J; ++j) {
+      if (j + 1 < J) load_frag(abase, j + 1, f[(j + 1) & 1]);
+      const Frag& c = f[j & 1];
+#pragma unroll
+      for (int m = 0; m < 16; ++m) {
+        const int rb = m >> 2, cb = m & 3;
+        acc.c[rb][cb] =
+            __builtin_amdgcn_mfma_f32_32x32x16_bf16(c.a[rb], c.b[cb], acc.c[rb][cb], 0, 0, 0);
+        if (j == 0 && (m & 1) && (m >> 1) < LOADS) {
+          __builtin_amdgcn_sched_barrier(0);
+          mid(m >> 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
     return true;
   }
   static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {
-    compute(ring, slot, acc, [] { return true; }, [] {});
+    compute(ring, slot, acc, [] { return true; }, [](int) {});
   }
 
   // Output element (tile-relative row, col) of accumulator register e.

@@ -9,9 +9,10 @@
 //
 // LDS layouts (bank-conflict-free for the MFMA operand reads):
 //  A stage: 128 rows x 128 B. 16-byte quad q of row r is stored at slot
-//           q ^ aswz(r), aswz(r) = (r ^ (r >> 3)) & 7: 8 (or 16) consecutive
-//           rows reading the same quad hit 8 (16) different 16-byte bank
-//           groups, whether the LDS serves 128 B or 256 B per cycle.
+//           q ^ aswz(r), aswz(r) = (r ^ ((r >> 3) & 1)) & 7: 8 (or 16)
+//           consecutive rows reading the same quad hit 8 (16) different
+//           16-byte bank groups, whether the LDS serves 128 B or 256 B per
+//           cycle.
 //  B stage: 32 rows x 512 B; 16-byte chunk c of row k is stored at slot
 //           c ^ (((k >> 2) & 1) << 3). An operand read is 32 consecutive
 //           dwords of row k for the lower half-wave and of row k+4 for the
@@ -46,7 +47,7 @@ struct EngMfma128 {
     f32x16 c[2][2];
   };
 
-  static __device__ __forceinline__ int aswz(int r) { return (r ^ (r >> 3)) & 7; }
+  static __device__ __forceinline__ int aswz(int r) { return (r ^ ((r >> 3) & 1)) & 7; }
   static __device__ __forceinline__ int bswz(int k) { return ((k >> 2) & 1) << 3; }
 
   struct Ctx {
@@ -73,30 +74,43 @@ struct EngMfma128 {
         for (int r = 0; r < 16; ++r) a.c[i][j][r] = 0.0f;
   }
 
-  // Issue the direct-to-LDS loads of k-stage `s` (k0 = s*KS) of the tile at
-  // (row0, col0) into ring slot `buf`. LOADS instructions per thread.
-  static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot,
-                                               int row0, int col0, int s) {
-    const int w = threadIdx.x >> 6, l = lane_id();
-    const int k0 = s * KS;
-    char* abase = ring + slot * STAGE;
-    char* bbase = abase + A_STAGE;
+  // Direct-to-LDS loads of one k-stage. A load i (< 4) fills the 1 KiB
+  // piece i*4 + wave of the A stage: rows 32*i + 8*wave + lane/8, quad slot
+  // lane%8. B load i fills rows 8*i + 2*wave + lane/32, chunk slot lane%32.
+  // Neither swizzle depends on the row bits that i changes, so each lane's
+  // offset is fixed per tile (Lane) and load i and stage s only add scalar
+  // offsets.
+  struct Lane {
+    uint32_t a, b;
+  };
+  static __device__ __forceinline__ Lane lane_offsets(const Ctx& c, int row0, int col0) {
+    const int w = wave_id(), l = lane_id();
+    const int ra = w * 8 + (l >> 3);
+    const int qa = (l & 7) ^ aswz(ra);
+    const int rb = w * 2 + (l >> 5);
+    const int cq = (l & 31) ^ bswz(rb);
+    return Lane{(uint32_t)(((row0 + ra) * c.K + 4 * qa) * 4),
+                (uint32_t)((rb * c.N + col0 + 4 * cq) * 4)};
+  }
+  static __device__ __forceinline__ void issue_one(uint32_t ring_lds, const Ctx& c,
+                                                   const Lane& ln, int slot, int s, int i) {
+    const int w = wave_id();
+    const uint32_t stage = ring_lds + (uint32_t)(slot * STAGE);
+    const uint32_t k0 = (uint32_t)(s * KS);
+    if (i < LOADS_A)
+      dma_x4(c.ra, stage + (uint32_t)((i * 4 + w) * 1024), ln.a,
+             k0 * 4u + (uint32_t)(i * 32) * (uint32_t)c.K * 4u);
+    else
+      dma_x4(c.rb, stage + A_STAGE + (uint32_t)(((i - LOADS_A) * 4 + w) * 1024), ln.b,
+             (k0 + (uint32_t)((i - LOADS_A) * 8)) * (uint32_t)c.N * 4u);
+  }
+  // All loads of stage s of the tile at (row0, col0) into ring slot `slot`.
+  static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot, int row0,
+                                               int col0, int s) {
+    const Lane ln = lane_offsets(c, row0, col0);
+    const uint32_t rl = lds_addr_of(ring);
 #pragma unroll
-    for (int i = 0; i < LOADS_A; ++i) {
-      const int ci = i * 4 + w;          // 1 KiB piece = 8 rows of 128 B
-      const int r = ci * 8 + (l >> 3);
-      const int q = (l & 7) ^ aswz(r);   // global quad landing in slot l&7
-      const uint32_t off = (uint32_t)(((row0 + r) * c.K + k0 + 4 * q) * 4);
-      load_lds_x4(c.ra, abase + ci * 1024, off);
-    }
-#pragma unroll
-    for (int i = 0; i < LOADS_B; ++i) {
-      const int ci = i * 4 + w;          // 1 KiB piece = 2 rows of 512 B
-      const int r = ci * 2 + (l >> 5);
-      const int cq = (l & 31) ^ bswz(r); // global chunk landing in slot l&31
-      const uint32_t off = (uint32_t)(((k0 + r) * c.N + col0 + 4 * cq) * 4);
-      load_lds_x4(c.rb, bbase + ci * 1024, off);
-    }
+    for (int i = 0; i < LOADS; ++i) issue_one(rl, c, ln, slot, s, i);
   }
 
   // Operands of k-group g (8 k values): one 16-byte A read per 32-row
@@ -128,44 +142,40 @@ struct EngMfma128 {
   }
 
   // One k-stage of MFMAs out of ring slot `slot`. The operands of group g+1
-  // are read from LDS while group g's 16 MFMAs run. Two hooks let the stage
-  // loops fold their per-stage work under it: `pre` runs after the first
-  // group's operand reads are issued (the preempt-flag check: its LDS read
-  // overlaps theirs); if it returns false the stage is abandoned before any
-  // accumulator changes and compute returns false. `mid` runs once the first
-  // group's MFMAs are issued (the next stage's direct-to-LDS loads, issued
-  // while the matrix cores are busy).
+  // are read from LDS while group g's 16 MFMAs run. `pre` runs after the
+  // first group's operand reads are issued (the preempt-flag check: its LDS
+  // read overlaps theirs); if it returns false the stage is abandoned before
+  // any accumulator changes and compute returns false. `mid(i)`, i = 0..
+  // LOADS-1, runs after MFMA 2i+1 of the first group: the stage loops issue
+  // the next stage's direct-to-LDS load i there, under the matrix work.
   template <class Pre, class Mid>
   static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
                                                  Pre&& pre, Mid&& mid) {
     const char* abase = ring + slot * STAGE;
     constexpr int G = KS / 8;
     Frag f[2];
-    auto group = [&](int g) {
+    load_frag(abase, 0, f[0]);
+    if (!pre()) return false;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
       if (g + 1 < G) load_frag(abase, g + 1, f[(g + 1) & 1]);
       const Frag& c = f[g & 1];
 #pragma unroll
-      for (int s = 0; s < 4; ++s)
-#pragma unroll
-        for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb)
-            acc.c[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(
-                c.a4[rb][s], c.bv[cb][s], acc.c[rb][cb], 0, 0, 0);
-    };
-    // Group 0 is peeled so that the hooks sit outside the unrolled loop.
-    load_frag(abase, 0, f[0]);
-    if (!pre()) return false;
-    group(0);
-    __builtin_amdgcn_sched_barrier(0);
-    mid();
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int g = 1; g < G; ++g) group(g);
+      for (int m = 0; m < 16; ++m) {
+        const int s = m >> 2, rb = (m >> 1) & 1, cb = m & 1;
+        acc.c[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(c.a4[rb][s], c.bv[cb][s],
+                                                             acc.c[rb][cb], 0, 0, 0);
+        if (g == 0 && (m & 1) && (m >> 1) < LOADS) {
+          __builtin_amdgcn_sched_barrier(0);
+          mid(m >> 1);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
     return true;
   }
   static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {
-    compute(ring, slot, acc, [] { return true; }, [] {});
+    compute(ring, slot, acc, [] { return true; }, [](int) {});
   }
 
   // Output element (tile-relative row, col) of accumulator register e.

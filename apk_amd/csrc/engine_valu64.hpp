@@ -61,32 +61,46 @@ struct EngValu64 {
 
   static __device__ __forceinline__ int aswz(int r) { return (r >> 2) & 7; }
 
-  static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot,
-                                               int row0, int col0, int s) {
-    const int w = threadIdx.x >> 6, l = lane_id();
-    const int k0 = s * KS;
-    char* abase = ring + slot * STAGE;
-    char* bbase = abase + A_STAGE;
+  // Direct-to-LDS loads of one k-stage. A load i (< 2) fills the 1 KiB
+  // piece i*4 + wave of the A stage: rows 32*i + 8*wave + lane/8, quad slot
+  // lane%8; B load i fills rows 16*i + 4*wave + lane/16. The A swizzle uses
+  // row bits 2-4 only, so each lane's offset is fixed per tile (Lane) and
+  // load i and stage s only add scalar offsets.
+  struct Lane {
+    uint32_t a, b;
+  };
+  static __device__ __forceinline__ Lane lane_offsets(const Ctx& c, int row0, int col0) {
+    const int w = wave_id(), l = lane_id();
+    const int ra = w * 8 + (l >> 3);
+    const int qa = (l & 7) ^ aswz(ra);
+    const int rb = w * 4 + (l >> 4);
+    return Lane{(uint32_t)(((row0 + ra) * c.K + 4 * qa) * 4),
+                (uint32_t)((rb * c.N + col0 + 4 * (l & 15)) * 4)};
+  }
+  static __device__ __forceinline__ void issue_one(uint32_t ring_lds, const Ctx& c,
+                                                   const Lane& ln, int slot, int s, int i) {
+    const int w = wave_id();
+    const uint32_t stage = ring_lds + (uint32_t)(slot * STAGE);
+    const uint32_t k0 = (uint32_t)(s * KS);
+    if (i < LOADS_A)
+      dma_x4(c.ra, stage + (uint32_t)((i * 4 + w) * 1024), ln.a,
+             k0 * 4u + (uint32_t)(i * 32) * (uint32_t)c.K * 4u);
+    else
+      dma_x4(c.rb, stage + A_STAGE + (uint32_t)(((i - LOADS_A) * 4 + w) * 1024), ln.b,
+             (k0 + (uint32_t)((i - LOADS_A) * 16)) * (uint32_t)c.N * 4u);
+  }
+  static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot, int row0,
+                                               int col0, int s) {
+    const Lane ln = lane_offsets(c, row0, col0);
+    const uint32_t rl = lds_addr_of(ring);
 #pragma unroll
-    for (int i = 0; i < LOADS_A; ++i) {
-      const int ci = i * 4 + w;          // 1 KiB piece = 8 rows of 128 B
-      const int r = ci * 8 + (l >> 3);
-      const int q = (l & 7) ^ aswz(r);
-      const uint32_t off = (uint32_t)(((row0 + r) * c.K + k0 + 4 * q) * 4);
-      load_lds_x4(c.ra, abase + ci * 1024, off);
-    }
-#pragma unroll
-    for (int i = 0; i < LOADS_B; ++i) {
-      const int ci = i * 4 + w;          // 1 KiB piece = 4 rows of 256 B
-      const int r = ci * 4 + (l >> 4);
-      const uint32_t off = (uint32_t)(((k0 + r) * c.N + col0 + 4 * (l & 15)) * 4);
-      load_lds_x4(c.rb, bbase + ci * 1024, off);
-    }
+    for (int i = 0; i < LOADS; ++i) issue_one(rl, c, ln, slot, s, i);
   }
 
   // One k-stage out of ring slot `slot`. `pre` runs first (flag check;
   // returning false abandons the stage before any accumulator changes),
-  // `mid` after the first k step (the next stage's direct-to-LDS loads).
+  // `mid(i)` after k step i for i < LOADS (the next stage's direct-to-LDS
+  // load i).
   template <class Pre, class Mid>
   static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
                                                  Pre&& pre, Mid&& mid) {
@@ -108,16 +122,20 @@ struct EngValu64 {
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc.v[i][j] = fmaf(a[i], bb[j], acc.v[i][j]);
     };
-    // k step 0 is peeled so that the hooks sit outside the unrolled loop.
+    // The first LOADS k steps are peeled so that the hooks sit outside the
+    // unrolled loop.
     if (!pre()) return false;
-    step(0);
-    mid();
 #pragma unroll
-    for (int kk = 1; kk < KS; ++kk) step(kk);
+    for (int kk = 0; kk < LOADS; ++kk) {
+      step(kk);
+      mid(kk);
+    }
+#pragma unroll
+    for (int kk = LOADS; kk < KS; ++kk) step(kk);
     return true;
   }
   static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {
-    compute(ring, slot, acc, [] { return true; }, [] {});
+    compute(ring, slot, acc, [] { return true; }, [](int) {});
   }
 
   // Output element (tile-relative row, col) of accumulator register e.

@@ -55,6 +55,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   float* ckslot = P.ckpt ? P.ckpt + (size_t)bid * Ckpt<E>::SLOT_FLOATS : nullptr;
   const bool isSetter = P.flag_set != nullptr && P.sched != nullptr && bid == 0;
 
+  const uint32_t ring_lds = lds_addr_of(ring);
   if (tid < E::NS) flagring[tid] = 0;
   if (P.run_gt && bid == 0 && tid == 0) P.run_gt[0] = wall_ticks();
   __syncthreads();
@@ -104,6 +105,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   // the urgent job needs no registers of its own.
   auto urgent_tile = [&](typename E::Acc& ua, int uidx, int ev) {
     const int ur0 = (uidx / uTilesN) * E::TM, uc0 = (uidx % uTilesN) * E::TN;
+    const typename E::Lane uln = E::lane_offsets(uctx, ur0, uc0);
     E::zero(ua);
     E::issue(ring, uctx, 0, ur0, uc0, 0);
     if (Su > 1) E::issue(ring, uctx, 1, ur0, uc0, 1);
@@ -116,8 +118,8 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
         lds_sync();
       }
       const int ahead = slot_after_next(slot);
-      E::compute(ring, slot, ua, [] { return true; }, [&] {
-        if (t + 2 < Su) E::issue(ring, uctx, ahead, ur0, uc0, t + 2);
+      E::compute(ring, slot, ua, [] { return true; }, [&](int i) {
+        if (t + 2 < Su) E::issue_one(ring_lds, uctx, uln, ahead, t + 2, i);
       });
       slot = next_slot(slot);
     }
@@ -148,6 +150,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     const int tile = (int)(task % (unsigned)totalTiles);
     const int row0 = (tile / tilesN) * E::TM;
     const int col0 = (tile % tilesN) * E::TN;
+    const typename E::Lane ln = E::lane_offsets(ctx, row0, col0);
     typename E::Acc acc;
     E::zero(acc);
     int lastSlot = -1;
@@ -250,8 +253,13 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
       // Stage s+2 (and the sample for a site at s+1) goes out under stage
       // s's matrix work; its slot held stage s-1, which every wave finished
       // before the barrier above.
-      E::compute(ring, slot, acc, at_site, [&] {
-        if (s + 2 <= S) issue_stage(ctx, row0, col0, s + 2, ahead, carry, lastSlot);
+      E::compute(ring, slot, acc, at_site, [&](int i) {
+        if (s + 2 > S) return;
+        if (POLL != APK_POLL_OFF && i == 0 && carry) {
+          sample_flag<SYS>(flag_rsrc, &flagring[ahead]);
+          lastSlot = ahead;
+        }
+        if (s + 2 < S) E::issue_one(ring_lds, ctx, ln, ahead, s + 2, i);
       });
       if (restart) {  // RESTART: the tile starts over from stage 0
         E::zero(acc);

@@ -84,14 +84,16 @@ __device__ __forceinline__ void run_stages(char* ring, const typename E::Ctx& c,
                                            int S, Hook&& hook) {
   E::issue(ring, c, 0, row0, col0, 0);
   if (S > 1) E::issue(ring, c, 1, row0, col0, 1);
+  const typename E::Lane ln = E::lane_offsets(c, row0, col0);
+  const uint32_t rl = lds_addr_of(ring);
   int slot = 0;
   for (int s = 0; s < S; ++s) {
     hook(s);
     wait_landed<E>(s + 1 < S);
     lds_sync();
     const int ahead = slot_after_next(slot);
-    E::compute(ring, slot, acc, [] { return true; }, [&] {
-      if (s + 2 < S) E::issue(ring, c, ahead, row0, col0, s + 2);
+    E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
+      if (s + 2 < S) E::issue_one(rl, c, ln, ahead, s + 2, i);
     });
     slot = next_slot(slot);
   }
