@@ -115,3 +115,51 @@ std::vector<long long> exp_schedule(unsigned seed, double mean_us, int events) {
 }
 
 }  // namespace host
+
+namespace host {
+
+uint16_t bf16_rne(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u && (u & 0x007fffffu)) return 0x7fc0;  // NaN
+  return (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+
+void fill_normal_bf16(unsigned seed, std::vector<float>& A, std::vector<uint16_t>& A_bits,
+                      std::vector<float>& B, std::vector<uint16_t>& B_bits) {
+  std::mt19937 g(seed);
+  const double two_pi = 6.283185307179586476925286766559;
+  bool have = false;
+  double spare = 0.0;
+  auto next = [&]() -> float {
+    if (have) {
+      have = false;
+      return (float)spare;
+    }
+    const double u1 = 1.0 - std::generate_canonical<double, 53>(g);
+    const double u2 = std::generate_canonical<double, 53>(g);
+    const double r = std::sqrt(-2.0 * std::log(u1));
+    spare = r * std::sin(two_pi * u2);
+    have = true;
+    return (float)(r * std::cos(two_pi * u2));
+  };
+  auto fill = [&](std::vector<float>& v, std::vector<uint16_t>& bits) {
+    bits.resize(v.size());
+    for (size_t i = 0; i < v.size(); ++i) {
+      bits[i] = bf16_rne(next());
+      const uint32_t u = (uint32_t)bits[i] << 16;
+      memcpy(&v[i], &u, 4);
+    }
+  };
+  fill(A, A_bits);
+  fill(B, B_bits);
+}
+
+std::vector<uint16_t> transpose_u16(const std::vector<uint16_t>& m, int rows, int cols) {
+  std::vector<uint16_t> t(m.size());
+  for (int r = 0; r < rows; ++r)
+    for (int c = 0; c < cols; ++c) t[(size_t)c * rows + r] = m[(size_t)r * cols + c];
+  return t;
+}
+
+}  // namespace host

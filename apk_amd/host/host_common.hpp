@@ -54,6 +54,23 @@ double percentile(std::vector<double> v, double q);
 // (src/persistent.cu:131-135). glibc treats seed 0 as seed 1.
 void fill_uniform_pm1(unsigned seed, std::vector<float>& A, std::vector<float>& B);
 
+// normal(0,1) values rounded to bf16 (round to nearest even): Box-Muller
+// over std::mt19937(seed) with std::generate_canonical<double, 53> draws
+// (u1 = 1 - u in (0,1], u2 in [0,1)), both outputs of each pair used, A
+// first then B; *_bits gets the bf16 bit patterns, A/B (sized by the caller)
+// the exact float values they encode (what the float64 reference
+// multiplies, as src/tcyield.cu:459-473 does for its fp16 data).
+void fill_normal_bf16(unsigned seed, std::vector<float>& A, std::vector<uint16_t>& A_bits,
+                      std::vector<float>& B, std::vector<uint16_t>& B_bits);
+uint16_t bf16_rne(float x);
+// rows x cols -> cols x rows.
+std::vector<uint16_t> transpose_u16(const std::vector<uint16_t>& m, int rows, int cols);
+template <class T>
+std::vector<uint8_t> as_bytes(const std::vector<T>& v) {
+  const uint8_t* p = reinterpret_cast<const uint8_t*>(v.data());
+  return std::vector<uint8_t>(p, p + v.size() * sizeof(T));
+}
+
 // float64 reference C = A.B (row-major), i-k-j order with double
 // accumulation per element (src/persistent.cu:221-227); rows are split over
 // OpenMP threads, which does not change any element's summation order.

@@ -18,21 +18,26 @@ static T* dalloc(size_t n) {
 YieldRig::YieldRig(const RigShape& s, const std::vector<float>& A,
                    const std::vector<float>& B, const std::vector<float>& Au,
                    const std::vector<float>& Bu)
+    : YieldRig(s, as_bytes(A), as_bytes(B), as_bytes(Au), as_bytes(Bu)) {}
+
+YieldRig::YieldRig(const RigShape& s, const std::vector<uint8_t>& A,
+                   const std::vector<uint8_t>& B, const std::vector<uint8_t>& Au,
+                   const std::vector<uint8_t>& Bu)
     : s_(s) {
   APK_CHECK(apk_engine_geometry_of(s.engine, &geo_));
   U_ = (s.Mu > 0 && s.Nu > 0) ? (s.Mu / geo_.tile_m) * (s.Nu / geo_.tile_n) : 0;
   const int E = s.events > 0 ? s.events : 1;
-  dA_ = dalloc<float>(A.size());
-  dB_ = dalloc<float>(B.size());
+  dA_ = (float*)dalloc<uint8_t>(A.size());
+  dB_ = (float*)dalloc<uint8_t>(B.size());
   dC_ = dalloc<float>((size_t)s.M * s.N);
-  HIP_CHECK(hipMemcpy(dA_, A.data(), A.size() * 4, hipMemcpyHostToDevice));
-  HIP_CHECK(hipMemcpy(dB_, B.data(), B.size() * 4, hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemcpy(dA_, A.data(), A.size(), hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemcpy(dB_, B.data(), B.size(), hipMemcpyHostToDevice));
   if (U_ > 0) {
-    dAu_ = dalloc<float>(Au.size());
-    dBu_ = dalloc<float>(Bu.size());
+    dAu_ = (float*)dalloc<uint8_t>(Au.size());
+    dBu_ = (float*)dalloc<uint8_t>(Bu.size());
     dCu_ = dalloc<float>((size_t)s.Mu * s.Nu * (s.cuPerEvent ? E : 1));
-    HIP_CHECK(hipMemcpy(dAu_, Au.data(), Au.size() * 4, hipMemcpyHostToDevice));
-    HIP_CHECK(hipMemcpy(dBu_, Bu.data(), Bu.size() * 4, hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dAu_, Au.data(), Au.size(), hipMemcpyHostToDevice));
+    HIP_CHECK(hipMemcpy(dBu_, Bu.data(), Bu.size(), hipMemcpyHostToDevice));
   }
   dNext_ = dalloc<unsigned>(APK_QUEUE_WORDS);
   const size_t flagBytes = (size_t)APK_FLAG_MAX_COPIES * APK_FLAG_STRIDE;

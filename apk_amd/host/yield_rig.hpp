@@ -37,6 +37,9 @@ class YieldRig {
  public:
   YieldRig(const RigShape& s, const std::vector<float>& A, const std::vector<float>& B,
            const std::vector<float>& Au, const std::vector<float>& Bu);
+  // Operands as raw bytes in the engine's element type and B layout.
+  YieldRig(const RigShape& s, const std::vector<uint8_t>& A, const std::vector<uint8_t>& B,
+           const std::vector<uint8_t>& Au, const std::vector<uint8_t>& Bu);
   ~YieldRig();
 
   const RigShape& shape() const { return s_; }
