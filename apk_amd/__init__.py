@@ -49,6 +49,7 @@ RESUME_CKPT_FULL, RESUME_CKPT_ACC, RESUME_RESTART = 0, 1, 2
 FLAG_STRIDE, FLAG_MAX_COPIES = 4096, 256
 STATS_PER_BLOCK = 8
 QUEUE_WORDS, QUEUE_XCDS = 16, 8
+SES_PER_XCD, RETREAT_DOMAINS = 4, 32
 
 
 class YieldParams(ctypes.Structure):
@@ -72,6 +73,11 @@ class YieldParams(ctypes.Structure):
         ("exec_count", ctypes.c_void_p), ("u_exec_count", ctypes.c_void_p),
         ("cu_event_stride", ctypes.c_longlong), ("naive", ctypes.c_int),
         ("run_gt", ctypes.c_void_p), ("exit_count", ctypes.c_void_p),
+        ("retreat", ctypes.c_int), ("retreat_count", ctypes.c_void_p),
+        ("retreat_gt", ctypes.c_void_p), ("rq_ctl", ctypes.c_void_p),
+        ("rq_entry", ctypes.c_void_p), ("rq_slots", ctypes.c_void_p),
+        ("rq_capacity", ctypes.c_uint), ("continuation", ctypes.c_int),
+        ("block_base", ctypes.c_int), ("obs_stride", ctypes.c_int),
     ]
 
 
@@ -86,6 +92,7 @@ _SIGNATURES = {
     "apk_persistent_yield": (_I, [_I, _I, _I, ctypes.POINTER(YieldParams), _I, _P]),
     "apk_yield_ckpt_floats": (ctypes.c_longlong, [_I]),
     "apk_persistent_yield_occupancy": (_I, [_I, _I, ctypes.POINTER(_I)]),
+    "apk_raise_flag": (_I, [_P, _I, _I, _P, _P]),
 }
 
 _lib = None
@@ -154,6 +161,12 @@ def yield_occupancy(engine, poll):
 
 def ckpt_floats(engine):
     return int(load().apk_yield_ckpt_floats(engine))
+
+
+def raise_flag(flag, copies, value, set_gt=None, stream=0):
+    """Queue apk_raise_flag on `stream`: store `value` into every flag copy
+    and the device tick into *set_gt. Asynchronous."""
+    check(load().apk_raise_flag(flag, copies, value, set_gt, stream))
 
 
 def persistent_yield(engine, poll, oracle, params, blocks, stream=0):

@@ -35,6 +35,17 @@ __device__ __forceinline__ void atomic_max_u64(unsigned long long* p,
                                                unsigned long long v) {
   __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+__device__ __forceinline__ void atomic_min_i64(long long* p, long long v) {
+  __hip_atomic_fetch_min(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void atomic_max_i64(long long* p, long long v) {
+  __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned cas_u32(unsigned* p, unsigned expected, unsigned desired) {
+  __hip_atomic_compare_exchange_strong(p, &expected, desired, __ATOMIC_RELAXED,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return expected;  // previous value
+}
 
 // ---------------------------------------------------------------------------
 // Timers. wall_ticks() is s_memrealtime: a constant-rate counter shared by
@@ -49,6 +60,11 @@ __device__ __forceinline__ unsigned hw_slot() { return __smid(); }
 // size-1 = 3 << 11 | offset 0 << 6 | 20.
 __device__ __forceinline__ unsigned xcc_id() {
   return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & (APK_QUEUE_XCDS - 1);
+}
+// The shader engine (0..3) of the executing wave inside its XCD: hardware
+// register HW_ID (4), SE_ID bits [14:13] -> size-1 = 1, offset 13.
+__device__ __forceinline__ unsigned se_id() {
+  return __builtin_amdgcn_s_getreg((1 << 11) | (13 << 6) | 4) & (APK_SES_PER_XCD - 1);
 }
 
 // ---------------------------------------------------------------------------

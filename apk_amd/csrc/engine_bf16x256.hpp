@@ -25,9 +25,10 @@
 // output's sum is formed in the same order whatever worker computes it and
 // however often it is checkpointed and resumed.
 //
-// Epilogue: the fp32 tile (256 KiB) does not fit LDS; every lane stores its
-// accumulators straight to C (each store instruction writes two 128-byte row
-// segments) and folds them into the tile fingerprint.
+// Epilogue: the fp32 tile (256 KiB) does not fit the 96 KiB ring, so it is
+// staged in 4 passes of 64 rows (32 rows of each wave row): the waves write
+// one 32x32 accumulator row block each into LDS, then the whole block moves
+// the 64 rows to C with 16-byte coalesced stores (and fingerprints them).
 #pragma once
 #include "device.hpp"
 
@@ -47,7 +48,10 @@ struct EngBf16x256 {
   static constexpr int LOADS = LOADS_A + LOADS_B;
   static constexpr int ACC_PER_THREAD = 256;                // floats
   static constexpr int ELEM_BYTES = 2;                      // bf16 operands
-  static constexpr bool DIRECT_STORE = true;
+  // Epilogue staging: STORE_PASSES passes of PASS_ROWS tile rows through LDS,
+  // row stride STAGE_LD floats (4 floats of padding: the two half-waves write
+  // rows 4 apart, which then fall on different banks).
+  static constexpr int STORE_PASSES = 4, PASS_ROWS = 64, STAGE_LD = TN + 4;
 
   struct Acc {
     f32x16 c[4][4];
@@ -189,32 +193,23 @@ struct EngBf16x256 {
     a.c[e >> 6][(e >> 4) & 3][e & 15] = v;
   }
 
-  // Epilogue straight from the accumulators. The fingerprint (wrapping sum
-  // of mix64(bits + (e << 32)), e = row * TN + col inside the tile; this
-  // thread's part is returned when want_hash) is taken from the values read
-  // back from C, so that no loop ever indexes the accumulators dynamically
-  // (that would move all 256 of them to scratch memory).
-  static __device__ __forceinline__ uint64_t store_direct(const Acc& acc, float* C, int ldc,
-                                                          int row0, int col0, bool want_hash) {
+  // Epilogue pass p: accumulator row block rb = p of every wave into LDS as
+  // rows [wm*32, wm*32+32) of a PASS_ROWS x TN tile (row stride STAGE_LD);
+  // LDS row rr holds tile row pass_row(p, rr).
+  static __device__ __forceinline__ void stage_pass(const Acc& acc, char* lds, int p) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w & 1, wn = w >> 1;
+    float* t = (float*)lds;
 #pragma unroll
-    for (int e = 0; e < ACC_PER_THREAD; ++e) {
-      int r, c;
-      coord(e, r, c);
-      C[(size_t)(row0 + r) * ldc + col0 + c] = get(acc, e);
-    }
-    uint64_t h = 0;
-    if (want_hash) {
-      // A thread's loads after its own stores to the same addresses return
-      // the stored values (program order per address).
-#pragma unroll 4
-      for (int e = 0; e < ACC_PER_THREAD; ++e) {
-        int r, c;
-        coord(e, r, c);
-        const float v = C[(size_t)(row0 + r) * ldc + col0 + c];
-        h += mix64((uint64_t)__float_as_uint(v) + ((uint64_t)(r * TN + c) << 32));
+    for (int cb = 0; cb < 4; ++cb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int rr = wm * 32 + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+        t[rr * STAGE_LD + wn * 128 + cb * 32 + (l & 31)] = acc.c[p][cb][i];
       }
-    }
-    return h;
+  }
+  static __device__ __forceinline__ int pass_row(int p, int rr) {
+    return (rr >> 5) * 128 + p * 32 + (rr & 31);
   }
 };
 

@@ -41,7 +41,8 @@ struct EngMfma128 {
   static constexpr int LOADS = LOADS_A + LOADS_B;           // per stage
   static constexpr int ACC_PER_THREAD = 64;                 // floats
   static constexpr int ELEM_BYTES = 4;                      // fp32 operands
-  static constexpr bool DIRECT_STORE = false;
+  // Epilogue: the whole tile is staged in LDS in one pass (row stride TN).
+  static constexpr int STORE_PASSES = 1, PASS_ROWS = TM, STAGE_LD = TN;
 
   struct Acc {
     f32x16 c[2][2];
@@ -194,7 +195,8 @@ struct EngMfma128 {
 
   // Write the accumulators into LDS as the row-major TM x TN tile (the ring
   // is free once a tile's last stage has been computed).
-  static __device__ __forceinline__ void stage_tile(const Acc& acc, char* lds) {
+  static __device__ __forceinline__ int pass_row(int, int rr) { return rr; }
+  static __device__ __forceinline__ void stage_pass(const Acc& acc, char* lds, int) {
     const int w = threadIdx.x >> 6, l = lane_id();
     const int wm = w & 1, wn = w >> 1;
     const int lr = l & 31, h = l >> 5;

@@ -31,7 +31,8 @@ struct EngValu64 {
   static constexpr int LOADS = LOADS_A + LOADS_B;
   static constexpr int ACC_PER_THREAD = 16;                 // floats
   static constexpr int ELEM_BYTES = 4;                      // fp32 operands
-  static constexpr bool DIRECT_STORE = false;
+  // Epilogue: the whole tile is staged in LDS in one pass (row stride TN).
+  static constexpr int STORE_PASSES = 1, PASS_ROWS = TM, STAGE_LD = TN;
 
   struct Acc {
     float v[4][4];
@@ -152,7 +153,8 @@ struct EngValu64 {
   }
 
   // Write the accumulators into LDS as the row-major TM x TN tile.
-  static __device__ __forceinline__ void stage_tile(const Acc& acc, char* lds) {
+  static __device__ __forceinline__ int pass_row(int, int rr) { return rr; }
+  static __device__ __forceinline__ void stage_pass(const Acc& acc, char* lds, int) {
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
     float* t = (float*)lds;
 #pragma unroll

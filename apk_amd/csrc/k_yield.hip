@@ -16,7 +16,11 @@
 //    continue -- the tile's k order is untouched, so C is bit-identical to an
 //    unpreempted run;
 //  * block 0 optionally acts as the device setter of a pre-scheduled event
-//    train (src/yield.cu:186-195).
+//    train (src/yield.cu:186-195);
+//  * retreat arm: instead of running the urgent job itself, a block that
+//    wins one of the event's `retreat` slots checkpoints its tile into an
+//    HBM resume queue and exits, handing its CU to a kernel queued on
+//    another stream; every worker pops that queue before new tasks.
 // Every branch that contains a barrier is taken on values all threads read
 // from LDS after a barrier (the snapshot discipline of src/midyield.cu:
 // 177-200), so a block never splits across barriers.
@@ -28,11 +32,15 @@
 
 namespace apk {
 
-template <class E, int POLL, bool ORACLE, bool SYS>
+// RETREAT selects the retreat arm (P.retreat > 0) at compile time, so the
+// cooperative instantiations carry none of its code and the retreat ones
+// none of the in-kernel urgent path.
+template <class E, int POLL, bool ORACLE, bool SYS, bool RETREAT>
 __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield_params P) {
   __shared__ __attribute__((aligned(16))) char ring[E::LDS_BYTES];
   __shared__ int flagring[E::NS];  // flag sample issued with stage t: [t % NS]
   __shared__ unsigned s_u32;
+  __shared__ int s_stage, s_kind;
   __shared__ uint64_t s_red[E::THREADS / 64];
 
   const int tid = threadIdx.x, bid = blockIdx.x, G = gridDim.x;
@@ -45,7 +53,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   const int pollStride =
       (POLL == APK_POLL_STAGE) ? 1 : spc * (P.poll_every > 0 ? P.poll_every : 1);
   const int uTilesN = P.Nu > 0 ? P.Nu / E::TN : 1;
-  const int U = (P.Au && P.Mu > 0 && P.Nu > 0) ? (P.Mu / E::TM) * uTilesN : 0;
+  const int U = (!RETREAT && P.Au && P.Mu > 0 && P.Nu > 0) ? (P.Mu / E::TM) * uTilesN : 0;
   const int Su = P.Ku / E::KS;
   const typename E::Ctx ctx = E::make_ctx(P.A, P.B, P.M, P.N, P.K);
   const typename E::Ctx uctx = E::make_ctx(U ? P.Au : P.A, U ? P.Bu : P.B, P.Mu, P.Nu, P.Ku);
@@ -54,6 +62,9 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
       make_rsrc((const char*)P.flag + (size_t)(bid % copies) * APK_FLAG_STRIDE, 4);
   float* ckslot = P.ckpt ? P.ckpt + (size_t)bid * Ckpt<E>::SLOT_FLOATS : nullptr;
   const bool isSetter = P.flag_set != nullptr && P.sched != nullptr && bid == 0;
+  constexpr bool retreatArm = RETREAT && POLL != APK_POLL_OFF;
+  const int row = P.block_base + bid;                 // this block's stats / obs column
+  const int obsStride = P.obs_stride > 0 ? P.obs_stride : G;
 
   const uint32_t ring_lds = lds_addr_of(ring);
   if (tid < E::NS) flagring[tid] = 0;
@@ -62,6 +73,20 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
 
   int lastSeen = 0;     // uniform: every thread derives it from the same samples
   int fLatest = 0;      // freshest landed sample, for the task-boundary stop check
+  if (POLL != APK_POLL_OFF && P.continuation) {
+    // A relaunch joins a running job: generations raised before it started
+    // were handled by the blocks that saw them.
+    if (tid == 0)
+      s_u32 = (unsigned)(SYS ? __hip_atomic_load(P.flag, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_SYSTEM)
+                             : flag_load(P.flag));
+    __syncthreads();
+    const int f0 = (int)uniform(s_u32);
+    __syncthreads();
+    if (f0 < 0) fLatest = f0;
+    else lastSeen = f0 < P.num_events ? f0 : P.num_events;
+  }
+  uint64_t stRetreats = 0, stResumed = 0, stErrors = 0;
   int nextEv = 0;       // setter state (thread 0 of block 0)
   int64_t gBase = 0;
   uint64_t stYields = 0, stSave = 0, stUrgent = 0, stRestore = 0, stInflight = 0;
@@ -141,10 +166,41 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     // loop iterations (lanes 1..63 spinning on a stale task at the barrier
     // below while lane 0 waits outside the loop to pop the next one).
     lds_sync();
-    if (tid == 0) s_u32 = tq.pop(home);
+    // Thread 0 takes the next task: a checkpointed tile from the resume
+    // queue first (retreat arm), else a new task from the work queue.
+    // s_kind: -1 new task; 0 restart from k = 0; 1 resume from the saved
+    // accumulators at stage s_stage; 2 the same plus the saved live stages.
+    if (tid == 0) {
+      unsigned t = 0xffffffffu;
+      int kind = -1, st = 0;
+      if constexpr (retreatArm) {
+        const unsigned tk = rq_pop(P.rq_ctl);
+        if (tk != RQ_NONE) {
+          const int ready = rq_wait_ready(P.rq_entry + (size_t)tk * 4);
+          if (ready > 0) {
+            t = (unsigned)P.rq_entry[(size_t)tk * 4];
+            st = P.rq_entry[(size_t)tk * 4 + 1];
+            kind = ready - 1;
+            s_stage = (int)tk;  // ticket, read below before s_stage is reused
+            ++stResumed;
+          } else {
+            ++stErrors;  // never published within the deadline: the task is lost
+            t = 0xfffffffeu;
+          }
+        }
+      }
+      if (t == 0xffffffffu) t = tq.pop(home);
+      s_u32 = t;
+      s_kind = kind;
+      if (kind < 0) s_stage = 0;
+      else s_red[0] = (uint64_t)(unsigned)s_stage | ((uint64_t)(unsigned)st << 32);
+    }
     __syncthreads();
     const unsigned task = uniform(s_u32);
+    const int kind = uniform(s_kind);
+    const uint64_t tkst = kind >= 0 ? s_red[0] : 0;
     __syncthreads();
+    if (task == 0xfffffffeu) continue;  // lost resume entry (counted)
     if (task >= P.num_tasks) break;
 
     const int tile = (int)(task % (unsigned)totalTiles);
@@ -152,12 +208,35 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     const int col0 = (tile % tilesN) * E::TN;
     const typename E::Lane ln = E::lane_offsets(ctx, row0, col0);
     typename E::Acc acc;
-    E::zero(acc);
     int lastSlot = -1;
-    issue_stage(ctx, row0, col0, 0, 0, false, lastSlot);
-    issue_stage(ctx, row0, col0, 1, 1, true, lastSlot);  // stage 0 is a poll site
-
     int s = 0, slot = 0, toPoll = 0;
+    if (!retreatArm || kind <= 0) {
+      E::zero(acc);
+      issue_stage(ctx, row0, col0, 0, 0, false, lastSlot);
+      issue_stage(ctx, row0, col0, 1, 1, true, lastSlot);  // stage 0 is a poll site
+    } else {
+      // Resume a tile another block checkpointed at stage s: accumulators
+      // hold stages [0, s); stages s, s+1 go to ring slots 0, 1 (from the
+      // checkpoint, or fetched again). The site at s gets a fresh sample.
+      const unsigned tk = uniform((unsigned)(uint32_t)tkst);
+      s = uniform((int)(tkst >> 32));
+      const float* rs = P.rq_slots + (size_t)tk * Ckpt<E>::SLOT_FLOATS;
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      Ckpt<E>::load_acc(acc, rs);
+      const int live = (S - s) < 2 ? (S - s) : 2;
+      if (kind == 2) {
+        Ckpt<E>::load_ring(ring, rs, 0, live);
+        issue_stage(ctx, row0, col0, S, 1, true, lastSlot);  // the sample alone
+        wait_vmcnt<0>();
+        __syncthreads();
+      } else {
+        issue_stage(ctx, row0, col0, s, 0, false, lastSlot);
+        issue_stage(ctx, row0, col0, s + 1, 1, true, lastSlot);
+      }
+      toPoll = POLL == APK_POLL_STAGE ? 0 : (pollStride - s % pollStride) % pollStride;
+    }
+    bool retreated = false;
+
     while (s < S) {
       wait_landed<E>(s + 1 < S);
       lds_sync();
@@ -198,10 +277,55 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
         if (f > P.num_events) f = P.num_events;  // never index past the event arrays
         if (f <= lastSeen) return true;
         const int64_t g = wall_ticks();
-        if (tid == 0)
-          for (int e = lastSeen; e < f; ++e) P.obs_gt[(size_t)e * G + bid] = g;
+        if (tid == 0 && P.obs_gt && row < obsStride)
+          for (int e = lastSeen; e < f; ++e) P.obs_gt[(size_t)e * obsStride + row] = g;
         const int ev = f - 1;
         lastSeen = f;
+        if constexpr (retreatArm) {
+          unsigned tk = RQ_NONE;
+          // The hardware deals a kernel's workgroups round-robin to the XCDs
+          // and their shader engines from wherever its pointers stand, and a
+          // workgroup runs only on a CU of its own shader engine: the urgent
+          // kernel's R workgroups land in R domains the host cannot name, so
+          // free ceil(R / 32) CUs in every (XCD, shader engine) domain.
+          const int quota = (P.retreat + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS;
+          const int dom = home * APK_SES_PER_XCD + (int)se_id();
+          if (tid == 0 &&
+              fetch_add_i32(&P.retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + dom], 1) < quota)
+            tk = rq_reserve(P.rq_ctl, P.rq_capacity);
+          tk = bcast(tk);
+          if (tk == RQ_NONE) return true;  // quota taken (or queue full): keep working
+
+          // ---- retreat: checkpoint into resume entry tk, then exit ----
+          wait_vmcnt<0>();  // always drain: nothing may land in LDS after the block exits
+          lds_sync();
+          const int64_t t0 = wall_ticks();
+          float* rs = P.rq_slots + (size_t)tk * Ckpt<E>::SLOT_FLOATS;
+          const int live = (S - s) < 2 ? (S - s) : 2;
+          int rkind = 0;
+          if (P.resume != APK_RESUME_RESTART) {
+            Ckpt<E>::save_acc(acc, rs);
+            rkind = 1;
+            if (P.resume == APK_RESUME_CKPT_FULL) {
+              Ckpt<E>::save_ring(ring, rs, slot, live);
+              rkind = 2;
+            }
+          }
+          __threadfence();  // this thread's checkpoint stores are visible device-wide
+          __syncthreads();
+          if (tid == 0) {
+            rq_publish(P.rq_entry + (size_t)tk * 4, (int)task, rkind > 0 ? s : 0, rkind, dom);
+            const int64_t t1 = wall_ticks();
+            ++stRetreats;
+            stSave += (uint64_t)(t1 - t0);
+            if (P.retreat_gt) {
+              atomic_min_i64(&P.retreat_gt[2 * (size_t)ev], t0);
+              atomic_max_i64(&P.retreat_gt[2 * (size_t)ev + 1], t1);
+            }
+          }
+          retreated = true;
+          return false;
+        }
         int uidx = U > 0 ? pop_urgent(ev) : U;
         if (uidx >= U) return true;
 
@@ -261,6 +385,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
         }
         if (s + 2 < S) E::issue_one(ring_lds, ctx, ln, ahead, s + 2, i);
       });
+      if (retreated) break;
       if (restart) {  // RESTART: the tile starts over from stage 0
         E::zero(acc);
         s = 0;
@@ -276,6 +401,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
       slot = next_slot(slot);
       ++s;
     }
+    if (retreated) break;  // the block exits; its tile waits in the resume queue
     lds_sync();  // every wave done with the ring; every sample has landed
     if (POLL != APK_POLL_OFF && lastSlot >= 0) fLatest = uniform(flagring[lastSlot]);
 
@@ -290,13 +416,15 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   if (P.run_gt && tid == 0 && fetch_add_u32(P.exit_count, 1u) == (unsigned)G - 1)
     P.run_gt[1] = wall_ticks();
   if (P.stats && tid == 0) {
-    unsigned long long* st = P.stats + (size_t)bid * APK_STATS_PER_BLOCK;
+    unsigned long long* st = P.stats + (size_t)row * APK_STATS_PER_BLOCK;
     st[0] = stYields;
     st[1] = stSave;
     st[2] = stUrgent;
     st[3] = stRestore;
     st[4] = stInflight;
-    st[5] = st[6] = st[7] = 0;
+    st[5] = stRetreats;
+    st[6] = stResumed;
+    st[7] = stErrors;
   }
 }
 
@@ -320,15 +448,30 @@ static int validate(const apk_yield_params* p, int poll, int oracle, int blocks)
     APK_REQUIRE(p->flag != nullptr, "persistent_yield: polling needs a flag");
     APK_REQUIRE(p->flag_copies >= 0 && p->flag_copies <= APK_FLAG_MAX_COPIES,
                 "persistent_yield: flag_copies=%d", p->flag_copies);
-    if (p->num_events > 0)
-      APK_REQUIRE(p->set_gt && p->obs_gt && p->claim && p->claim_site && p->u_gt &&
-                      p->u_end_max && p->uq_next,
-                  "persistent_yield: NULL event array");
     if (p->flag_set) APK_REQUIRE(p->sched != nullptr, "persistent_yield: setter without schedule");
     APK_REQUIRE(p->resume >= APK_RESUME_CKPT_FULL && p->resume <= APK_RESUME_RESTART,
                 "persistent_yield: resume=%d", p->resume);
-    if (p->resume != APK_RESUME_RESTART)
-      APK_REQUIRE(p->ckpt != nullptr, "persistent_yield: checkpointing needs ckpt storage");
+    APK_REQUIRE(p->retreat >= 0, "persistent_yield: retreat=%d", p->retreat);
+    APK_REQUIRE(p->block_base >= 0 && p->obs_stride >= 0,
+                "persistent_yield: block_base=%d obs_stride=%d", p->block_base, p->obs_stride);
+    if (p->retreat > 0) {
+      APK_REQUIRE(p->num_events > 0 && p->retreat_count && p->rq_ctl && p->rq_entry &&
+                      p->rq_capacity > 0,
+                  "persistent_yield: the retreat arm needs events, retreat_count and a resume "
+                  "queue");
+      APK_REQUIRE(p->rq_slots || p->resume == APK_RESUME_RESTART,
+                  "persistent_yield: checkpointing retreats need rq_slots");
+      APK_REQUIRE(p->Au == nullptr, "persistent_yield: the retreat arm runs no urgent job");
+      APK_REQUIRE(p->flag_system == 0, "persistent_yield: the retreat arm polls a device flag");
+    } else {
+      if (p->num_events > 0)
+        APK_REQUIRE(p->set_gt && p->obs_gt && p->claim && p->claim_site && p->u_gt &&
+                        p->u_end_max && p->uq_next,
+                    "persistent_yield: NULL event array");
+      if (p->resume != APK_RESUME_RESTART)
+        APK_REQUIRE(p->ckpt != nullptr, "persistent_yield: checkpointing needs ckpt storage");
+      APK_REQUIRE(p->block_base == 0, "persistent_yield: block_base is for the retreat arm");
+    }
   }
   if (p->Au) {
     APK_REQUIRE(p->Bu && p->Cu && p->Mu > 0 && p->Nu > 0 && p->Ku > 0 &&
@@ -346,9 +489,9 @@ static int validate(const apk_yield_params* p, int poll, int oracle, int blocks)
   return APK_OK;
 }
 
-template <class E, int POLL, bool ORACLE, bool SYS>
+template <class E, int POLL, bool ORACLE, bool SYS, bool RETREAT = false>
 static int launch_t(const apk_yield_params* p, int blocks, hipStream_t st) {
-  hipLaunchKernelGGL((k_persistent_yield<E, POLL, ORACLE, SYS>), dim3(blocks),
+  hipLaunchKernelGGL((k_persistent_yield<E, POLL, ORACLE, SYS, RETREAT>), dim3(blocks),
                      dim3(E::THREADS), 0, st, *p);
   APK_LAUNCHED();
   return APK_OK;
@@ -357,6 +500,11 @@ static int launch_t(const apk_yield_params* p, int blocks, hipStream_t st) {
 template <class E, int POLL>
 static int launch_p(const apk_yield_params* p, int oracle, int blocks, hipStream_t st) {
   const bool sys = p->flag_system != 0;
+  if constexpr (POLL != APK_POLL_OFF) {
+    if (p->retreat > 0)  // device-memory flag only (validated)
+      return oracle ? launch_t<E, POLL, true, false, true>(p, blocks, st)
+                    : launch_t<E, POLL, false, false, true>(p, blocks, st);
+  }
   if (oracle) return sys ? launch_t<E, POLL, true, true>(p, blocks, st)
                          : launch_t<E, POLL, true, false>(p, blocks, st);
   return sys ? launch_t<E, POLL, false, true>(p, blocks, st)
@@ -414,15 +562,15 @@ extern "C" int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_
   };
   int rc;
   switch (engine * 3 + poll) {
-    case 0: rc = q(k_persistent_yield<EngValu64, 0, false, false>, 256); break;
-    case 1: rc = q(k_persistent_yield<EngValu64, 1, false, false>, 256); break;
-    case 2: rc = q(k_persistent_yield<EngValu64, 2, false, false>, 256); break;
-    case 3: rc = q(k_persistent_yield<EngMfma128, 0, false, false>, 256); break;
-    case 4: rc = q(k_persistent_yield<EngMfma128, 1, false, false>, 256); break;
-    case 5: rc = q(k_persistent_yield<EngMfma128, 2, false, false>, 256); break;
-    case 6: rc = q(k_persistent_yield<EngBf16x256, 0, false, false>, 256); break;
-    case 7: rc = q(k_persistent_yield<EngBf16x256, 1, false, false>, 256); break;
-    case 8: rc = q(k_persistent_yield<EngBf16x256, 2, false, false>, 256); break;
+    case 0: rc = q(k_persistent_yield<EngValu64, 0, false, false, false>, 256); break;
+    case 1: rc = q(k_persistent_yield<EngValu64, 1, false, false, false>, 256); break;
+    case 2: rc = q(k_persistent_yield<EngValu64, 2, false, false, false>, 256); break;
+    case 3: rc = q(k_persistent_yield<EngMfma128, 0, false, false, false>, 256); break;
+    case 4: rc = q(k_persistent_yield<EngMfma128, 1, false, false, false>, 256); break;
+    case 5: rc = q(k_persistent_yield<EngMfma128, 2, false, false, false>, 256); break;
+    case 6: rc = q(k_persistent_yield<EngBf16x256, 0, false, false, false>, 256); break;
+    case 7: rc = q(k_persistent_yield<EngBf16x256, 1, false, false, false>, 256); break;
+    case 8: rc = q(k_persistent_yield<EngBf16x256, 2, false, false, false>, 256); break;
     default:
       set_error("occupancy: engine %d poll %d", engine, poll);
       return APK_EINVAL;

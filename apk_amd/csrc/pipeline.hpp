@@ -55,6 +55,61 @@ struct TaskQueue {
 };
 
 // ---------------------------------------------------------------------------
+// Resume queue of the retreat arm: tickets [head, tail) in rq_ctl[0..1],
+// entry t = {task, stage, ready, domain} (ready = checkpoint kind + 1, written
+// last with a release), checkpoint slot t in a separate array. Tickets are
+// never reused within a job (capacity = retreats the job may take), so a
+// producer never waits; a consumer that has claimed ticket h waits for its
+// producer (a resident block on its exit path) with a bounded spin.
+constexpr unsigned RQ_NONE = 0xffffffffu;
+// Longest wait for a claimed entry to be published: 20 ms at the 100 MHz
+// wall clock. A producer publishes within microseconds; running out means a
+// lost task, which the exactly-once counts then report.
+constexpr int64_t RQ_WAIT_TICKS = 2000000;
+
+// Thread-0 only. Claims ticket `tail` unless the job's capacity is used up.
+__device__ __forceinline__ unsigned rq_reserve(unsigned* ctl, unsigned cap) {
+  for (;;) {
+    const unsigned t = __hip_atomic_load(&ctl[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (t >= cap) return RQ_NONE;
+    if (cas_u32(&ctl[1], t, t + 1) == t) return t;
+  }
+}
+// Thread-0 only. Claims the oldest reserved ticket, or RQ_NONE if none.
+__device__ __forceinline__ unsigned rq_pop(unsigned* ctl) {
+  for (;;) {
+    const unsigned h = __hip_atomic_load(&ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const unsigned t = __hip_atomic_load(&ctl[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (h >= t) return RQ_NONE;
+    if (cas_u32(&ctl[0], h, h + 1) == h) return h;
+  }
+}
+// Thread-0 only, after every thread's checkpoint stores were fenced and a
+// barrier: entry fields, then `ready` with release semantics.
+__device__ __forceinline__ void rq_publish(int* en, int task, int stage, int kind,
+                                           int domain) {
+  en[0] = task;
+  en[1] = stage;
+  en[3] = domain;  // where the retreat freed a CU: xcd * 4 + shader engine
+  __threadfence();
+  __hip_atomic_store(&en[2], kind + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Thread-0 only. Waits (bounded) for a claimed entry; returns ready (kind +
+// 1), or 0 if it was not published within RQ_WAIT_TICKS.
+__device__ __forceinline__ int rq_wait_ready(int* en) {
+  const int64_t deadline = wall_ticks() + RQ_WAIT_TICKS;
+  for (;;) {
+    const int r = __hip_atomic_load(&en[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (r != 0) {
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      return r;
+    }
+    if (wall_ticks() > deadline) return 0;
+    __builtin_amdgcn_s_sleep(8);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // The ring protocol of every stage loop here (NS = 3 slots, one barrier per
 // k-stage):
 //   prologue  issue(0), issue(1)
@@ -129,25 +184,26 @@ __device__ __forceinline__ void sample_flag(i32x4 flag_rsrc, int* lds_dst) {
 // not matter, so each thread hashes its own accumulators and the block
 // reduces. The CPU oracle computes the same definition.
 
-// Epilogue through LDS: the tile is staged row-major in LDS, then every
-// thread moves 16-byte pieces to C (coalesced rows) and, when asked, folds
-// them into the fingerprint. Returns the per-thread partial hash. The caller
-// must have finished every read of the ring (lds_sync) before calling.
+// Epilogue through LDS, in E::STORE_PASSES passes: each pass stages
+// E::PASS_ROWS rows of the tile row-major in LDS (row stride E::STAGE_LD
+// floats; LDS row rr is tile row E::pass_row(p, rr)), then every thread moves
+// 16-byte pieces to C (coalesced rows) and, when asked, folds them into the
+// fingerprint. Returns the per-thread partial hash. The caller must have
+// finished every read of the ring (lds_sync) before calling.
 template <class E>
 __device__ __forceinline__ uint64_t store_tile(const typename E::Acc& acc, char* lds,
                                                float* C, int ldc, int row0, int col0,
                                                bool want_hash) {
-  if constexpr (E::DIRECT_STORE) {
-    return E::store_direct(acc, C, ldc, row0, col0, want_hash);
-  } else {
-    E::stage_tile(acc, lds);
+  uint64_t h = 0;
+  constexpr int Q = E::TN / 4;  // float4 per row
+#pragma unroll
+  for (int p = 0; p < E::STORE_PASSES; ++p) {
+    E::stage_pass(acc, lds, p);
     lds_sync();
-    uint64_t h = 0;
-    const float4* t = (const float4*)lds;
-    constexpr int Q = E::TN / 4;  // float4 per row
-    for (int i = threadIdx.x; i < E::TM * Q; i += E::THREADS) {
-      const int r = i / Q, c4 = (i % Q) * 4;
-      const float4 v = t[i];
+    for (int i = threadIdx.x; i < E::PASS_ROWS * Q; i += E::THREADS) {
+      const int rr = i / Q, c4 = (i % Q) * 4;
+      const int r = E::pass_row(p, rr);
+      const float4 v = *(const float4*)((const float*)lds + rr * E::STAGE_LD + c4);
       *(float4*)(C + (size_t)(row0 + r) * ldc + col0 + c4) = v;
       if (want_hash) {
         const uint64_t e = (uint64_t)(r * E::TN + c4);
@@ -157,9 +213,9 @@ __device__ __forceinline__ uint64_t store_tile(const typename E::Acc& acc, char*
         h += mix64((uint64_t)__float_as_uint(v.w) + ((e + 3) << 32));
       }
     }
-    lds_sync();  // LDS reads done before the ring is refilled
-    return h;
+    lds_sync();  // LDS reads done before the next pass or the ring refill
   }
+  return h;
 }
 
 // Sum a per-thread uint64 over the block; valid in thread 0. `red` holds
@@ -194,27 +250,42 @@ struct Ckpt {
 
   // Buffer stores/loads: one lane offset register, the float4 index in the
   // scalar offset, so the checkpoint adds no live address registers.
+  // Both move the accumulators in groups of GROUP float4 per lane with a
+  // scheduling barrier between groups: left free, the scheduler hoists every
+  // accumulator read (or every load) to the top, which needs 4 VGPRs per
+  // float4 at once -- all 256 VGPRs for the bf16 tile -- and spills.
+  static constexpr int NJ = E::ACC_PER_THREAD / 4, GROUP = NJ < 8 ? NJ : 8;
   static __device__ __forceinline__ void save_acc(const typename E::Acc& a, float* slot) {
     const buf_rsrc r = make_buf_rsrc(slot, ACC_FLOATS * 4);
     const int vo = (int)threadIdx.x * 16;
 #pragma unroll
-    for (int j = 0; j < E::ACC_PER_THREAD / 4; ++j) {
-      const float4 v = {E::get(a, 4 * j), E::get(a, 4 * j + 1), E::get(a, 4 * j + 2),
-                        E::get(a, 4 * j + 3)};
-      buf_store_f4(v, r, vo, j * E::THREADS * 16);
+    for (int j0 = 0; j0 < NJ; j0 += GROUP) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = j0; j < j0 + GROUP; ++j) {
+        const float4 v = {E::get(a, 4 * j), E::get(a, 4 * j + 1), E::get(a, 4 * j + 2),
+                          E::get(a, 4 * j + 3)};
+        buf_store_f4(v, r, vo, j * E::THREADS * 16);
+      }
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
   static __device__ __forceinline__ void load_acc(typename E::Acc& a, const float* slot) {
     const buf_rsrc r = make_buf_rsrc(slot, ACC_FLOATS * 4);
     const int vo = (int)threadIdx.x * 16;
 #pragma unroll
-    for (int j = 0; j < E::ACC_PER_THREAD / 4; ++j) {
-      const float4 v = buf_load_f4(r, vo, j * E::THREADS * 16);
-      E::set(a, 4 * j, v.x);
-      E::set(a, 4 * j + 1, v.y);
-      E::set(a, 4 * j + 2, v.z);
-      E::set(a, 4 * j + 3, v.w);
+    for (int j0 = 0; j0 < NJ; j0 += GROUP) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int j = j0; j < j0 + GROUP; ++j) {
+        const float4 v = buf_load_f4(r, vo, j * E::THREADS * 16);
+        E::set(a, 4 * j, v.x);
+        E::set(a, 4 * j + 1, v.y);
+        E::set(a, 4 * j + 2, v.z);
+        E::set(a, 4 * j + 3, v.w);
+      }
     }
+    __builtin_amdgcn_sched_barrier(0);
     // Retire the loads here, on the rare restore path. Otherwise the
     // compiler's wait insertion sees loads still pending into the
     // accumulator registers where the restore path rejoins the stage loop and

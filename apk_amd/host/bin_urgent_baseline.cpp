@@ -24,6 +24,25 @@
 // urgent-blocks tiles of depth --gemm-k, as the reference), --arrival
 // uniform|exp with --mean-gap-us (exponential delays, redrawn until they fall
 // inside the drain), --seed, --verify-rows.
+//
+// --yield 1 is the same experiment with preemption on (the retreat arm): the
+// background polls the flag (--poll stage|chunk, --poll-every), and the
+// urgent stream carries [raise flag -> urgent GEMM -> continuation]. At the
+// flag, ceil(R / 32) blocks in each of the 32 (XCD, shader engine) dispatch
+// domains (R = --retreat, default --urgent-blocks: the urgent kernel's
+// workgroups land in R domains that cannot be named in advance) checkpoint
+// their tile (--resume
+// ckpt|acc|restart) into the HBM resume queue and exit, the urgent GEMM is
+// dispatched onto their CUs, and the continuation relaunches as many workers,
+// which join the job; resumed tiles are finished by whichever worker pops
+// them. Per trial it checks every task's fingerprint against an
+// unpreempted run and (--oracle 1) that every task completed exactly once.
+// CSV columns appended: raise_to_ustart_us (flag raised -> first urgent tile
+// starts, device clock), retreat_first_us, retreat_last_us (flag -> first /
+// last retreating block's checkpoint start / exit), retreats,
+// urgent_block_xcd (per urgent tile: the urgent block that ran it and its XCD),
+// retreat_xcds (the domain xcd*4+se of each retreating block), urgent_end_us, cont_start_us
+// (flag -> last urgent tile done, flag -> continuation's block 0 starts).
 #include <omp.h>
 
 #include <algorithm>
@@ -56,6 +75,22 @@ int main(int argc, char** argv) {
   const double meanGapUs = parse_arg(argc, argv, "--mean-gap-us", 2000);
   const unsigned seed = (unsigned)parse_arg(argc, argv, "--seed", 21);
   const int verifyRows = (int)parse_arg(argc, argv, "--verify-rows", 0);
+  const bool yieldArm = parse_arg(argc, argv, "--yield", 0) != 0;
+  const std::string pollS = parse_str(argc, argv, "--poll", "stage");
+  const int pollEvery = (int)parse_arg(argc, argv, "--poll-every", 1);
+  const std::string resumeS = parse_str(argc, argv, "--resume", "ckpt");
+  const int retreatN = (int)parse_arg(argc, argv, "--retreat", urgentBlocks);
+  const bool oracle = parse_arg(argc, argv, "--oracle", 0) != 0;
+  const int poll = pollS == "stage" ? APK_POLL_STAGE : pollS == "chunk" ? APK_POLL_CHUNK : -1;
+  const int resume = resumeS == "ckpt"      ? APK_RESUME_CKPT_FULL
+                     : resumeS == "acc"     ? APK_RESUME_CKPT_ACC
+                     : resumeS == "restart" ? APK_RESUME_RESTART
+                                            : -1;
+  if (yieldArm && (poll < 0 || resume < 0 || retreatN < 1 || pollEvery < 1)) {
+    fprintf(stderr, "bad --poll (stage|chunk), --resume (ckpt|acc|restart), --retreat or "
+            "--poll-every\n");
+    return 1;
+  }
 
   const int engine = engName == "mfma128" ? APK_ENGINE_MFMA128
                      : engName == "valu64" ? APK_ENGINE_VALU64
@@ -87,7 +122,7 @@ int main(int argc, char** argv) {
 
   const Device dev = device_query();
   int maxPerCU = 0;
-  APK_CHECK(apk_persistent_yield_occupancy(engine, APK_POLL_OFF, &maxPerCU));
+  APK_CHECK(apk_persistent_yield_occupancy(engine, yieldArm ? poll : APK_POLL_OFF, &maxPerCU));
   const int sat = dev.info.cu_count * maxPerCU;
   if (blocks <= 0) {
     if (reserve >= 0) blocks = sat - reserve;
@@ -127,6 +162,16 @@ int main(int argc, char** argv) {
   rs.blocks = blocks;
   rs.events = 1;
   rs.runTimes = true;
+  // Blocks that retreat per event: ceil(R / 32) in each of the 32 (XCD,
+  // shader engine) dispatch domains.
+  const int retreatBlocks =
+      APK_RETREAT_DOMAINS * ((retreatN + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS);
+  if (yieldArm) {
+    rs.retreatCap = (unsigned)retreatBlocks;
+    rs.extraRows = retreatBlocks + blocks;  // continuation + drain relaunch
+    rs.hashTasks = (unsigned)bgTasks;
+    if (oracle) rs.oracleTasks = (unsigned)bgTasks;
+  }
   YieldRig rig(rs, hA, hB, {}, {});
 
   float *dAu, *dBu, *dCu;
@@ -149,8 +194,12 @@ int main(int argc, char** argv) {
   HIP_CHECK(hipStreamCreateWithFlags(&uStream, hipStreamNonBlocking));
 
   auto launch_bg = [&]() {
-    rig.launch(APK_POLL_OFF, 1, APK_RESUME_RESTART, 0, (unsigned)bgTasks, false, 0, false,
-               bgStream);
+    if (yieldArm)
+      rig.launchRetreat(poll, pollEvery, resume, (unsigned)bgTasks, retreatN, 1, oracle, blocks,
+                        0, false, rig.dRunGT(), rig.dExitCount(), bgStream);
+    else
+      rig.launch(APK_POLL_OFF, 1, APK_RESUME_RESTART, 0, (unsigned)bgTasks, false, 0, false,
+                 bgStream);
   };
   auto launch_urgent = [&]() {
     HIP_CHECK(hipMemsetAsync(dUNext, 0, APK_QUEUE_WORDS * sizeof(unsigned), uStream));
@@ -168,6 +217,19 @@ int main(int argc, char** argv) {
       e = std::max<long long>(e, r.end);
     }
     return std::make_pair(s, e);
+  };
+  // Which XCD each urgent tile ran on and which urgent block ran it, as
+  // "block:xcd" pairs in tile order (hw slot bits [9:6] hold the XCC id).
+  auto urgent_placement = [&]() {
+    std::vector<apk_tile_record> rec((size_t)uTiles * uChunks);
+    HIP_CHECK(hipMemcpy(rec.data(), dULog, rec.size() * sizeof(apk_tile_record),
+                        hipMemcpyDeviceToHost));
+    std::string out;
+    for (const auto& r : rec) {
+      if (!out.empty()) out += ' ';
+      out += std::to_string(r.block) + ":" + std::to_string((r.smid >> 6) & 15);
+    }
+    return out;
   };
   const double tickUs = 1.0 / dev.wall_mhz;
 
@@ -213,6 +275,183 @@ int main(int argc, char** argv) {
   const double drainEstUs = (be0 - bs0) * tickUs;
   printf("bg drain, no urgent: %.0f us for %d tasks on %d blocks\n", drainEstUs, bgTasks,
          blocks);
+
+  if (yieldArm) {
+    // --- Retreat arm. Reference fingerprints of every task, unpreempted.
+    const std::vector<unsigned long long> refHash = [&] {
+      rig.reset(false);
+      launch_bg();
+      HIP_CHECK(hipStreamSynchronize(bgStream));
+      return rig.readTaskHash((unsigned)bgTasks);
+    }();
+    const std::vector<float> uRefBits = [&] {
+      std::vector<float> v((size_t)urgentM * urgentN);
+      HIP_CHECK(hipMemcpy(v.data(), dCu, v.size() * 4, hipMemcpyDeviceToHost));
+      return v;
+    }();
+    long long* dRun2;
+    unsigned* dExit2;
+    HIP_CHECK(hipMalloc(&dRun2, 2 * sizeof(long long)));
+    HIP_CHECK(hipMalloc(&dExit2, sizeof(unsigned)));
+    // The continuation goes on a third stream ordered after the urgent GEMM by
+    // an event: on the urgent stream itself the event the host waits for would
+    // only be reported once the continuation (which runs to the end of the
+    // job) had finished as well.
+    hipEvent_t evU;
+    HIP_CHECK(hipEventCreateWithFlags(&evU, hipEventDisableTiming));
+    hipStream_t cStream;
+    HIP_CHECK(hipStreamCreateWithFlags(&cStream, hipStreamNonBlocking));
+    std::mt19937 rng(seed);
+    std::uniform_real_distribution<double> frac(0.2, 0.8);
+    std::exponential_distribution<double> expo(1.0 / std::max(1.0, meanGapUs));
+    struct YRow {
+      double delayUs, e2eUs, execUs, gapUs, drainUs, raiseUs, rFirstUs, rLastUs;
+      double uEndUs, contUs;  // flag -> urgent GEMM end, flag -> continuation start
+      unsigned consumed;
+      int retreats;
+      std::string placement, retreatXcds;
+    };
+    std::vector<YRow> rows;
+    long long hashBad = 0, oracleBad = 0, uBad = 0, lost = 0;
+    int lateDrains = 0, noRetreat = 0;
+    unsigned long long retreats = 0, resumed = 0, errors = 0, saveTicks = 0;
+    for (int t = 0; t < trials; ++t) {
+      rig.reset(false);
+      HIP_CHECK(hipMemset(dRun2, 0, 2 * sizeof(long long)));
+      HIP_CHECK(hipMemset(dExit2, 0, sizeof(unsigned)));
+      HIP_CHECK(hipMemset(dCu, 0xFF, (size_t)urgentM * urgentN * 4));
+      HIP_CHECK(hipDeviceSynchronize());
+      double delayUs;
+      if (arrival == "uniform") {
+        delayUs = frac(rng) * drainEstUs;
+      } else {
+        do delayUs = expo(rng);
+        while (delayUs >= 0.95 * drainEstUs);
+      }
+      const int64_t t0 = now_ns();
+      launch_bg();
+      spin_until_ns(t0 + (int64_t)(delayUs * 1e3));
+      const int64_t tArrive = now_ns();
+      HIP_CHECK(hipMemcpyAsync(hConsumed, rig.dNextTask(), APK_QUEUE_XCDS * sizeof(unsigned),
+                               hipMemcpyDeviceToHost, uStream));
+      APK_CHECK(apk_raise_flag(rig.dFlag(), 1, 1, rig.dSetGT(), uStream));
+      launch_urgent();
+      HIP_CHECK(hipEventRecord(evU, uStream));
+      HIP_CHECK(hipStreamWaitEvent(cStream, evU, 0));
+      rig.launchRetreat(poll, pollEvery, resume, (unsigned)bgTasks, retreatN, 1, oracle,
+                        retreatBlocks, blocks, true, dRun2, dExit2, cStream);
+      HIP_CHECK(hipEventSynchronize(evU));
+      const int64_t tDone = now_ns();
+      HIP_CHECK(hipStreamSynchronize(cStream));
+      HIP_CHECK(hipStreamSynchronize(bgStream));
+      RetreatResult rr = rig.readRetreat(1);
+      if (rr.tail > rr.head) {
+        // A block retreated after the continuation had already drained the
+        // queue: relaunch workers until every checkpointed tile is finished.
+        ++lateDrains;
+        rig.launchRetreat(poll, pollEvery, resume, (unsigned)bgTasks, retreatN, 1, oracle,
+                          blocks, blocks + retreatBlocks, true, nullptr, nullptr, bgStream);
+        HIP_CHECK(hipStreamSynchronize(bgStream));
+        rr = rig.readRetreat(1);
+      }
+      if (rr.tail != rr.head) lost += rr.tail - rr.head;
+      if (rr.tail == 0) ++noRetreat;
+      const EventResult er = rig.readEvents(0);
+      for (int b = 0; b < blocks + retreatBlocks; ++b) {
+        const unsigned long long* st = &er.stats[(size_t)b * APK_STATS_PER_BLOCK];
+        retreats += st[5];
+        resumed += st[6];
+        errors += st[7];
+        saveTicks += st[1];
+      }
+      const std::vector<unsigned long long> h = rig.readTaskHash((unsigned)bgTasks);
+      for (int i = 0; i < bgTasks; ++i) hashBad += h[i] != refHash[i];
+      if (oracle) {
+        const std::vector<int> ex = rig.readExec((unsigned)bgTasks);
+        for (int i = 0; i < bgTasks; ++i) oracleBad += ex[i] != 1;
+      }
+      std::vector<float> hCu((size_t)urgentM * urgentN);
+      HIP_CHECK(hipMemcpy(hCu.data(), dCu, hCu.size() * 4, hipMemcpyDeviceToHost));
+      uBad += memcmp(hCu.data(), uRefBits.data(), hCu.size() * 4) != 0;
+      auto [bS, bE] = rig.readRunGT();
+      long long r2[2];
+      HIP_CHECK(hipMemcpy(r2, dRun2, sizeof r2, hipMemcpyDeviceToHost));
+      const long long bgEnd = std::max(bE, r2[1]);
+      auto [uS, uE] = urgent_window();
+      const long long setGT = rr.setGT[0];
+      unsigned consumed = 0;
+      for (int q = 0; q < APK_QUEUE_XCDS; ++q) consumed += hConsumed[q];
+      const bool any = rr.tail > 0;
+      rows.push_back({delayUs, (tDone - tArrive) / 1e3, (uE - uS) * tickUs, (uS - bgEnd) * tickUs,
+                      (bgEnd - bS) * tickUs, (uS - setGT) * tickUs,
+                      any ? (rr.retreatGT[0] - setGT) * tickUs : -1.0,
+                      any ? (rr.retreatGT[1] - setGT) * tickUs : -1.0,
+                      (uE - setGT) * tickUs, (r2[0] - setGT) * tickUs,
+                      std::min(consumed, (unsigned)bgTasks), (int)rr.tail,
+                      urgent_placement(), [&] {
+                        std::string x;
+                        for (int v : rr.xcd) x += (x.empty() ? "" : " ") + std::to_string(v);
+                        return x;
+                      }()});
+    }
+    std::vector<double> e2e, raise, rFirst, rLast, exec, drain;
+    for (const YRow& r : rows) {
+      e2e.push_back(r.e2eUs);
+      raise.push_back(r.raiseUs);
+      exec.push_back(r.execUs);
+      drain.push_back(r.drainUs);
+      if (r.retreats > 0) {
+        rFirst.push_back(r.rFirstUs);
+        rLast.push_back(r.rLastUs);
+      }
+    }
+    printf("\n--- %s, yield on (retreat arm: poll %s every %d, %d retreats per event, resume "
+           "%s): %d trials ---\n", mode.c_str(), pollS.c_str(), pollEvery, retreatN,
+           resumeS.c_str(), trials);
+    printf("urgent e2e (us):  p50 %.1f | p90 %.1f | p99 %.1f | max %.1f\n",
+           percentile(e2e, 0.50), percentile(e2e, 0.90), percentile(e2e, 0.99),
+           *std::max_element(e2e.begin(), e2e.end()));
+    printf("preempt latency, flag raised -> urgent GEMM starts (us): p50 %.2f | p90 %.2f | "
+           "p99 %.2f | max %.2f\n", percentile(raise, 0.50), percentile(raise, 0.90),
+           percentile(raise, 0.99), *std::max_element(raise.begin(), raise.end()));
+    if (!rFirst.empty())
+      printf("retreat after the flag (us): first checkpoint start p50 %.2f | last exit p50 "
+             "%.2f p99 %.2f\n", percentile(rFirst, 0.5), percentile(rLast, 0.5),
+             percentile(rLast, 0.99));
+    printf("urgent exec (us): p50 %.2f | p99 %.2f\n", percentile(exec, 0.50),
+           percentile(exec, 0.99));
+    printf("bg drain (us):    p50 %.0f (no urgent job: %.0f)\n", percentile(drain, 0.50),
+           drainEstUs);
+    printf("retreats %llu | resumed %llu | save %.2f us per retreat | trials without a "
+           "retreat %d | late drains %d | resume errors %llu | lost %lld\n", retreats, resumed,
+           retreats ? saveTicks * tickUs / retreats : 0.0, noRetreat, lateDrains, errors, lost);
+    printf("SAFETY: %lld of %lld task fingerprints differ from the unpreempted run | urgent "
+           "outputs not bit-identical: %lld of %d\n", hashBad, (long long)trials * bgTasks,
+           uBad, trials);
+    if (oracle)
+      printf("ORACLE: %s (%lld tasks not executed exactly once over %d trials)\n",
+             oracleBad == 0 ? "PASS" : "FAIL", oracleBad, trials);
+    if (csvPath[0]) {
+      FILE* csv = fopen(csvPath, "w");
+      if (csv) {
+        fprintf(csv, "trial,delay_us,consumed_at_arrival,remaining_at_arrival,e2e_us,exec_us,"
+                     "gap_us,drain_us,raise_to_ustart_us,retreat_first_us,retreat_last_us,"
+                     "retreats,urgent_block_xcd,retreat_xcds,urgent_end_us,cont_start_us\n");
+        for (int t = 0; t < trials; ++t)
+          fprintf(csv, "%d,%.1f,%u,%d,%.1f,%.2f,%.1f,%.1f,%.2f,%.2f,%.2f,%d,%s,%s,%.2f,%.2f\n", t,
+                  rows[t].delayUs, rows[t].consumed, bgTasks - (int)rows[t].consumed,
+                  rows[t].e2eUs, rows[t].execUs, rows[t].gapUs, rows[t].drainUs,
+                  rows[t].raiseUs, rows[t].rFirstUs, rows[t].rLastUs, rows[t].retreats,
+                  rows[t].placement.c_str(), rows[t].retreatXcds.c_str(), rows[t].uEndUs,
+                  rows[t].contUs);
+        fclose(csv);
+        printf("raw trial records: %s\n", csvPath);
+      }
+    }
+    const bool pass = hashBad == 0 && uBad == 0 && lost == 0 && errors == 0 && oracleBad == 0;
+    printf("yield: %s\n", pass ? "PASS" : "FAIL");
+    return pass ? 0 : 1;
+  }
 
   // --- Trials.
   std::mt19937 rng(seed);

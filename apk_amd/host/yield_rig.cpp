@@ -59,7 +59,14 @@ YieldRig::YieldRig(const RigShape& s, const std::vector<uint8_t>& A,
   dCkpt_ = dalloc<float>((size_t)s.blocks * apk_yield_ckpt_floats(s.engine));
   if (s.hashTasks) dTaskHash_ = dalloc<unsigned long long>(s.hashTasks);
   if (U_ > 0) dUHash_ = dalloc<unsigned long long>((size_t)E * U_);
-  dStats_ = dalloc<unsigned long long>((size_t)s.blocks * APK_STATS_PER_BLOCK);
+  dStats_ = dalloc<unsigned long long>((size_t)(s.blocks + s.extraRows) * APK_STATS_PER_BLOCK);
+  if (s.retreatCap) {
+    dRetreatCount_ = dalloc<int>((size_t)E * APK_RETREAT_DOMAINS);
+    dRetreatGT_ = dalloc<long long>(2 * (size_t)E);
+    dRqCtl_ = dalloc<unsigned>(2);
+    dRqEntry_ = dalloc<int>((size_t)s.retreatCap * 4);
+    dRqSlots_ = dalloc<float>((size_t)s.retreatCap * apk_yield_ckpt_floats(s.engine));
+  }
   if (s.oracleTasks) {
     dExec_ = dalloc<int>(s.oracleTasks);
     dUExec_ = dalloc<int>(E);
@@ -88,7 +95,8 @@ void YieldRig::reset(bool nanFill) {
   HIP_CHECK(hipMemset(dSite_, 0xFF, E * sizeof(int)));
   HIP_CHECK(hipMemset(dUq_, 0, E * sizeof(int)));
   HIP_CHECK(hipMemset(dUEnd_, 0, E * sizeof(unsigned long long)));
-  HIP_CHECK(hipMemset(dStats_, 0, (size_t)s_.blocks * APK_STATS_PER_BLOCK * 8));
+  HIP_CHECK(hipMemset(dStats_, 0, (size_t)(s_.blocks + s_.extraRows) * APK_STATS_PER_BLOCK * 8));
+  if (s_.retreatCap) resetRetreat();
   if (dTaskHash_) HIP_CHECK(hipMemset(dTaskHash_, 0, (size_t)s_.hashTasks * 8));
   if (dUHash_) HIP_CHECK(hipMemset(dUHash_, 0, (size_t)E * U_ * 8));
   if (dExec_) {
@@ -191,6 +199,88 @@ void YieldRig::launch(int poll, int pollEvery, int resume, int poison, unsigned 
   APK_CHECK(apk_persistent_yield(s_.engine, poll, oracle ? 1 : 0, &p, s_.blocks, stream));
 }
 
+void YieldRig::resetRetreat() {
+  const int E = s_.events > 0 ? s_.events : 1;
+  HIP_CHECK(hipMemset(dRetreatCount_, 0, (size_t)E * APK_RETREAT_DOMAINS * sizeof(int)));
+  std::vector<long long> gt(2 * (size_t)E, 0);
+  for (int e = 0; e < E; ++e) gt[2 * (size_t)e] = INT64_MAX;
+  HIP_CHECK(hipMemcpy(dRetreatGT_, gt.data(), gt.size() * 8, hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemset(dRqCtl_, 0, 2 * sizeof(unsigned)));
+  HIP_CHECK(hipMemset(dRqEntry_, 0, (size_t)s_.retreatCap * 4 * sizeof(int)));
+  HIP_CHECK(hipMemset(dSet_, 0, E * sizeof(long long)));
+}
+
+void YieldRig::launchRetreat(int poll, int pollEvery, int resume, unsigned numTasks,
+                             int retreat, int nEvents, bool oracle, int blocks, int blockBase,
+                             bool continuation, long long* runGT, unsigned* exitCount,
+                             hipStream_t stream) {
+  if (!s_.retreatCap || blockBase + blocks > s_.blocks + s_.extraRows) {
+    fprintf(stderr, "launchRetreat: no resume queue, or stats rows %d..%d beyond %d\n",
+            blockBase, blockBase + blocks, s_.blocks + s_.extraRows);
+    exit(1);
+  }
+  apk_yield_params p;
+  memset(&p, 0, sizeof p);
+  p.A = dA_;
+  p.B = dB_;
+  p.C = dC_;
+  p.M = s_.M;
+  p.N = s_.N;
+  p.K = s_.K;
+  p.k_chunk = s_.kChunk;
+  p.num_tasks = numTasks;
+  p.next_task = dNext_;
+  p.flag = dFlag_;
+  p.flag_copies = s_.flagCopies;
+  p.flag_system = hFlag_ ? 1 : 0;
+  p.num_events = nEvents;
+  p.poll_every = pollEvery;
+  p.resume = resume;
+  p.task_hash = (dTaskHash_ && numTasks <= s_.hashTasks) ? dTaskHash_ : nullptr;
+  p.stats = dStats_;
+  p.run_gt = runGT;
+  p.exit_count = exitCount;
+  if (oracle) {
+    if (!dExec_ || numTasks > s_.oracleTasks) {
+      fprintf(stderr, "oracle launch needs %u task counters (have %u)\n", numTasks,
+              s_.oracleTasks);
+      exit(1);
+    }
+    p.exec_count = dExec_;
+  }
+  p.retreat = retreat;
+  p.retreat_count = dRetreatCount_;
+  p.retreat_gt = dRetreatGT_;
+  p.rq_ctl = dRqCtl_;
+  p.rq_entry = dRqEntry_;
+  p.rq_slots = dRqSlots_;
+  p.rq_capacity = s_.retreatCap;
+  p.continuation = continuation ? 1 : 0;
+  p.block_base = blockBase;
+  APK_CHECK(apk_persistent_yield(s_.engine, poll, oracle ? 1 : 0, &p, blocks, stream));
+}
+
+RetreatResult YieldRig::readRetreat(int nEvents) const {
+  RetreatResult r;
+  const int n = std::max(nEvents, 1);
+  r.setGT.resize(n);
+  r.retreatGT.resize(2 * (size_t)n);
+  r.count.resize((size_t)n * APK_RETREAT_DOMAINS);
+  HIP_CHECK(hipMemcpy(r.setGT.data(), dSet_, n * 8, hipMemcpyDeviceToHost));
+  HIP_CHECK(hipMemcpy(r.retreatGT.data(), dRetreatGT_, 2 * (size_t)n * 8, hipMemcpyDeviceToHost));
+  HIP_CHECK(hipMemcpy(r.count.data(), dRetreatCount_, r.count.size() * sizeof(int),
+                      hipMemcpyDeviceToHost));
+  unsigned ctl[2];
+  HIP_CHECK(hipMemcpy(ctl, dRqCtl_, sizeof ctl, hipMemcpyDeviceToHost));
+  r.head = ctl[0];
+  r.tail = ctl[1];
+  const unsigned n4 = std::min(r.tail, s_.retreatCap);
+  std::vector<int> en((size_t)n4 * 4);
+  if (n4) HIP_CHECK(hipMemcpy(en.data(), dRqEntry_, en.size() * sizeof(int), hipMemcpyDeviceToHost));
+  for (unsigned t = 0; t < n4; ++t) r.xcd.push_back(en[(size_t)t * 4 + 3]);
+  return r;
+}
+
 void YieldRig::hostSetFlag(int v) {
   if (!hFlag_) {
     fprintf(stderr, "hostSetFlag without a host-mapped flag\n");
@@ -217,7 +307,7 @@ EventResult YieldRig::readEvents(int nEvents) const {
   r.site = d2h(dSite_, E);
   r.uEnd = d2h(dUEnd_, E);
   if (dUHash_) r.uHash = d2h(dUHash_, E * U_);
-  r.stats = d2h(dStats_, (size_t)s_.blocks * APK_STATS_PER_BLOCK);
+  r.stats = d2h(dStats_, (size_t)(s_.blocks + s_.extraRows) * APK_STATS_PER_BLOCK);
   return r;
 }
 

@@ -23,6 +23,20 @@ struct RigShape {
   int flagCopies = 1;          // replicas of the flag, APK_FLAG_STRIDE apart
   bool cuPerEvent = false;     // one urgent output per event (CuAll)
   bool runTimes = false;       // record the run's start / last-exit ticks
+  // Retreat arm: resume-queue tickets per job (0 = no retreat arm) and rows
+  // of stats kept for relaunched (continuation) blocks after the first
+  // `blocks` rows.
+  unsigned retreatCap = 0;
+  int extraRows = 0;
+};
+
+// Per-event timeline of the retreat arm (device ticks).
+struct RetreatResult {
+  std::vector<long long> setGT;       // flag raised (apk_raise_flag)
+  std::vector<long long> retreatGT;   // [2e] earliest checkpoint start, [2e+1] latest exit
+  std::vector<int> count;             // [e * 32 + domain] blocks that asked for a retreat slot
+  unsigned head = 0, tail = 0;        // resume tickets popped / reserved
+  std::vector<int> xcd;               // per reserved ticket: domain (xcd * 4 + se) that retreated
 };
 
 struct EventResult {
@@ -61,6 +75,18 @@ class YieldRig {
               bool devSetter, int nEvents, bool oracle, hipStream_t stream,
               long long stopAfterTicks = 0, int naive = 0);
 
+  // Retreat arm: launch `blocks` workers (rows blockBase.. of stats) that
+  // retreat `retreat` blocks per event into the resume queue; continuation
+  // = a relaunch joining the running job. runGT (2 ticks) / exitCount may
+  // be NULL.
+  void launchRetreat(int poll, int pollEvery, int resume, unsigned numTasks, int retreat,
+                     int nEvents, bool oracle, int blocks, int blockBase, bool continuation,
+                     long long* runGT, unsigned* exitCount, hipStream_t stream);
+  // Zero the resume queue and the per-event retreat bookkeeping of a job.
+  void resetRetreat();
+  RetreatResult readRetreat(int nEvents) const;
+  long long* dSetGT() const { return dSet_; }
+
   // Host-mapped flag (host-set mode): relaxed store visible to the GPU.
   void hostSetFlag(int v);
 
@@ -76,6 +102,8 @@ class YieldRig {
   float* dC() const { return dC_; }
   unsigned* dNextTask() const { return dNext_; }
   int* dFlag() const { return dFlag_; }
+  long long* dRunGT() const { return dRunGT_; }
+  unsigned* dExitCount() const { return dExit_; }
 
  private:
   RigShape s_;
@@ -94,6 +122,11 @@ class YieldRig {
   int *dExec_ = nullptr, *dUExec_ = nullptr;
   long long* dRunGT_ = nullptr;
   unsigned* dExit_ = nullptr;
+  int* dRetreatCount_ = nullptr;
+  long long* dRetreatGT_ = nullptr;
+  unsigned* dRqCtl_ = nullptr;
+  int* dRqEntry_ = nullptr;
+  float* dRqSlots_ = nullptr;
 };
 
 // Per-event summary of an observation matrix (src/yield.cu:889-928).

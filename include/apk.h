@@ -144,6 +144,11 @@ enum { APK_POLL_OFF = 0, APK_POLL_CHUNK = 1, APK_POLL_STAGE = 2 };
  * when it is empty. Task u always computes tile u mod (tilesM * tilesN). */
 #define APK_QUEUE_WORDS 16
 #define APK_QUEUE_XCDS 8
+/* Dispatch domains of the retreat arm: a workgroup is dealt round-robin to
+ * one of the 8 XCDs and then to one of its 4 shader engines, and runs only
+ * on a CU of that shader engine. */
+#define APK_SES_PER_XCD 4
+#define APK_RETREAT_DOMAINS 32
 enum { APK_RESUME_CKPT_FULL = 0, APK_RESUME_CKPT_ACC = 1, APK_RESUME_RESTART = 2 };
 
 typedef struct apk_yield_params {
@@ -208,6 +213,36 @@ typedef struct apk_yield_params {
    * 0 at launch */
   long long* run_gt;
   unsigned int* exit_count;
+  /* ---- retreat arm: hand CUs to a kernel queued on another stream ----
+   * retreat = R > 0: the urgent kernel has R workgroups. The hardware deals
+   * a kernel's workgroups round-robin to the XCDs and their shader engines
+   * (APK_RETREAT_DOMAINS in all), starting wherever its pointers stand, and a
+   * workgroup only runs on a CU of its own shader engine. So at a new
+   * generation e the first ceil(R / 32) blocks of EVERY shader engine to see
+   * it (counted in retreat_count[(e-1) * 32 + xcd * 4 + se]; 32 * ceil(R/32)
+   * blocks in all) drain their loads,
+   * checkpoint their tile into the resume queue (per `resume`: accumulators
+   * + live LDS stages, accumulators only, or nothing = restart from k = 0)
+   * and exit, so that the kernel waiting on another stream is dispatched
+   * onto their CUs. Every
+   * worker pops the resume queue before taking a new task, so the tile is
+   * finished by whichever worker (of this launch or of a later relaunch on
+   * any stream) pops its entry; its k order never changes. The urgent job
+   * is not run inside this kernel (Au may be NULL). 0 = cooperative arm. */
+  int retreat;
+  int* retreat_count;            /* [events * APK_RETREAT_DOMAINS], 0 at job start */
+  long long* retreat_gt;         /* [2 * events] or NULL: [2e] earliest checkpoint
+                                    start (host sets INT64_MAX), [2e+1] latest exit (0) */
+  unsigned int* rq_ctl;          /* resume queue tickets: [0] head, [1] tail; 0 at job start */
+  int* rq_entry;                 /* [rq_capacity * 4]: task, stage, ready (kind + 1), the
+                                    retreating block's domain (xcd * 4 + shader engine);
+                                    0 at job start */
+  float* rq_slots;               /* rq_capacity * apk_yield_ckpt_floats(engine) floats */
+  unsigned int rq_capacity;      /* tickets in this job; a retreat beyond it is declined */
+  int continuation;              /* 1: a relaunch joining a running job -- generations
+                                    already raised when it starts are not acted on */
+  int block_base;                /* this launch's first row in obs_gt columns and stats */
+  int obs_stride;                /* obs_gt row length (0 = gridDim); obs_gt may be NULL */
 } apk_yield_params;
 
 /* persistent_yield / persistent_midyield (src/yield.cu:95-204,
@@ -219,6 +254,16 @@ int apk_persistent_yield(int engine, int poll, int oracle,
 /* Floats of checkpoint storage one block needs (accumulators + two LDS
  * stages). */
 long long apk_yield_ckpt_floats(int engine);
+
+/* Raise the generation flag from a stream: one wave stores `value` into
+ * every copy of the flag (agent scope, flag_copies ints APK_FLAG_STRIDE
+ * apart) and, if set_gt is not NULL, its device wall-clock tick into
+ * *set_gt. Queued ahead of an urgent kernel on the urgent stream it is the
+ * "urgent task submitted" signal of the retreat arm: it needs no LDS and few
+ * registers, so it is dispatched beside a fully resident persistent grid.
+ * Replaces the reference's host flag write (cudaMemcpyAsync of the flag on a
+ * control stream, src/yield.cu:845-858). */
+int apk_raise_flag(int* flag, int flag_copies, int value, long long* set_gt, void* stream);
 
 /* Resident blocks per CU of the preemptible kernel. */
 int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_per_cu);

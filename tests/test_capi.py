@@ -115,3 +115,42 @@ def test_python_constants_match_header():
     assert int(defines["APK_FLAG_STRIDE"]) == apk_amd.FLAG_STRIDE
     assert int(defines["APK_FLAG_MAX_COPIES"]) == apk_amd.FLAG_MAX_COPIES
     assert int(defines["APK_STATS_PER_BLOCK"]) == apk_amd.STATS_PER_BLOCK
+    assert int(defines["APK_QUEUE_WORDS"]) == apk_amd.QUEUE_WORDS
+    assert int(defines["APK_QUEUE_XCDS"]) == apk_amd.QUEUE_XCDS
+    assert int(defines["APK_SES_PER_XCD"]) == apk_amd.SES_PER_XCD
+    assert int(defines["APK_RETREAT_DOMAINS"]) == apk_amd.RETREAT_DOMAINS == 32
+
+
+def test_retreat_arm_rejects_bad_args():
+    lib = apk_amd.load()
+    p = apk_amd.YieldParams()
+    fake = 0x1000
+    p.A = p.B = p.C = p.next_task = p.flag = fake
+    p.M, p.N, p.K, p.k_chunk = 128, 128, 64, 32
+    p.resume = apk_amd.RESUME_CKPT_FULL
+    p.retreat = 2
+    call = lambda: lib.apk_persistent_yield(apk_amd.ENGINE_MFMA128, apk_amd.POLL_STAGE, 0,
+                                            ctypes.byref(p), 1, None)
+    assert call() == apk_amd.APK_EINVAL and b"resume queue" in lib.apk_last_error()
+    p.num_events = 1
+    p.retreat_count = p.rq_ctl = p.rq_entry = fake
+    p.rq_capacity = 2
+    assert call() == apk_amd.APK_EINVAL and b"rq_slots" in lib.apk_last_error()
+    p.rq_slots = fake
+    p.Au = fake
+    assert call() == apk_amd.APK_EINVAL and b"no urgent job" in lib.apk_last_error()
+    p.Au = None
+    p.retreat = -1
+    assert call() == apk_amd.APK_EINVAL and b"retreat" in lib.apk_last_error()
+    p.retreat = 0
+    p.num_events = 0
+    p.ckpt = fake
+    p.block_base = 3
+    assert call() == apk_amd.APK_EINVAL and b"block_base" in lib.apk_last_error()
+
+
+def test_raise_flag_rejects_bad_args():
+    lib = apk_amd.load()
+    assert lib.apk_raise_flag(None, 1, 1, None, None) == apk_amd.APK_EINVAL
+    assert lib.apk_raise_flag(ctypes.c_void_p(0x1000), 0, 1, None, None) == apk_amd.APK_EINVAL
+    assert b"flag_copies" in lib.apk_last_error()
