@@ -40,7 +40,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   __shared__ __attribute__((aligned(16))) char ring[E::LDS_BYTES];
   __shared__ int flagring[E::NS];  // flag sample issued with stage t: [t % NS]
   __shared__ unsigned s_u32;
-  __shared__ int s_stage, s_kind;
+  __shared__ int s_i32[3];
   __shared__ uint64_t s_red[E::THREADS / 64];
 
   const int tid = threadIdx.x, bid = blockIdx.x, G = gridDim.x;
@@ -172,16 +172,16 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     // accumulators at stage s_stage; 2 the same plus the saved live stages.
     if (tid == 0) {
       unsigned t = 0xffffffffu;
-      int kind = -1, st = 0;
+      int kind = -1, st = 0, tk = 0;
       if constexpr (retreatArm) {
-        const unsigned tk = rq_pop(P.rq_ctl);
-        if (tk != RQ_NONE) {
-          const int ready = rq_wait_ready(P.rq_entry + (size_t)tk * 4);
+        const unsigned q = rq_pop(P.rq_ctl);
+        if (q != RQ_NONE) {
+          const int ready = rq_wait_ready(P.rq_entry + (size_t)q * 4);
           if (ready > 0) {
-            t = (unsigned)P.rq_entry[(size_t)tk * 4];
-            st = P.rq_entry[(size_t)tk * 4 + 1];
+            t = (unsigned)P.rq_entry[(size_t)q * 4];
+            st = P.rq_entry[(size_t)q * 4 + 1];
             kind = ready - 1;
-            s_stage = (int)tk;  // ticket, read below before s_stage is reused
+            tk = (int)q;
             ++stResumed;
           } else {
             ++stErrors;  // never published within the deadline: the task is lost
@@ -191,14 +191,15 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
       }
       if (t == 0xffffffffu) t = tq.pop(home);
       s_u32 = t;
-      s_kind = kind;
-      if (kind < 0) s_stage = 0;
-      else s_red[0] = (uint64_t)(unsigned)s_stage | ((uint64_t)(unsigned)st << 32);
+      s_i32[0] = kind;
+      s_i32[1] = st;
+      s_i32[2] = tk;
     }
     __syncthreads();
     const unsigned task = uniform(s_u32);
-    const int kind = uniform(s_kind);
-    const uint64_t tkst = kind >= 0 ? s_red[0] : 0;
+    const int kind = uniform(s_i32[0]);
+    const int qStage = uniform(s_i32[1]);
+    const int qTicket = uniform(s_i32[2]);
     __syncthreads();
     if (task == 0xfffffffeu) continue;  // lost resume entry (counted)
     if (task >= P.num_tasks) break;
@@ -209,136 +210,175 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     const typename E::Lane ln = E::lane_offsets(ctx, row0, col0);
     typename E::Acc acc;
     int lastSlot = -1;
-    int s = 0, slot = 0, toPoll = 0;
-    if (!retreatArm || kind <= 0) {
-      E::zero(acc);
-      issue_stage(ctx, row0, col0, 0, 0, false, lastSlot);
-      issue_stage(ctx, row0, col0, 1, 1, true, lastSlot);  // stage 0 is a poll site
-    } else {
-      // Resume a tile another block checkpointed at stage s: accumulators
-      // hold stages [0, s); stages s, s+1 go to ring slots 0, 1 (from the
-      // checkpoint, or fetched again). The site at s gets a fresh sample.
-      const unsigned tk = uniform((unsigned)(uint32_t)tkst);
-      s = uniform((int)(tkst >> 32));
-      const float* rs = P.rq_slots + (size_t)tk * Ckpt<E>::SLOT_FLOATS;
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      Ckpt<E>::load_acc(acc, rs);
-      const int live = (S - s) < 2 ? (S - s) : 2;
-      if (kind == 2) {
-        Ckpt<E>::load_ring(ring, rs, 0, live);
-        issue_stage(ctx, row0, col0, S, 1, true, lastSlot);  // the sample alone
-        wait_vmcnt<0>();
-        __syncthreads();
-      } else {
-        issue_stage(ctx, row0, col0, s, 0, false, lastSlot);
-        issue_stage(ctx, row0, col0, s + 1, 1, true, lastSlot);
-      }
-      toPoll = POLL == APK_POLL_STAGE ? 0 : (pollStride - s % pollStride) % pollStride;
+
+    // The stage loop is (re)entered with the tile's state taken from:
+    //   FRESH   start at k = 0 (new task, or a restart);
+    //   ACC     accumulators from `src`; stages s, s+1 fetched again;
+    //   FULL    accumulators and the two live stages from `src`;
+    //   AS_IS   nothing to do: the loop left at a poll site with its state
+    //           intact (the site found nothing to yield for).
+    // A resume entry of the retreat arm enters once with ACC / FULL. The
+    // stage loop itself only notices a new generation and leaves; the event
+    // log, the setter, the yield decision and the checkpoint all happen
+    // here, outside it, so that none of their state is live in the loop.
+    enum { FRESH = 0, ACC = 1, FULL = 2, AS_IS = 3 };
+    const float* src = nullptr;
+    int s = 0, slot = 0, toPoll = 0, siteDone = -1;
+    int srcKind = FRESH;
+    if (retreatArm && kind > 0) {
+      src = P.rq_slots + (size_t)qTicket * Ckpt<E>::SLOT_FLOATS;
+      s = qStage;
+      srcKind = kind;
     }
     bool retreated = false;
 
-    while (s < S) {
-      wait_landed<E>(s + 1 < S);
-      lds_sync();
-
-      const int ahead = slot_after_next(slot);
-      const bool carry = (toPoll == 1) || (toPoll == 0 && pollStride == 1);  // s+1 is a site
-      const bool site = POLL != APK_POLL_OFF && toPoll == 0;
-      bool restart = false;
-
-      // The site's flag sample (issued in front of stage s+1's loads, so
-      // landed by the wait above) is read under stage s's first operand
-      // reads. Everything past "no new generation" is the rare path: event
-      // log, urgent pop, and the yield itself -- drain, checkpoint, urgent
-      // tiles through the ring, restore. Restored accumulators and ring are
-      // bit-identical to what was saved, so the stage then simply computes
-      // (the operands already read are the same bytes). Only RESTART
-      // abandons the stage.
-      auto at_site = [&]() -> bool {
-        if (!site) return true;
-        int f = uniform(flagring[next_slot(slot)]);
-        fLatest = f;
-        if (f == lastSeen && !isSetter) return true;
-
-        if (isSetter && tid == 0 && f >= 0) {
-          const int64_t now = wall_ticks();
-          if (gBase == 0) gBase = now;
-          if (nextEv < P.num_events) {
-            if (now >= gBase + P.sched[nextEv]) {
-              P.set_gt[nextEv] = now;
-              set_flag(++nextEv);
-            }
-          } else if (P.stop_after > 0 &&
-                     now >= gBase + (P.num_events ? P.sched[P.num_events - 1] : 0) +
-                                P.stop_after) {
-            set_flag(-1);  // self-terminating run: no host in the loop
-          }
-        }
-        if (f > P.num_events) f = P.num_events;  // never index past the event arrays
-        if (f <= lastSeen) return true;
-        const int64_t g = wall_ticks();
-        if (tid == 0 && P.obs_gt && row < obsStride)
-          for (int e = lastSeen; e < f; ++e) P.obs_gt[(size_t)e * obsStride + row] = g;
-        const int ev = f - 1;
-        lastSeen = f;
-        if constexpr (retreatArm) {
-          unsigned tk = RQ_NONE;
-          // The hardware deals a kernel's workgroups round-robin to the XCDs
-          // and their shader engines from wherever its pointers stand, and a
-          // workgroup runs only on a CU of its own shader engine: the urgent
-          // kernel's R workgroups land in R domains the host cannot name, so
-          // free ceil(R / 32) CUs in every (XCD, shader engine) domain.
-          const int quota = (P.retreat + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS;
-          const int dom = home * APK_SES_PER_XCD + (int)se_id();
-          if (tid == 0 &&
-              fetch_add_i32(&P.retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + dom], 1) < quota)
-            tk = rq_reserve(P.rq_ctl, P.rq_capacity);
-          tk = bcast(tk);
-          if (tk == RQ_NONE) return true;  // quota taken (or queue full): keep working
-
-          // ---- retreat: checkpoint into resume entry tk, then exit ----
-          wait_vmcnt<0>();  // always drain: nothing may land in LDS after the block exits
-          lds_sync();
-          const int64_t t0 = wall_ticks();
-          float* rs = P.rq_slots + (size_t)tk * Ckpt<E>::SLOT_FLOATS;
+    for (;;) {  // (re)entries of the stage loop of this tile
+      if (srcKind != AS_IS) {
+        toPoll = POLL == APK_POLL_STAGE ? 0 : (pollStride - s % pollStride) % pollStride;
+        const int64_t tIn = wall_ticks();
+        if (srcKind == FRESH) {
+          E::zero(acc);
+          issue_stage(ctx, row0, col0, s, slot, false, lastSlot);
+          issue_stage(ctx, row0, col0, s + 1, next_slot(slot), true, lastSlot);  // s is a site
+        } else {
+          // Accumulators hold stages [0, s); stages s, s+1 go to ring slots
+          // slot, slot+1 (from the checkpoint, or fetched again), and the
+          // site at s gets a fresh sample.
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+          Ckpt<E>::load_acc(acc, src);
           const int live = (S - s) < 2 ? (S - s) : 2;
-          int rkind = 0;
-          if (P.resume != APK_RESUME_RESTART) {
-            Ckpt<E>::save_acc(acc, rs);
-            rkind = 1;
-            if (P.resume == APK_RESUME_CKPT_FULL) {
-              Ckpt<E>::save_ring(ring, rs, slot, live);
-              rkind = 2;
-            }
+          if (srcKind == FULL) {
+            Ckpt<E>::load_ring(ring, src, slot, live);
+            issue_stage(ctx, row0, col0, S, next_slot(slot), true, lastSlot);  // sample alone
+            wait_vmcnt<0>();
+            __syncthreads();  // restored ring visible to all waves
+          } else {
+            issue_stage(ctx, row0, col0, s, slot, false, lastSlot);
+            issue_stage(ctx, row0, col0, s + 1, next_slot(slot), true, lastSlot);
           }
-          __threadfence();  // this thread's checkpoint stores are visible device-wide
-          __syncthreads();
-          if (tid == 0) {
-            rq_publish(P.rq_entry + (size_t)tk * 4, (int)task, rkind > 0 ? s : 0, rkind, dom);
-            const int64_t t1 = wall_ticks();
-            ++stRetreats;
-            stSave += (uint64_t)(t1 - t0);
-            if (P.retreat_gt) {
-              atomic_min_i64(&P.retreat_gt[2 * (size_t)ev], t0);
-              atomic_max_i64(&P.retreat_gt[2 * (size_t)ev + 1], t1);
-            }
-          }
-          retreated = true;
-          return false;
+          if (tid == 0 && src == ckslot) stRestore += (uint64_t)(wall_ticks() - tIn);
         }
-        int uidx = U > 0 ? pop_urgent(ev) : U;
-        if (uidx >= U) return true;
+      }
 
-        // ---- yield: this block hands its CU to the urgent job ----
-        if (!P.naive) wait_vmcnt<0>();  // drain: stage s+1 has landed
+      bool atSite = false;
+      int fSeen = 0;
+      while (s < S) {
+        wait_landed<E>(s + 1 < S);
         lds_sync();
-        const int64_t t0 = wall_ticks();
-        const int live = (S - s) < 2 ? (S - s) : 2;  // stages s, s+1: resident, not computed
-        if (P.resume != APK_RESUME_RESTART) {
-          Ckpt<E>::save_acc(acc, ckslot);
-          if (P.resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, ckslot, slot, live);
+        // Poll site: the flag sample issued in front of stage s+1's loads has
+        // landed with stage s. A new generation (or the setter's turn) ends
+        // the loop here, before stage s is computed.
+        if (POLL != APK_POLL_OFF && toPoll == 0 && s != siteDone) {
+          const int f = uniform(flagring[next_slot(slot)]);
+          fLatest = f;
+          if (f != lastSeen || isSetter) {
+            fSeen = f;
+            atSite = true;
+            break;
+          }
         }
-        lds_sync();  // ring reads done before the urgent tile overwrites it
+        const int ahead = slot_after_next(slot);
+        const bool carry = (toPoll == 1) || (toPoll == 0 && pollStride == 1);  // s+1 is a site
+        // Stage s+2 (and the sample for a site at s+1) goes out under stage
+        // s's matrix work; its slot held stage s-1, which every wave finished
+        // before the barrier above.
+        E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
+          if (s + 2 > S) return;
+          if (POLL != APK_POLL_OFF && i == 0 && carry) {
+            sample_flag<SYS>(flag_rsrc, &flagring[ahead]);
+            lastSlot = ahead;
+          }
+          if (s + 2 < S) E::issue_one(ring_lds, ctx, ln, ahead, s + 2, i);
+        });
+        toPoll = (toPoll == 0 ? pollStride : toPoll) - 1;
+        slot = next_slot(slot);
+        ++s;
+      }
+      if (!atSite) break;  // the tile is computed
+
+      // ---- poll site s with a new generation (or the setter's turn) ----
+      siteDone = s;
+      int f = fSeen;
+      if (isSetter && tid == 0 && f >= 0) {
+        const int64_t now = wall_ticks();
+        if (gBase == 0) gBase = now;
+        if (nextEv < P.num_events) {
+          if (now >= gBase + P.sched[nextEv]) {
+            P.set_gt[nextEv] = now;
+            set_flag(++nextEv);
+          }
+        } else if (P.stop_after > 0 &&
+                   now >= gBase + (P.num_events ? P.sched[P.num_events - 1] : 0) + P.stop_after) {
+          set_flag(-1);  // self-terminating run: no host in the loop
+        }
+      }
+      if (f > P.num_events) f = P.num_events;  // never index past the event arrays
+      srcKind = AS_IS;
+      if (f <= lastSeen) continue;
+      const int64_t g = wall_ticks();
+      if (tid == 0 && P.obs_gt && row < obsStride)
+        for (int e = lastSeen; e < f; ++e) P.obs_gt[(size_t)e * obsStride + row] = g;
+      const int ev = f - 1;
+      lastSeen = f;
+
+      // Does this block hand over its CU (retreat) or run urgent tiles?
+      float* dst;
+      unsigned tk = RQ_NONE;
+      int uidx = 0;
+      if constexpr (retreatArm) {
+        // The hardware deals a kernel's workgroups round-robin to the XCDs
+        // and their shader engines from wherever its pointers stand, and a
+        // workgroup runs only on a CU of its own shader engine: the urgent
+        // kernel's R workgroups land in R domains the host cannot name, so
+        // free ceil(R / 32) CUs in every (XCD, shader engine) domain.
+        const int quota = (P.retreat + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS;
+        const int dom = home * APK_SES_PER_XCD + (int)se_id();
+        unsigned t = RQ_NONE;
+        if (tid == 0 &&
+            fetch_add_i32(&P.retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + dom], 1) < quota)
+          t = rq_reserve(P.rq_ctl, P.rq_capacity);
+        tk = bcast(t);
+        if (tk == RQ_NONE) continue;  // quota taken (or queue full): keep working
+        dst = P.rq_slots + (size_t)tk * Ckpt<E>::SLOT_FLOATS;
+        wait_vmcnt<0>();  // always drain: nothing may land in LDS after the block exits
+      } else {
+        uidx = U > 0 ? pop_urgent(ev) : U;
+        if (uidx >= U) continue;
+        dst = ckslot;
+        if (!P.naive) wait_vmcnt<0>();  // drain: stage s+1 has landed
+      }
+
+      // ---- checkpoint: accumulators and the live stages s, s+1 ----
+      lds_sync();
+      const int64_t tSave = wall_ticks();
+      const int live = (S - s) < 2 ? (S - s) : 2;  // resident, not computed
+      if (P.resume != APK_RESUME_RESTART) {
+        Ckpt<E>::save_acc(acc, dst);
+        if (P.resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, dst, slot, live);
+      }
+
+      if constexpr (retreatArm) {
+        // ---- retreat: publish resume entry tk and exit, handing the CU on ----
+        const int rkind = P.resume == APK_RESUME_RESTART ? 0
+                          : P.resume == APK_RESUME_CKPT_FULL ? 2 : 1;
+        __threadfence();  // this thread's checkpoint stores are visible device-wide
+        __syncthreads();
+        if (tid == 0) {
+          rq_publish(P.rq_entry + (size_t)tk * 4, (int)task, rkind > 0 ? s : 0, rkind,
+                     home * APK_SES_PER_XCD + (int)se_id());
+          const int64_t t1 = wall_ticks();
+          ++stRetreats;
+          stSave += (uint64_t)(t1 - tSave);
+          if (P.retreat_gt) {
+            atomic_min_i64(&P.retreat_gt[2 * (size_t)ev], tSave);
+            atomic_max_i64(&P.retreat_gt[2 * (size_t)ev + 1], t1);
+          }
+        }
+        retreated = true;
+        break;
+      } else {
+        // ---- cooperative yield: this block runs the event's urgent tiles ----
+        lds_sync();  // ring reads (checkpoint) done before the urgent tiles overwrite it
         const int64_t t1 = wall_ticks();
         if (uidx == 0 && tid == 0) {
           P.claim[ev] = bid + 1;
@@ -355,51 +395,20 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
           P.u_gt[2 * (size_t)ev + 1] = t2;
           ++stYields;
           stInflight += live > 1 ? 1 : 0;  // stage s+1 was issued, not waited for
-          stSave += (uint64_t)(t1 - t0);
+          stSave += (uint64_t)(t1 - tSave);
           stUrgent += (uint64_t)(t2 - t1);
         }
-        if (P.resume == APK_RESUME_RESTART) {
-          restart = true;
-          return false;
-        }
-        Ckpt<E>::load_acc(acc, ckslot);
-        if (P.resume == APK_RESUME_CKPT_FULL) {
-          Ckpt<E>::load_ring(ring, ckslot, slot, live);
+        if (P.resume == APK_RESUME_RESTART) {  // the tile starts over from k = 0
+          srcKind = FRESH;
+          s = 0;
+          slot = 0;
+          siteDone = -1;
         } else {
-          E::issue(ring, ctx, slot, row0, col0, s);
-          if (live > 1) E::issue(ring, ctx, next_slot(slot), row0, col0, s + 1);
-          wait_vmcnt<0>();
+          src = ckslot;
+          srcKind = P.resume == APK_RESUME_CKPT_FULL ? FULL : ACC;
         }
-        __syncthreads();  // restored ring visible to all waves
-        if (tid == 0) stRestore += (uint64_t)(wall_ticks() - t2);
-        return true;
-      };
-      // Stage s+2 (and the sample for a site at s+1) goes out under stage
-      // s's matrix work; its slot held stage s-1, which every wave finished
-      // before the barrier above.
-      E::compute(ring, slot, acc, at_site, [&](int i) {
-        if (s + 2 > S) return;
-        if (POLL != APK_POLL_OFF && i == 0 && carry) {
-          sample_flag<SYS>(flag_rsrc, &flagring[ahead]);
-          lastSlot = ahead;
-        }
-        if (s + 2 < S) E::issue_one(ring_lds, ctx, ln, ahead, s + 2, i);
-      });
-      if (retreated) break;
-      if (restart) {  // RESTART: the tile starts over from stage 0
-        E::zero(acc);
-        s = 0;
-        slot = 0;
-        toPoll = 0;
-        lastSlot = -1;
-        issue_stage(ctx, row0, col0, 0, 0, false, lastSlot);
-        issue_stage(ctx, row0, col0, 1, 1, true, lastSlot);
-        lds_sync();  // reconverge before the back-edge (see the task loop)
-        continue;
+        lds_sync();  // reconverge before re-entering the stage loop
       }
-      toPoll = (toPoll == 0 ? pollStride : toPoll) - 1;
-      slot = next_slot(slot);
-      ++s;
     }
     if (retreated) break;  // the block exits; its tile waits in the resume queue
     lds_sync();  // every wave done with the ring; every sample has landed
