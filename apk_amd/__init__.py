@@ -81,6 +81,19 @@ class YieldParams(ctypes.Structure):
     ]
 
 
+class TinyParams(ctypes.Structure):
+    """Mirror of apk_tiny_params (include/apk.h)."""
+    _fields_ = [
+        ("num_tasks", ctypes.c_uint), ("next_task", ctypes.c_void_p), ("batch", ctypes.c_int),
+        ("A", ctypes.c_void_p), ("Bt", ctypes.c_void_p), ("pa", ctypes.c_int), ("pb", ctypes.c_int),
+        ("exec_count", ctypes.c_void_p), ("checksum", ctypes.c_void_p), ("flag", ctypes.c_void_p),
+        ("sched", ctypes.c_void_p), ("num_events", ctypes.c_int), ("set_gt", ctypes.c_void_p),
+        ("uq_next", ctypes.c_void_p), ("urgent_per_event", ctypes.c_int),
+        ("u_exec_count", ctypes.c_void_p), ("ckpt", ctypes.c_void_p), ("stats", ctypes.c_void_p),
+        ("c_debug", ctypes.c_void_p), ("n_debug", ctypes.c_uint),
+    ]
+
+
 _P = ctypes.c_void_p
 _I = ctypes.c_int
 _SIGNATURES = {
@@ -93,6 +106,7 @@ _SIGNATURES = {
     "apk_yield_ckpt_floats": (ctypes.c_longlong, [_I]),
     "apk_persistent_yield_occupancy": (_I, [_I, _I, ctypes.POINTER(_I)]),
     "apk_raise_flag": (_I, [_P, _I, _I, _P, _P]),
+    "apk_tiny_oracle": (_I, [ctypes.POINTER(TinyParams), _I, _P]),
 }
 
 _lib = None
@@ -173,3 +187,8 @@ def persistent_yield(engine, poll, oracle, params, blocks, stream=0):
     """Launch apk_persistent_yield with a YieldParams. Asynchronous."""
     check(load().apk_persistent_yield(engine, poll, 1 if oracle else 0,
                                       ctypes.byref(params), blocks, stream))
+
+
+def tiny_oracle(params, blocks, stream=0):
+    """Launch apk_tiny_oracle with a TinyParams. Asynchronous."""
+    check(load().apk_tiny_oracle(ctypes.byref(params), blocks, stream))

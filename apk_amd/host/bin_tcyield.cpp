@@ -19,13 +19,18 @@
 // addition is the midyield driver's: --engine, --gemm-k, --resume,
 // --urgent-m/-n/-k, --arrival, --mean-gap-us, --seed, --flag-copies,
 // --verify-rows.
+// --mode tiny runs the scheduler oracle on 1e8 tiny tasks (tiny_oracle.hpp).
 #include "mid_common.hpp"
+#include "tiny_oracle.hpp"
+#include "host_common.hpp"
 
 #include <cstring>
 #include <string>
 #include <vector>
 
 int main(int argc, char** argv) {
+  if (std::strcmp(host::parse_str(argc, argv, "--mode", "events"), "tiny") == 0)
+    return host::run_tiny_oracle(argc, argv);
   // --poll pe (the reference's tile-boundary poll) is midyield's "boundary".
   std::vector<char*> args(argv, argv + argc);
   static char boundary[] = "boundary";

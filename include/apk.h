@@ -269,6 +269,52 @@ int apk_raise_flag(int* flag, int flag_copies, int value, long long* set_gt, voi
 int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_per_cu);
 
 /* ------------------------------------------------------------------------
+ * Scheduler oracle on tiny tasks (the cfg5 exactly-once oracle; the
+ * reference's oracle instantiations count full tiles, src/yield.cu:570-667,
+ * src/tcyield.cu:815-839). Every wave is a worker: it pops `batch` task ids
+ * at a time from APK_QUEUE_WORDS fetch-add counters (one list per XCD,
+ * stealing when its own is empty) and runs each task as one
+ * v_mfma_f32_16x16x16_bf16: task t multiplies A tile t % pa by B tile
+ * (t / pa) % pb (16x16 bf16 each; B tiles passed transposed, N x K). Between
+ * the MFMA and the task's completion the wave checks the generation flag; a
+ * wave that pops an urgent task of a new event saves its accumulator tile to
+ * HBM, runs urgent tasks until the event's mini-queue is empty, restores and
+ * completes. Wave 0 of block 0 raises the events on a device-clock schedule.
+ * Completion: exec_count[t] += 1 and the task's fingerprint
+ * mix64(v + t * 0x9E3779B97F4A7C15) -- v = the wrapping sum over lanes l and
+ * registers j of mix64(bits(C[l][j]) + ((4l + j) << 32)) -- is added to
+ * checksum[0]; urgent task id = e * urgent_per_event + u uses A tile
+ * (7 id + 3) % pa and B tile (13 id + 5) % pb, adds
+ * mix64(v + id * 0x9E3779B97F4A7C15 + 0xD1B54A32D192ED03) to checksum[1] and
+ * u_exec_count[e] += 1. Before a wave exits it checks the flag once more, so
+ * every raised event is served. */
+typedef struct apk_tiny_params {
+  unsigned int num_tasks;
+  unsigned int* next_task;       /* APK_QUEUE_WORDS counters, 0 at launch */
+  int batch;                     /* task ids per pop, >= 1 */
+  const uint16_t* A;             /* pa tiles of 16x16 bf16, row-major (M x K) */
+  const uint16_t* Bt;            /* pb tiles of 16x16 bf16, transposed (N x K) */
+  int pa, pb;
+  int* exec_count;               /* [num_tasks], 0 at launch */
+  unsigned long long* checksum;  /* [2]: background, urgent; 0 at launch */
+  int* flag;                     /* generation flag, 0 at launch */
+  const long long* sched;        /* [num_events] cumulative ticks after the setter's start */
+  int num_events;
+  long long* set_gt;             /* [num_events] */
+  int* uq_next;                  /* [num_events] urgent mini-queue counters, 0 */
+  int urgent_per_event;
+  int* u_exec_count;             /* [num_events], 0 */
+  float* ckpt;                   /* [waves * 256]: one accumulator tile per wave */
+  unsigned long long* stats;     /* [2]: yields, urgent tasks run; 0 at launch */
+  float* c_debug;                /* NULL, or [n_debug * 256]: C of tasks t < n_debug, lane-major */
+  unsigned int n_debug;
+} apk_tiny_params;
+
+/* Launch the tiny-task oracle on `blocks` blocks of 256 threads (4 waves);
+ * blocks * 4 waves need blocks * 4 * 256 floats of ckpt. */
+int apk_tiny_oracle(const apk_tiny_params* params, int blocks, void* stream);
+
+/* ------------------------------------------------------------------------
  * Notification microbenchmark (visibility_poll, src/yield.cu:216-293): every
  * block loops {work_iters dependent FMAs; optionally one 16-byte read of a
  * DRAM-resident traffic buffer; barrier; thread 0 loads its flag copy with a

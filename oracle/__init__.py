@@ -55,6 +55,9 @@ def load():
         "apko_count_tasks": (None, [_P, _I64, _P, _P, _P]),
         "apko_count_events": (_I, [_P, _P, _P, _I, _I, _P, _P, _P]),
         "apko_tile_hash": (ctypes.c_uint64, [_P, _I, _I, _I, _I, _I]),
+        "apko_tiny_tile": (None, [_P, _P, _I, _I, _P]),
+        "apko_tiny_expected": (None, [_P, _P, _I, _I, ctypes.c_uint64, ctypes.c_uint64, _I,
+                                      _P, _P]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -193,3 +196,32 @@ def count_events(set_gt, uexec, claim, urgent_per_event):
 def tile_hash(C, row0, col0, tile_m, tile_n):
     C = np.ascontiguousarray(C, dtype=np.float32)
     return load().apko_tile_hash(_ptr(C), C.shape[1], row0, col0, tile_m, tile_n)
+
+
+def tiny_pool(seed, tiles, lo=-2, hi=2):
+    """`tiles` 16x16 tiles of small-integer bf16 bit patterns (exact in
+    bf16), seeded; returns (bits uint16 [tiles, 256], values float32)."""
+    rng = np.random.default_rng(seed)
+    v = rng.integers(lo, hi + 1, size=(tiles, 256)).astype(np.float32)
+    bits = (v.view(np.uint32) >> 16).astype(np.uint16)
+    return np.ascontiguousarray(bits), v
+
+
+def tiny_tile(A, Bt, ia, ib):
+    """Product of A tile ia and B tile ib (Bt stored N x K) in the device's
+    lane-major register order: out[4 l + j] = C[4 (l // 16) + j][l % 16]."""
+    A = np.ascontiguousarray(A, dtype=np.uint16)
+    Bt = np.ascontiguousarray(Bt, dtype=np.uint16)
+    out = np.empty(256, dtype=np.float32)
+    load().apko_tiny_tile(_ptr(A), _ptr(Bt), ia, ib, _ptr(out))
+    return out
+
+
+def tiny_expected(A, Bt, n, n_urgent, threads=8):
+    """Expected (background, urgent) checksums of the tiny-task oracle."""
+    A = np.ascontiguousarray(A, dtype=np.uint16)
+    Bt = np.ascontiguousarray(Bt, dtype=np.uint16)
+    bg, u = ctypes.c_uint64(), ctypes.c_uint64()
+    load().apko_tiny_expected(_ptr(A), _ptr(Bt), A.shape[0], Bt.shape[0], n, n_urgent,
+                              threads, ctypes.byref(bg), ctypes.byref(u))
+    return bg.value, u.value

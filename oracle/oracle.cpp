@@ -21,6 +21,8 @@
 //   apko_percentile         pinned by brute-force definition on small inputs
 //   apko_count_*            pinned by planted duplicates/misses on the CPU
 //   apko_tile_hash          pinned by bit-flip sensitivity and order invariance
+//   apko_tiny_*             pinned against a plain-Python restatement (small
+//                           pools) and the device's register-order dumps
 #include <algorithm>
 #include <cmath>
 #include <cstdint>
@@ -402,6 +404,81 @@ uint64_t apko_tile_hash(const float* C, int ldc, int row0, int col0,
       h += mix64((uint64_t)bits + (e << 32));
     }
   return h;
+}
+
+// ---------------------------------------------------------------------------
+// Tiny-task scheduler oracle (cfg5: the reference's exactly-once oracle,
+// src/yield.cu:570-667 and src/tcyield.cu:815-839, run on 1e8 16x16x16
+// tasks). A task multiplies a 16x16 bf16 A tile by a 16x16 bf16 B tile; the
+// B tile is stored transposed (Bt, N x K). The device's register order of
+// the 16x16 fp32 result is lane-major: lane l, register j holds
+// C[4 (l / 16) + j][l % 16] -- apko_tiny_tile writes the product in that
+// order, so it can be compared word for word with the device's dump.
+// Operands are small integers, so every product and partial sum is exact in
+// fp32 and the summation order of the matrix core cannot change a bit.
+// Fingerprints (the device computes the same definitions):
+//   v(tile)   = sum over 256 positions p = 4 l + j of mix64(bits + (p << 32))
+//   task t    : A tile t % pa, B tile (t / pa) % pb,
+//               contributes mix64(v + t * 0x9E3779B97F4A7C15)
+//   urgent id : A tile (7 id + 3) % pa, B tile (13 id + 5) % pb,
+//               contributes mix64(v + id * 0x9E3779B97F4A7C15 + 0xD1B54A32D192ED03)
+// Pinned by tests/test_oracle.py against a plain-Python restatement on
+// small pools and, on the GPU, by the device's own dumps and checksums.
+static const uint64_t kTinyGolden = 0x9E3779B97F4A7C15ull;
+static const uint64_t kTinyUrgentSalt = 0xD1B54A32D192ED03ull;
+
+void apko_tiny_tile(const uint16_t* A, const uint16_t* Bt, int ia, int ib, float* out) {
+  const uint16_t* a = A + (size_t)ia * 256;
+  const uint16_t* b = Bt + (size_t)ib * 256;
+  for (int l = 0; l < 64; ++l)
+    for (int j = 0; j < 4; ++j) {
+      const int row = 4 * (l / 16) + j, col = l % 16;
+      float acc = 0.0f;
+      for (int k = 0; k < 16; ++k)
+        acc += apko_bf16_to_f32(a[row * 16 + k]) * apko_bf16_to_f32(b[col * 16 + k]);
+      out[l * 4 + j] = acc;
+    }
+}
+
+static uint64_t tiny_value(const uint16_t* A, const uint16_t* Bt, int ia, int ib) {
+  float c[256];
+  apko_tiny_tile(A, Bt, ia, ib, c);
+  uint64_t v = 0;
+  for (int p = 0; p < 256; ++p) {
+    uint32_t bits;
+    std::memcpy(&bits, &c[p], 4);
+    v += mix64((uint64_t)bits + ((uint64_t)p << 32));
+  }
+  return v;
+}
+
+// Expected background checksum of tasks [0, n) and urgent checksum of ids
+// [0, n_urgent), computed with `threads` threads.
+void apko_tiny_expected(const uint16_t* A, const uint16_t* Bt, int pa, int pb, uint64_t n,
+                        uint64_t n_urgent, int threads, uint64_t* sum_bg, uint64_t* sum_u) {
+  std::vector<uint64_t> V((size_t)pa * pb);
+  for (int ia = 0; ia < pa; ++ia)
+    for (int ib = 0; ib < pb; ++ib) V[(size_t)ib * pa + ia] = tiny_value(A, Bt, ia, ib);
+  if (threads < 1) threads = 1;
+  std::vector<uint64_t> part(threads, 0);
+  std::vector<std::thread> pool;
+  for (int w = 0; w < threads; ++w)
+    pool.emplace_back([&, w] {
+      uint64_t h = 0;
+      const uint64_t lo = n * w / threads, hi = n * (w + 1) / threads;
+      for (uint64_t t = lo; t < hi; ++t)
+        h += mix64(V[(size_t)((t / pa) % pb) * pa + t % pa] + t * kTinyGolden);
+      part[w] = h;
+    });
+  for (auto& th : pool) th.join();
+  uint64_t bg = 0;
+  for (uint64_t h : part) bg += h;
+  uint64_t u = 0;
+  for (uint64_t id = 0; id < n_urgent; ++id)
+    u += mix64(tiny_value(A, Bt, (int)((id * 7 + 3) % pa), (int)((id * 13 + 5) % pb)) +
+               id * kTinyGolden + kTinyUrgentSalt);
+  *sum_bg = bg;
+  *sum_u = u;
 }
 
 }  // extern "C"

@@ -154,3 +154,31 @@ def test_raise_flag_rejects_bad_args():
     assert lib.apk_raise_flag(None, 1, 1, None, None) == apk_amd.APK_EINVAL
     assert lib.apk_raise_flag(ctypes.c_void_p(0x1000), 0, 1, None, None) == apk_amd.APK_EINVAL
     assert b"flag_copies" in lib.apk_last_error()
+
+
+def test_tiny_params_layout_matches_header(tmp_path):
+    src = tmp_path / "tz.c"
+    fields = [f[0] for f in apk_amd.TinyParams._fields_]
+    body = "".join(f'printf("%zu ", offsetof(apk_tiny_params, {f}));' for f in fields)
+    src.write_text('#include <stdio.h>\n#include <stddef.h>\n#include "apk.h"\n'
+                   'int main(){' + body + 'printf("%zu\\n", sizeof(apk_tiny_params));return 0;}\n')
+    exe = tmp_path / "tz"
+    subprocess.check_call(["gcc", "-I", apk_amd.os.path.join(apk_amd.ROOT, "include"),
+                           str(src), "-o", str(exe)])
+    got = [int(x) for x in subprocess.check_output([str(exe)]).split()]
+    want = [getattr(apk_amd.TinyParams, f).offset for f in fields] + [ctypes.sizeof(apk_amd.TinyParams)]
+    assert got == want
+
+
+def test_tiny_oracle_rejects_bad_args():
+    lib = apk_amd.load()
+    p = apk_amd.TinyParams()
+    call = lambda blocks=1: lib.apk_tiny_oracle(ctypes.byref(p), blocks, None)
+    assert call() == apk_amd.APK_EINVAL and b"NULL" in lib.apk_last_error()
+    fake = 0x1000
+    p.next_task = p.A = p.Bt = p.exec_count = p.checksum = p.flag = p.ckpt = fake
+    assert call() == apk_amd.APK_EINVAL and b"batch" in lib.apk_last_error()
+    p.batch, p.pa, p.pb = 1, 4, 4
+    assert call(0) == apk_amd.APK_EINVAL and b"blocks" in lib.apk_last_error()
+    p.num_events = 3
+    assert call() == apk_amd.APK_EINVAL and b"events need" in lib.apk_last_error()

@@ -233,3 +233,56 @@ def test_tile_hash_sensitivity():
     E[0, 0], E[0, 1] = C[0, 1], C[0, 0]    # same multiset, moved
     assert oracle.tile_hash(E, 0, 0, 64, 64) != h
     assert oracle.tile_hash(C, 64, 0, 64, 64) != h  # other tile
+
+
+def _py_mix64(z):
+    M = (1 << 64) - 1
+    z &= M
+    z = ((z ^ (z >> 30)) * 0xbf58476d1ce4e5b9) & M
+    z = ((z ^ (z >> 27)) * 0x94d049bb133111eb) & M
+    return z ^ (z >> 31)
+
+
+def _py_tiny_value(Av, Btv, ia, ib):
+    """Plain-Python restatement: C = A[ia] . B[ib] (Bt stored N x K) from the
+    small-integer values, in lane-major register order, then the positional
+    fingerprint."""
+    a = Av[ia].reshape(16, 16)
+    bt = Btv[ib].reshape(16, 16)
+    C = a.astype(np.int64) @ bt.astype(np.int64).T            # exact integers
+    v = 0
+    for lane in range(64):
+        for j in range(4):
+            x = np.float32(C[4 * (lane // 16) + j][lane % 16])
+            bits = int(x.view(np.uint32))
+            v += _py_mix64(bits + ((4 * lane + j) << 32))
+    return v & ((1 << 64) - 1)
+
+
+def test_tiny_tile_layout_and_values():
+    A, Av = oracle.tiny_pool(1, 3)
+    Bt, Btv = oracle.tiny_pool(2, 2)
+    out = oracle.tiny_tile(A, Bt, 2, 1)
+    C = Av[2].reshape(16, 16) @ Btv[1].reshape(16, 16).T
+    for lane in (0, 5, 17, 33, 63):
+        for j in range(4):
+            assert out[4 * lane + j] == C[4 * (lane // 16) + j][lane % 16]
+    # a transposed operand (the plausible mistake) gives a different tile
+    assert not np.array_equal(out.reshape(64, 4),
+                              (Av[2].reshape(16, 16) @ Btv[1].reshape(16, 16))
+                              [np.arange(4)[None, :] + 4 * (np.arange(64)[:, None] // 16),
+                               np.arange(64)[:, None] % 16])
+
+
+def test_tiny_expected_matches_python_restatement():
+    A, Av = oracle.tiny_pool(3, 3)
+    Bt, Btv = oracle.tiny_pool(4, 2)
+    pa, pb, n, nu = 3, 2, 40, 9
+    G, SALT, M = 0x9E3779B97F4A7C15, 0xD1B54A32D192ED03, (1 << 64) - 1
+    bg = sum(_py_mix64(_py_tiny_value(Av, Btv, t % pa, (t // pa) % pb) + t * G)
+             for t in range(n)) & M
+    u = sum(_py_mix64(_py_tiny_value(Av, Btv, (i * 7 + 3) % pa, (i * 13 + 5) % pb) + i * G + SALT)
+            for i in range(nu)) & M
+    assert oracle.tiny_expected(A, Bt, n, nu, threads=3) == (bg, u)
+    # the sum over tasks is order-free but not task-free: dropping one task changes it
+    assert oracle.tiny_expected(A, Bt, n - 1, nu)[0] != bg
