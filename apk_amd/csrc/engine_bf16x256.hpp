@@ -14,12 +14,13 @@
 // rows x 64 B (16 KiB); 3 stages = 96 KiB of the 160 KiB LDS (1 block/CU).
 //
 // LDS layout (both operands): row r of a stage is 64 B = four 16-byte
-// chunks; chunk q is stored at slot q ^ swz(r), swz(r) = ((r >> 1) ^ (r >> 3))
-// & 3. A 32-row operand read (lanes 0-31 chunk 2j, lanes 32-63 chunk 2j+1)
-// is then conflict-free whether the LDS serves 8 lanes (128 B) or 16 lanes
-// (256 B) of a 16-byte read per cycle: 8 resp. 16 consecutive rows land on
-// distinct bank groups. (With (r >> 1) & 3 alone, rows r and r+8 collide on
-// a 256-byte bank space: half of all LDS-active cycles were conflicts.)
+// chunks; chunk q is stored at slot q ^ swz(r), swz(r) = (r >> 2) & 3. A
+// 32-row operand read (lanes 0-31 chunk 2j, lanes 32-63 chunk 2j+1) then
+// takes the minimum 4 LDS cycles per ds_read_b128 on gfx950: measured with
+// SQ_LDS_BANK_CONFLICT on a probe of this exact access pattern, where
+// ((r >> 1) ^ (r >> 3)) & 3 and (r >> 1) & 3 cost 8 cycles (2-way) and r & 3
+// costs 16; (r >> 2) & 3, (r >> 3) & 3, (r ^ (r >> 2)) & 3 and
+// ((r >> 1) ^ (r >> 2)) & 3 are conflict-free.
 //
 // k order: a k-stage is two MFMA k-steps of 16, in ascending k; every
 // output's sum is formed in the same order whatever worker computes it and
@@ -80,7 +81,7 @@ struct EngBf16x256 {
         for (int r = 0; r < 16; ++r) a.c[i][j][r] = 0.0f;
   }
 
-  static __device__ __forceinline__ int swz(int r) { return ((r >> 1) ^ (r >> 3)) & 3; }
+  static __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
   // Direct-to-LDS loads of one k-stage: load i (0..LOADS-1) fills the
   // 1 KiB piece i*4 + wave of the A stage (i < 4) or of the Bt stage, i.e.
