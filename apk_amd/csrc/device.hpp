@@ -179,6 +179,23 @@ __device__ __forceinline__ void load_lds_x4(i32x4 rsrc, const void* lds_base,
       : "memory");
 }
 
+// The kernel's explicit arguments, read in place in the kernel-argument
+// segment (they start at its offset 0) through a pointer the optimiser cannot
+// see through: loads through it are neither hoisted above the point of use
+// nor merged with earlier ones. Kernels with many parameters read them this
+// way where they are used, so the compiler does not load every parameter at
+// entry and keep them all live in scalar registers (where they spill into
+// vector registers). Taking the address of a by-value kernel parameter
+// instead would copy the whole struct to scratch memory.
+template <class T>
+using KArg = __attribute__((address_space(4))) const T;
+template <class T>
+__device__ __forceinline__ KArg<T>* kernel_args() {
+  KArg<T>* p = (KArg<T>*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return p;
+}
+
 __device__ __forceinline__ int lane_id() { return (int)__lane_id(); }
 
 // A value every lane of the block holds identically (read from LDS after a

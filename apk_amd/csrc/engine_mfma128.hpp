@@ -159,7 +159,11 @@ struct EngMfma128 {
     if (!pre()) return false;
 #pragma unroll
     for (int g = 0; g < G; ++g) {
+      // The reads of group g+1 are issued ahead of group g's 16 MFMAs (the
+      // scheduling barrier keeps the compiler from sinking each read next to
+      // its first use, where the LDS latency would stall the matrix pipe).
       if (g + 1 < G) load_frag(abase, g + 1, f[(g + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
       const Frag& c = f[g & 1];
 #pragma unroll
       for (int m = 0; m < 16; ++m) {

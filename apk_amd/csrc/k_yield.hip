@@ -36,78 +36,74 @@ namespace apk {
 // cooperative instantiations carry none of its code and the retreat ones
 // none of the in-kernel urgent path.
 template <class E, int POLL, bool ORACLE, bool SYS, bool RETREAT>
-__global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield_params P) {
+__global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield_params) {
+  // Every parameter is re-read from the kernel-argument segment where it is
+  // used (P() is opaque to the optimiser), instead of being loaded once at
+  // entry and held in scalar registers for the whole kernel: the stage loop
+  // then keeps its own values in registers without spilling.
+  auto P = [&]() -> const KArg<apk_yield_params>& { return *kernel_args<apk_yield_params>(); };
   __shared__ __attribute__((aligned(16))) char ring[E::LDS_BYTES];
   __shared__ int flagring[E::NS];  // flag sample issued with stage t: [t % NS]
   __shared__ unsigned s_u32;
   __shared__ int s_i32[3];
   __shared__ uint64_t s_red[E::THREADS / 64];
 
-  const int tid = threadIdx.x, bid = blockIdx.x, G = gridDim.x;
-  const int tilesN = P.N / E::TN;
-  const int totalTiles = (P.M / E::TM) * tilesN;
-  const TaskQueue tq(P.next_task, P.M / E::TM, tilesN, P.num_tasks);
-  const int home = (int)xcc_id();
-  const int S = P.K / E::KS;
-  const int spc = P.k_chunk / E::KS;
-  const int pollStride =
-      (POLL == APK_POLL_STAGE) ? 1 : spc * (P.poll_every > 0 ? P.poll_every : 1);
-  const int uTilesN = P.Nu > 0 ? P.Nu / E::TN : 1;
-  const int U = (!RETREAT && P.Au && P.Mu > 0 && P.Nu > 0) ? (P.Mu / E::TM) * uTilesN : 0;
-  const int Su = P.Ku / E::KS;
-  const typename E::Ctx ctx = E::make_ctx(P.A, P.B, P.M, P.N, P.K);
-  const typename E::Ctx uctx = E::make_ctx(U ? P.Au : P.A, U ? P.Bu : P.B, P.Mu, P.Nu, P.Ku);
-  const int copies = P.flag_copies > 0 ? P.flag_copies : 1;
+  // Block-wide counters of thread 0 (yields, times, retreats, ...) and the
+  // setter's state live in LDS: they are touched only off the stage loop.
+  __shared__ unsigned long long s_stats[APK_STATS_PER_BLOCK];
+  __shared__ long long s_setter[2];  // next event, time base
+  __shared__ long long s_serve_t1;   // start of the current service's urgent work
+
+  const int tid = threadIdx.x, bid = blockIdx.x;
+  // Values the stage loop does not need are recomputed from the parameters
+  // where they are used rather than held across it.
+  auto tilesN = [&] { return P().N / E::TN; };
+  auto uTilesN = [&] { return P().Nu > 0 ? P().Nu / E::TN : 1; };
+  auto nU = [&] {
+    return (!RETREAT && P().Au && P().Mu > 0 && P().Nu > 0) ? (P().Mu / E::TM) * uTilesN() : 0;
+  };
+  auto ckslot = [&]() -> float* {
+    return P().ckpt ? P().ckpt + (size_t)bid * Ckpt<E>::SLOT_FLOATS : nullptr;
+  };
+  auto copies = [&] { return P().flag_copies > 0 ? P().flag_copies : 1; };
+  auto row = [&] { return P().block_base + bid; };  // this block's stats / obs column
+  const int pollStride = (POLL == APK_POLL_STAGE)
+                             ? 1
+                             : (P().k_chunk / E::KS) * (P().poll_every > 0 ? P().poll_every : 1);
   const i32x4 flag_rsrc =
-      make_rsrc((const char*)P.flag + (size_t)(bid % copies) * APK_FLAG_STRIDE, 4);
-  float* ckslot = P.ckpt ? P.ckpt + (size_t)bid * Ckpt<E>::SLOT_FLOATS : nullptr;
-  const bool isSetter = P.flag_set != nullptr && P.sched != nullptr && bid == 0;
+      make_rsrc((const char*)P().flag + (size_t)(bid % copies()) * APK_FLAG_STRIDE, 4);
+  const bool isSetter = P().flag_set != nullptr && P().sched != nullptr && bid == 0;
   constexpr bool retreatArm = RETREAT && POLL != APK_POLL_OFF;
-  const int row = P.block_base + bid;                 // this block's stats / obs column
-  const int obsStride = P.obs_stride > 0 ? P.obs_stride : G;
 
   const uint32_t ring_lds = lds_addr_of(ring);
   if (tid < E::NS) flagring[tid] = 0;
-  if (P.run_gt && bid == 0 && tid == 0) P.run_gt[0] = wall_ticks();
+  if (tid < APK_STATS_PER_BLOCK) s_stats[tid] = 0;
+  if (tid < 2) s_setter[tid] = 0;
+  if (P().run_gt && bid == 0 && tid == 0) P().run_gt[0] = wall_ticks();
   __syncthreads();
 
   int lastSeen = 0;     // uniform: every thread derives it from the same samples
   int fLatest = 0;      // freshest landed sample, for the task-boundary stop check
-  if (POLL != APK_POLL_OFF && P.continuation) {
+  if (POLL != APK_POLL_OFF && P().continuation) {
     // A relaunch joins a running job: generations raised before it started
     // were handled by the blocks that saw them.
     if (tid == 0)
-      s_u32 = (unsigned)(SYS ? __hip_atomic_load(P.flag, __ATOMIC_RELAXED,
+      s_u32 = (unsigned)(SYS ? __hip_atomic_load(P().flag, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_SYSTEM)
-                             : flag_load(P.flag));
+                             : flag_load(P().flag));
     __syncthreads();
     const int f0 = (int)uniform(s_u32);
     __syncthreads();
     if (f0 < 0) fLatest = f0;
-    else lastSeen = f0 < P.num_events ? f0 : P.num_events;
+    else lastSeen = f0 < P().num_events ? f0 : P().num_events;
   }
-  uint64_t stRetreats = 0, stResumed = 0, stErrors = 0;
-  int nextEv = 0;       // setter state (thread 0 of block 0)
-  int64_t gBase = 0;
-  uint64_t stYields = 0, stSave = 0, stUrgent = 0, stRestore = 0, stInflight = 0;
+  enum { ST_YIELDS, ST_SAVE, ST_URGENT, ST_RESTORE, ST_INFLIGHT, ST_RETREATS, ST_RESUMED,
+         ST_ERRORS };
+  auto stat = [&](int k, uint64_t v) { s_stats[k] += v; };  // thread 0 only
 
-  // Poll sites are the stages s with s % pollStride == 0, tracked with a
-  // countdown (`toPoll` stages until the next site) rather than divisions.
-  // The sample a site s reads is issued in front of the data loads of stage
-  // s+1, i.e. right behind stage s's own loads, so the ordinary "stage s
-  // landed" wait retires it too. For a site at the tile's last stage the
-  // sample is issued alone, in place of stage S.
-  auto issue_stage = [&](const typename E::Ctx& c, int row0, int col0, int t, int tslot,
-                         bool carry, int& lastSlot) {
-    if (POLL != APK_POLL_OFF && carry) {
-      sample_flag<SYS>(flag_rsrc, &flagring[tslot]);
-      lastSlot = tslot;
-    }
-    if (t < S) E::issue(ring, c, tslot, row0, col0, t);
-  };
   auto set_flag = [&](int v) {
-    for (int c = 0; c < copies; ++c)
-      flag_store((int*)((char*)P.flag_set + (size_t)c * APK_FLAG_STRIDE), v);
+    for (int c = 0, n = copies(); c < n; ++c)
+      flag_store((int*)((char*)P().flag_set + (size_t)c * APK_FLAG_STRIDE), v);
   };
 
   // Broadcast a value thread 0 computed (uniform afterwards).
@@ -121,125 +117,163 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
 
   auto pop_urgent = [&](int ev) -> int {
     unsigned v = 0;
-    if (tid == 0) v = (unsigned)fetch_add_i32(&P.uq_next[ev], 1);
+    if (tid == 0) v = (unsigned)fetch_add_i32(&P().uq_next[ev], 1);
     return (int)bcast(v);
   };
 
-  // One urgent tile through the ring (non-preemptible). `ua` is the
-  // background accumulator, already checkpointed (or to be restarted), so
-  // the urgent job needs no registers of its own.
-  auto urgent_tile = [&](typename E::Acc& ua, int uidx, int ev) {
-    const int ur0 = (uidx / uTilesN) * E::TM, uc0 = (uidx % uTilesN) * E::TN;
-    const typename E::Lane uln = E::lane_offsets(uctx, ur0, uc0);
-    E::zero(ua);
-    E::issue(ring, uctx, 0, ur0, uc0, 0);
-    if (Su > 1) E::issue(ring, uctx, 1, ur0, uc0, 1);
-    int slot = 0;
-    for (int t = 0; t < Su; ++t) {
-      wait_landed<E>(t + 1 < Su);
-      lds_sync();
-      if (P.poison && t == 0) {
-        if (tid == 0) *(float*)(ring + E::A_STAGE) += 1.0f;  // staged B[0][uc0]
-        lds_sync();
-      }
-      const int ahead = slot_after_next(slot);
-      E::compute(ring, slot, ua, [] { return true; }, [&](int i) {
-        if (t + 2 < Su) E::issue_one(ring_lds, uctx, uln, ahead, t + 2, i);
-      });
-      slot = next_slot(slot);
-    }
-    lds_sync();
-    float* cu = P.Cu + (size_t)ev * (size_t)P.cu_event_stride;
-    const uint64_t hp = store_tile<E>(ua, ring, cu, P.Nu, ur0, uc0, P.u_hash != nullptr);
-    if (P.u_hash) {
-      const uint64_t h = block_sum_u64(hp, s_red);
-      if (tid == 0) P.u_hash[(size_t)ev * U + uidx] = h;
-    }
-    if (ORACLE && tid == 0) fetch_add_i32(&P.u_exec_count[ev], 1);
-  };
+  // A job is one output tile through the stage loop below: a background
+  // task (from the resume queue or the work queue), preemptible at poll
+  // sites; or, while the block serves event `serving`, one tile of that
+  // event's urgent GEMM (its own A, B, C and K; not preemptible). A service
+  // ends with the interrupted background tile re-entering from its
+  // checkpoint. Urgent tiles go through the same loop, so the kernel holds
+  // one software pipeline and one epilogue, not two of each.
+  enum { FRESH = 0, ACC = 1, FULL = 2, AS_IS = 3 };
+  int serving = -1;        // event this block serves, or -1
+  int uidx = 0;            // while serving: the urgent tile of the next job
+  unsigned savedTask = 0;  // while serving: the interrupted background task,
+  int savedStage = 0;      // its stage and how it re-enters
+  int savedKind = FRESH;
 
   for (;;) {
-    if (POLL != APK_POLL_OFF && fLatest < 0) break;  // host stop sentinel
+    if (POLL != APK_POLL_OFF && serving < 0 && fLatest < 0) break;  // host stop sentinel
     // Reconverge before the thread-0 pop: without a barrier here the
     // compiler may thread the previous iteration's thread-0 regions into
     // this one across the back-edge and split the block's lanes over two
     // loop iterations (lanes 1..63 spinning on a stale task at the barrier
     // below while lane 0 waits outside the loop to pop the next one).
     lds_sync();
-    // Thread 0 takes the next task: a checkpointed tile from the resume
-    // queue first (retreat arm), else a new task from the work queue.
-    // s_kind: -1 new task; 0 restart from k = 0; 1 resume from the saved
-    // accumulators at stage s_stage; 2 the same plus the saved live stages.
-    if (tid == 0) {
-      unsigned t = 0xffffffffu;
-      int kind = -1, st = 0, tk = 0;
-      if constexpr (retreatArm) {
-        const unsigned q = rq_pop(P.rq_ctl);
-        if (q != RQ_NONE) {
-          const int ready = rq_wait_ready(P.rq_entry + (size_t)q * 4);
-          if (ready > 0) {
-            t = (unsigned)P.rq_entry[(size_t)q * 4];
-            st = P.rq_entry[(size_t)q * 4 + 1];
-            kind = ready - 1;
-            tk = (int)q;
-            ++stResumed;
-          } else {
-            ++stErrors;  // never published within the deadline: the task is lost
-            t = 0xfffffffeu;
-          }
-        }
-      }
-      if (t == 0xffffffffu) t = tq.pop(home);
-      s_u32 = t;
-      s_i32[0] = kind;
-      s_i32[1] = st;
-      s_i32[2] = tk;
-    }
-    __syncthreads();
-    const unsigned task = uniform(s_u32);
-    const int kind = uniform(s_i32[0]);
-    const int qStage = uniform(s_i32[1]);
-    const int qTicket = uniform(s_i32[2]);
-    __syncthreads();
-    if (task == 0xfffffffeu) continue;  // lost resume entry (counted)
-    if (task >= P.num_tasks) break;
 
-    const int tile = (int)(task % (unsigned)totalTiles);
-    const int row0 = (tile / tilesN) * E::TM;
-    const int col0 = (tile % tilesN) * E::TN;
-    const typename E::Lane ln = E::lane_offsets(ctx, row0, col0);
-    typename E::Acc acc;
-    int lastSlot = -1;
-
+    // ---- the next job ----
     // The stage loop is (re)entered with the tile's state taken from:
-    //   FRESH   start at k = 0 (new task, or a restart);
+    //   FRESH   start at k = 0 (new task, urgent tile, or a restart);
     //   ACC     accumulators from `src`; stages s, s+1 fetched again;
     //   FULL    accumulators and the two live stages from `src`;
     //   AS_IS   nothing to do: the loop left at a poll site with its state
     //           intact (the site found nothing to yield for).
-    // A resume entry of the retreat arm enters once with ACC / FULL. The
-    // stage loop itself only notices a new generation and leaves; the event
-    // log, the setter, the yield decision and the checkpoint all happen
-    // here, outside it, so that none of their state is live in the loop.
-    enum { FRESH = 0, ACC = 1, FULL = 2, AS_IS = 3 };
+    unsigned task = 0;
+    int srcKind = FRESH, s = 0, siteDone = -1;
     const float* src = nullptr;
-    int s = 0, slot = 0, toPoll = 0, siteDone = -1;
-    int srcKind = FRESH;
-    if (retreatArm && kind > 0) {
-      src = P.rq_slots + (size_t)qTicket * Ckpt<E>::SLOT_FLOATS;
-      s = qStage;
-      srcKind = kind;
+    bool urgent = false;
+    if (!RETREAT && serving >= 0) {
+      if (uidx < nU()) {
+        urgent = true;
+      } else {
+        // Every urgent tile of the event is taken: the service ends and the
+        // interrupted tile re-enters at the site it left (not polled again).
+        if (tid == 0) {
+          const int64_t t2 = wall_ticks();
+          atomic_max_u64(&P().u_end_max[serving], (unsigned long long)t2);
+          P().u_gt[2 * (size_t)serving + 1] = t2;
+          stat(ST_YIELDS, 1);
+          stat(ST_URGENT, (uint64_t)(t2 - s_serve_t1));
+        }
+        task = savedTask;
+        srcKind = savedKind;
+        if (savedKind != FRESH) {
+          s = savedStage;
+          siteDone = savedStage;
+          src = ckslot();
+        }
+        serving = -1;
+      }
+    } else {
+      // Thread 0 takes the next task: a checkpointed tile from the resume
+      // queue first (retreat arm), else a new task from the work queue.
+      // kind: -1 new task; 0 restart from k = 0; 1 resume from the saved
+      // accumulators at the saved stage; 2 the same plus the live stages.
+      if (tid == 0) {
+        unsigned t = 0xffffffffu;
+        int kind = -1, st = 0, tk = 0;
+        if constexpr (retreatArm) {
+          const unsigned q = rq_pop(P().rq_ctl);
+          if (q != RQ_NONE) {
+            const int ready = rq_wait_ready(P().rq_entry + (size_t)q * 4);
+            if (ready > 0) {
+              t = (unsigned)P().rq_entry[(size_t)q * 4];
+              st = P().rq_entry[(size_t)q * 4 + 1];
+              kind = ready - 1;
+              tk = (int)q;
+              stat(ST_RESUMED, 1);
+            } else {
+              stat(ST_ERRORS, 1);  // never published within the deadline: the task is lost
+              t = 0xfffffffeu;
+            }
+          }
+        }
+        if (t == 0xffffffffu)
+          t = TaskQueue(P().next_task, P().M / E::TM, tilesN(), P().num_tasks).pop((int)xcc_id());
+        s_u32 = t;
+        s_i32[0] = kind;
+        s_i32[1] = st;
+        s_i32[2] = tk;
+      }
+      __syncthreads();
+      task = uniform(s_u32);
+      const int kind = uniform(s_i32[0]);
+      const int qStage = uniform(s_i32[1]);
+      const int qTicket = uniform(s_i32[2]);
+      __syncthreads();
+      if (task == 0xfffffffeu) continue;  // lost resume entry (counted)
+      if (task >= P().num_tasks) break;
+      if (retreatArm && kind > 0) {
+        src = P().rq_slots + (size_t)qTicket * Ckpt<E>::SLOT_FLOATS;
+        s = qStage;
+        srcKind = kind;
+      }
     }
-    bool retreated = false;
 
-    for (;;) {  // (re)entries of the stage loop of this tile
+    // The job's operands and output tile.
+    const typename E::Ctx ctx = urgent ? E::make_ctx(P().Au, P().Bu, P().Mu, P().Nu, P().Ku)
+                                       : E::make_ctx(P().A, P().B, P().M, P().N, P().K);
+    const int S = (urgent ? P().Ku : P().K) / E::KS;
+    int row0, col0;
+    if (urgent) {
+      row0 = (uidx / uTilesN()) * E::TM;
+      col0 = (uidx % uTilesN()) * E::TN;
+    } else {
+      const int tile = (int)(task % (unsigned)((P().M / E::TM) * tilesN()));
+      row0 = (tile / tilesN()) * E::TM;
+      col0 = (tile % tilesN()) * E::TN;
+    }
+    const bool pollable = POLL != APK_POLL_OFF && !urgent;
+    const typename E::Lane ln = E::lane_offsets(ctx, row0, col0);
+    typename E::Acc acc;
+    int slot = 0, toPoll = 0, lastSlot = -1;
+
+    // Poll sites are the stages s with s % pollStride == 0, tracked with a
+    // countdown (`toPoll` stages until the next site) rather than divisions;
+    // an urgent tile never reaches one. The sample a site s reads is issued
+    // in front of the data loads of stage s+1, i.e. right behind stage s's
+    // own loads, so the ordinary "stage s landed" wait retires it too. For a
+    // site at the tile's last stage the sample is issued alone, in place of
+    // stage S.
+    auto issue_stage = [&](int t, int tslot, bool carry) {
+      if (POLL != APK_POLL_OFF && carry) {
+        sample_flag<SYS>(flag_rsrc, &flagring[tslot]);
+        lastSlot = tslot;
+      }
+      if (t < S) E::issue(ring, ctx, tslot, row0, col0, t);
+    };
+
+    bool retreated = false, yielded = false;
+    for (;;) {  // (re)entries of the stage loop of this job
       if (srcKind != AS_IS) {
-        toPoll = POLL == APK_POLL_STAGE ? 0 : (pollStride - s % pollStride) % pollStride;
+        toPoll = !pollable                  ? S + 2
+                 : POLL == APK_POLL_STAGE ? 0
+                                          : (pollStride - s % pollStride) % pollStride;
         const int64_t tIn = wall_ticks();
         if (srcKind == FRESH) {
           E::zero(acc);
-          issue_stage(ctx, row0, col0, s, slot, false, lastSlot);
-          issue_stage(ctx, row0, col0, s + 1, next_slot(slot), true, lastSlot);  // s is a site
+          issue_stage(s, slot, false);
+          issue_stage(s + 1, next_slot(slot), pollable);  // s is a site
+          if (urgent && P().poison) {
+            // Test hook: corrupt the staged B[0][col0] of the urgent tile.
+            wait_landed<E>(S > 1);
+            lds_sync();
+            if (tid == 0) *(float*)(ring + E::A_STAGE) += 1.0f;
+            lds_sync();
+          }
         } else {
           // Accumulators hold stages [0, s); stages s, s+1 go to ring slots
           // slot, slot+1 (from the checkpoint, or fetched again), and the
@@ -249,17 +283,20 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
           const int live = (S - s) < 2 ? (S - s) : 2;
           if (srcKind == FULL) {
             Ckpt<E>::load_ring(ring, src, slot, live);
-            issue_stage(ctx, row0, col0, S, next_slot(slot), true, lastSlot);  // sample alone
+            issue_stage(S, next_slot(slot), true);  // sample alone
             wait_vmcnt<0>();
             __syncthreads();  // restored ring visible to all waves
           } else {
-            issue_stage(ctx, row0, col0, s, slot, false, lastSlot);
-            issue_stage(ctx, row0, col0, s + 1, next_slot(slot), true, lastSlot);
+            issue_stage(s, slot, false);
+            issue_stage(s + 1, next_slot(slot), true);
           }
-          if (tid == 0 && src == ckslot) stRestore += (uint64_t)(wall_ticks() - tIn);
+          if (tid == 0 && src == ckslot()) stat(ST_RESTORE, (uint64_t)(wall_ticks() - tIn));
         }
       }
 
+      // The stage loop itself only notices a new generation and leaves; the
+      // event log, the setter, the yield decision and the checkpoint all
+      // happen below, outside it, so that none of their state is live in it.
       bool atSite = false;
       int fSeen = 0;
       while (s < S) {
@@ -301,139 +338,137 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
       int f = fSeen;
       if (isSetter && tid == 0 && f >= 0) {
         const int64_t now = wall_ticks();
-        if (gBase == 0) gBase = now;
-        if (nextEv < P.num_events) {
-          if (now >= gBase + P.sched[nextEv]) {
-            P.set_gt[nextEv] = now;
-            set_flag(++nextEv);
+        if (s_setter[1] == 0) s_setter[1] = now;
+        const long long gBase = s_setter[1];
+        const int nextEv = (int)s_setter[0];
+        if (nextEv < P().num_events) {
+          if (now >= gBase + P().sched[nextEv]) {
+            P().set_gt[nextEv] = now;
+            s_setter[0] = nextEv + 1;
+            set_flag(nextEv + 1);
           }
-        } else if (P.stop_after > 0 &&
-                   now >= gBase + (P.num_events ? P.sched[P.num_events - 1] : 0) + P.stop_after) {
+        } else if (P().stop_after > 0 &&
+                   now >= gBase + (P().num_events ? P().sched[P().num_events - 1] : 0) +
+                              P().stop_after) {
           set_flag(-1);  // self-terminating run: no host in the loop
         }
       }
-      if (f > P.num_events) f = P.num_events;  // never index past the event arrays
+      if (f > P().num_events) f = P().num_events;  // never index past the event arrays
       srcKind = AS_IS;
       if (f <= lastSeen) continue;
       const int64_t g = wall_ticks();
-      if (tid == 0 && P.obs_gt && row < obsStride)
-        for (int e = lastSeen; e < f; ++e) P.obs_gt[(size_t)e * obsStride + row] = g;
+      if (tid == 0 && P().obs_gt) {
+        const int obsStride = P().obs_stride > 0 ? P().obs_stride : (int)gridDim.x;
+        if (row() < obsStride)
+          for (int e = lastSeen; e < f; ++e) P().obs_gt[(size_t)e * obsStride + row()] = g;
+      }
       const int ev = f - 1;
       lastSeen = f;
 
       // Does this block hand over its CU (retreat) or run urgent tiles?
       float* dst;
       unsigned tk = RQ_NONE;
-      int uidx = 0;
       if constexpr (retreatArm) {
         // The hardware deals a kernel's workgroups round-robin to the XCDs
         // and their shader engines from wherever its pointers stand, and a
         // workgroup runs only on a CU of its own shader engine: the urgent
         // kernel's R workgroups land in R domains the host cannot name, so
         // free ceil(R / 32) CUs in every (XCD, shader engine) domain.
-        const int quota = (P.retreat + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS;
-        const int dom = home * APK_SES_PER_XCD + (int)se_id();
+        const int quota = (P().retreat + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS;
+        const int dom = (int)xcc_id() * APK_SES_PER_XCD + (int)se_id();
         unsigned t = RQ_NONE;
         if (tid == 0 &&
-            fetch_add_i32(&P.retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + dom], 1) < quota)
-          t = rq_reserve(P.rq_ctl, P.rq_capacity);
+            fetch_add_i32(&P().retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + dom], 1) < quota)
+          t = rq_reserve(P().rq_ctl, P().rq_capacity);
         tk = bcast(t);
         if (tk == RQ_NONE) continue;  // quota taken (or queue full): keep working
-        dst = P.rq_slots + (size_t)tk * Ckpt<E>::SLOT_FLOATS;
+        dst = P().rq_slots + (size_t)tk * Ckpt<E>::SLOT_FLOATS;
         wait_vmcnt<0>();  // always drain: nothing may land in LDS after the block exits
       } else {
+        const int U = nU();
         uidx = U > 0 ? pop_urgent(ev) : U;
         if (uidx >= U) continue;
-        dst = ckslot;
-        if (!P.naive) wait_vmcnt<0>();  // drain: stage s+1 has landed
+        dst = ckslot();
+        if (!P().naive) wait_vmcnt<0>();  // drain: stage s+1 has landed
       }
 
       // ---- checkpoint: accumulators and the live stages s, s+1 ----
       lds_sync();
       const int64_t tSave = wall_ticks();
       const int live = (S - s) < 2 ? (S - s) : 2;  // resident, not computed
-      if (P.resume != APK_RESUME_RESTART) {
+      if (P().resume != APK_RESUME_RESTART) {
         Ckpt<E>::save_acc(acc, dst);
-        if (P.resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, dst, slot, live);
+        if (P().resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, dst, slot, live);
       }
 
       if constexpr (retreatArm) {
         // ---- retreat: publish resume entry tk and exit, handing the CU on ----
-        const int rkind = P.resume == APK_RESUME_RESTART ? 0
-                          : P.resume == APK_RESUME_CKPT_FULL ? 2 : 1;
+        const int rkind = P().resume == APK_RESUME_RESTART ? 0
+                          : P().resume == APK_RESUME_CKPT_FULL ? 2 : 1;
         __threadfence();  // this thread's checkpoint stores are visible device-wide
         __syncthreads();
         if (tid == 0) {
-          rq_publish(P.rq_entry + (size_t)tk * 4, (int)task, rkind > 0 ? s : 0, rkind,
-                     home * APK_SES_PER_XCD + (int)se_id());
+          rq_publish(P().rq_entry + (size_t)tk * 4, (int)task, rkind > 0 ? s : 0, rkind,
+                     (int)xcc_id() * APK_SES_PER_XCD + (int)se_id());
           const int64_t t1 = wall_ticks();
-          ++stRetreats;
-          stSave += (uint64_t)(t1 - tSave);
-          if (P.retreat_gt) {
-            atomic_min_i64(&P.retreat_gt[2 * (size_t)ev], tSave);
-            atomic_max_i64(&P.retreat_gt[2 * (size_t)ev + 1], t1);
+          stat(ST_RETREATS, 1);
+          stat(ST_SAVE, (uint64_t)(t1 - tSave));
+          if (P().retreat_gt) {
+            atomic_min_i64(&P().retreat_gt[2 * (size_t)ev], tSave);
+            atomic_max_i64(&P().retreat_gt[2 * (size_t)ev + 1], t1);
           }
         }
         retreated = true;
-        break;
       } else {
-        // ---- cooperative yield: this block runs the event's urgent tiles ----
+        // ---- cooperative yield: this block serves the event next ----
         lds_sync();  // ring reads (checkpoint) done before the urgent tiles overwrite it
-        const int64_t t1 = wall_ticks();
-        if (uidx == 0 && tid == 0) {
-          P.claim[ev] = bid + 1;
-          P.claim_site[ev] = s;
-          P.u_gt[2 * (size_t)ev] = t1;
-        }
-        while (uidx < U) {
-          urgent_tile(acc, uidx, ev);
-          uidx = pop_urgent(ev);
-        }
-        const int64_t t2 = wall_ticks();
         if (tid == 0) {
-          atomic_max_u64(&P.u_end_max[ev], (unsigned long long)t2);
-          P.u_gt[2 * (size_t)ev + 1] = t2;
-          ++stYields;
-          stInflight += live > 1 ? 1 : 0;  // stage s+1 was issued, not waited for
-          stSave += (uint64_t)(t1 - tSave);
-          stUrgent += (uint64_t)(t2 - t1);
+          const int64_t t1 = wall_ticks();
+          s_serve_t1 = t1;
+          if (uidx == 0) {
+            P().claim[ev] = bid + 1;
+            P().claim_site[ev] = s;
+            P().u_gt[2 * (size_t)ev] = t1;
+          }
+          stat(ST_INFLIGHT, live > 1 ? 1 : 0);  // stage s+1 was issued, not waited for
+          stat(ST_SAVE, (uint64_t)(t1 - tSave));
         }
-        if (P.resume == APK_RESUME_RESTART) {  // the tile starts over from k = 0
-          srcKind = FRESH;
-          s = 0;
-          slot = 0;
-          siteDone = -1;
-        } else {
-          src = ckslot;
-          srcKind = P.resume == APK_RESUME_CKPT_FULL ? FULL : ACC;
-        }
-        lds_sync();  // reconverge before re-entering the stage loop
+        serving = ev;
+        savedTask = task;
+        savedStage = s;
+        savedKind = P().resume == APK_RESUME_RESTART   ? FRESH
+                    : P().resume == APK_RESUME_CKPT_FULL ? FULL
+                                                          : ACC;
+        yielded = true;
       }
+      break;
     }
     if (retreated) break;  // the block exits; its tile waits in the resume queue
+    if (yielded) continue;  // the event's urgent tiles first, then this tile again
     lds_sync();  // every wave done with the ring; every sample has landed
     if (POLL != APK_POLL_OFF && lastSlot >= 0) fLatest = uniform(flagring[lastSlot]);
 
-    const uint64_t hp = store_tile<E>(acc, ring, P.C, P.N, row0, col0, P.task_hash != nullptr);
-    if (P.task_hash) {
+    // ---- epilogue: C tile, fingerprint, exactly-once count ----
+    float* C = urgent ? P().Cu + (size_t)serving * (size_t)P().cu_event_stride : P().C;
+    unsigned long long* hashDst =
+        urgent ? (P().u_hash ? P().u_hash + (size_t)serving * nU() + uidx : nullptr)
+               : (P().task_hash ? P().task_hash + task : nullptr);
+    const uint64_t hp = store_tile<E>(acc, ring, C, urgent ? P().Nu : P().N, row0, col0,
+                                      hashDst != nullptr);
+    if (hashDst) {
       const uint64_t h = block_sum_u64(hp, s_red);
-      if (tid == 0) P.task_hash[task] = h;
+      if (tid == 0) *hashDst = h;
     }
-    if (ORACLE && tid == 0) fetch_add_i32(&P.exec_count[task], 1);
+    if (ORACLE && tid == 0)
+      fetch_add_i32(urgent ? &P().u_exec_count[serving] : &P().exec_count[task], 1);
+    if (urgent) uidx = pop_urgent(serving);
   }
 
-  if (P.run_gt && tid == 0 && fetch_add_u32(P.exit_count, 1u) == (unsigned)G - 1)
-    P.run_gt[1] = wall_ticks();
-  if (P.stats && tid == 0) {
-    unsigned long long* st = P.stats + (size_t)row * APK_STATS_PER_BLOCK;
-    st[0] = stYields;
-    st[1] = stSave;
-    st[2] = stUrgent;
-    st[3] = stRestore;
-    st[4] = stInflight;
-    st[5] = stRetreats;
-    st[6] = stResumed;
-    st[7] = stErrors;
+  if (P().run_gt && tid == 0 && fetch_add_u32(P().exit_count, 1u) == gridDim.x - 1)
+    P().run_gt[1] = wall_ticks();
+  if (P().stats && tid == 0) {
+    unsigned long long* st = P().stats + (size_t)row() * APK_STATS_PER_BLOCK;
+    for (int k = 0; k < APK_STATS_PER_BLOCK; ++k) st[k] = s_stats[k];
   }
 }
 
