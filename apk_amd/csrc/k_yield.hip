@@ -76,6 +76,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   constexpr bool retreatArm = RETREAT && POLL != APK_POLL_OFF;
 
   const uint32_t ring_lds = lds_addr_of(ring);
+  const uint32_t flag_lds = lds_addr_of(flagring);
   if (tid < E::NS) flagring[tid] = 0;
   if (tid < APK_STATS_PER_BLOCK) s_stats[tid] = 0;
   if (tid < 2) s_setter[tid] = 0;
@@ -239,18 +240,18 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     const bool pollable = POLL != APK_POLL_OFF && !urgent;
     const typename E::Lane ln = E::lane_offsets(ctx, row0, col0);
     typename E::Acc acc;
-    int slot = 0, toPoll = 0, lastSlot = -1;
+    int slot = 0, nextSite = 0, lastSlot = -1;
 
-    // Poll sites are the stages s with s % pollStride == 0, tracked with a
-    // countdown (`toPoll` stages until the next site) rather than divisions;
-    // an urgent tile never reaches one. The sample a site s reads is issued
+    // Poll sites are the stages s with s % pollStride == 0; `nextSite` is the
+    // next one not yet passed (an urgent tile never reaches one), so a stage
+    // costs two scalar compares. The sample a site s reads is issued
     // in front of the data loads of stage s+1, i.e. right behind stage s's
     // own loads, so the ordinary "stage s landed" wait retires it too. For a
     // site at the tile's last stage the sample is issued alone, in place of
     // stage S.
     auto issue_stage = [&](int t, int tslot, bool carry) {
       if (POLL != APK_POLL_OFF && carry) {
-        sample_flag<SYS>(flag_rsrc, &flagring[tslot]);
+        sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)tslot);
         lastSlot = tslot;
       }
       if (t < S) E::issue(ring, ctx, tslot, row0, col0, t);
@@ -259,9 +260,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     bool retreated = false, yielded = false;
     for (;;) {  // (re)entries of the stage loop of this job
       if (srcKind != AS_IS) {
-        toPoll = !pollable                  ? S + 2
-                 : POLL == APK_POLL_STAGE ? 0
-                                          : (pollStride - s % pollStride) % pollStride;
+        nextSite = !pollable ? S + 2 : (s + pollStride - 1) / pollStride * pollStride;
         const int64_t tIn = wall_ticks();
         if (srcKind == FRESH) {
           E::zero(acc);
@@ -305,29 +304,31 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
         // Poll site: the flag sample issued in front of stage s+1's loads has
         // landed with stage s. A new generation (or the setter's turn) ends
         // the loop here, before stage s is computed.
-        if (POLL != APK_POLL_OFF && toPoll == 0 && s != siteDone) {
-          const int f = uniform(flagring[next_slot(slot)]);
-          fLatest = f;
-          if (f != lastSeen || isSetter) {
-            fSeen = f;
-            atSite = true;
-            break;
+        if (POLL != APK_POLL_OFF && s == nextSite) {
+          if (s != siteDone) {
+            const int f = uniform(flagring[next_slot(slot)]);
+            fLatest = f;
+            if (f != lastSeen || isSetter) {
+              fSeen = f;
+              atSite = true;
+              break;
+            }
           }
+          nextSite += pollStride;
         }
         const int ahead = slot_after_next(slot);
-        const bool carry = (toPoll == 1) || (toPoll == 0 && pollStride == 1);  // s+1 is a site
+        const bool carry = s + 1 == nextSite;  // s+1 is a site
         // Stage s+2 (and the sample for a site at s+1) goes out under stage
         // s's matrix work; its slot held stage s-1, which every wave finished
         // before the barrier above.
         E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
           if (s + 2 > S) return;
           if (POLL != APK_POLL_OFF && i == 0 && carry) {
-            sample_flag<SYS>(flag_rsrc, &flagring[ahead]);
+            sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)ahead);
             lastSlot = ahead;
           }
           if (s + 2 < S) E::issue_one(ring_lds, ctx, ln, ahead, s + 2, i);
         });
-        toPoll = (toPoll == 0 ? pollStride : toPoll) - 1;
         slot = next_slot(slot);
         ++s;
       }

@@ -163,9 +163,7 @@ __device__ __forceinline__ void run_stages(char* ring, const typename E::Ctx& c,
 // a host-mapped flag is read at system scope (sc0 sc1). The other waves read
 // the sample from LDS after the next barrier.
 template <bool SYSTEM>
-__device__ __forceinline__ void sample_flag(i32x4 flag_rsrc, int* lds_dst) {
-  const uint32_t lds_addr = (uint32_t)(uintptr_t)(
-      (__attribute__((address_space(3))) const void*)lds_dst);
+__device__ __forceinline__ void sample_flag(i32x4 flag_rsrc, uint32_t lds_addr) {
   const uint32_t m0 = __builtin_amdgcn_readfirstlane(lds_addr);
   const uint32_t zero = 0;
   if (threadIdx.x == 0) {
