@@ -12,11 +12,23 @@ and the CPU baseline: the reference's float64 host GEMM (i-k-j,
 src/persistent.cu:221-227, restated in oracle/) timed on this host on a
 bounded sample of the same GEMM's rows.
 
-Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3]
+The same line carries `preemption`: the cfg3 experiment (background fp32
+SGEMM M=N=8192, K=4096, 128x128 tiles, k-chunk 128, on all 256 CUs; urgent
+fp32 GEMM 256x256x256 at exponential arrivals, mean 2 ms) run by the
+product binaries on a bounded sample of arrivals -- cooperative tile-boundary
+yield latency (flag set -> last block observes, the reference's latency),
+the retreat arm (flag raised -> urgent GEMM starts on its own stream), the
+no-preemption baseline, the tile-boundary polling overhead (ABAB drains) and
+the tile time at full residency they are measured against -- and `bf16`: the
+cfg5 bf16 MFMA GEMM throughput (M=N=K=8192, 256x256 tiles, no yields).
+
+Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-preempt]
 """
 import argparse
 import json
 import os
+import re
+import subprocess
 import sys
 import time
 
@@ -68,6 +80,100 @@ def measured_traffic(profile="profiles/persistent_gemm_mfma128_cfg2.md"):
     return None
 
 
+BIN = os.path.join(ROOT, "apk_amd", "bin")
+# cfg3: background 8192x8192 (64x64 tiles of 128), K=4096 in k-chunks of 128,
+# one pass over the grid per trial; urgent 256x256x256 on 4 workers.
+CFG3 = ["--engine", "mfma128", "--tiles-m", "64", "--tiles-n", "64", "--gemm-k", "4096",
+        "--k", "128"]
+CFG3_URGENT = ["--urgent-m", "256", "--urgent-n", "256", "--urgent-k", "256"]
+
+
+def run_bin(name, args, timeout=300):
+    """Run a product binary (apk_amd/bin) and return its stdout; its exit
+    status must be 0 (every binary checks its own results)."""
+    cmd = [os.path.join(BIN, name)] + [str(a) for a in args]
+    log(f"$ apk_amd/bin/{name} " + " ".join(cmd[1:]))
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=timeout)
+    if r.returncode != 0:
+        raise RuntimeError(f"{name} exited {r.returncode}:\n{r.stdout[-2000:]}\n{r.stderr[-2000:]}")
+    return r.stdout
+
+
+def grab(text, pattern, cast=float):
+    m = re.search(pattern, text)
+    if not m:
+        raise RuntimeError(f"pattern {pattern!r} not found in:\n{text[-2000:]}")
+    return tuple(cast(g) for g in m.groups())
+
+
+def preemption_metrics(events, trials):
+    """cfg3 preemption figures from the product binaries (see module doc)."""
+    out = {"workload": ("cfg3: bg fp32 SGEMM M=N=8192 K=4096, 128x128 tiles, k-chunk 128, "
+                        "256 workers (1/CU); urgent fp32 GEMM 256x256x256; exponential "
+                        "arrivals, mean 2 ms, seed 21")}
+    # Polling overhead (ABAB drains, medians): flag sampled at tile (k-chunk)
+    # boundaries, and at every k-stage; the tile time from the poll-off drain.
+    ovh = {}
+    for poll in ("chunk", "stage"):
+        t = run_bin("yield", ["--mode", "overhead"] + CFG3 + ["--tasks", 4096, "--reps", 6,
+                                                               "--poll", poll])
+        on_ms, = grab(t, r"poll ON : ([\d.]+) ms")
+        off_ms, = grab(t, r"poll OFF: ([\d.]+) ms")
+        pct, = grab(t, r"polling overhead: ([-\d.]+)%")
+        ovh[poll] = (pct, on_ms, off_ms)
+    # 4096 tasks of 32 k-chunks each over 256 workers: chunk time per worker.
+    tile_us = min(ovh["chunk"][2], ovh["stage"][2]) * 1e3 * 256 / 4096 / 32
+    out["tile_us_full_residency"] = round(tile_us, 3)
+    out["overhead_pct"] = {"tile_boundary": ovh["chunk"][0], "k_stage": ovh["stage"][0]}
+    # Cooperative yield: set -> last block observes (the reference's
+    # latency); urgent e2e. Flag polled at every k-stage, and at tile
+    # boundaries only.
+    for poll, key in (("stage", "coop"), ("chunk", "coop_tile_boundary")):
+        lat = run_bin("yield", ["--mode", "latency"] + CFG3 + CFG3_URGENT +
+                      ["--poll", poll, "--arrival", "exp", "--mean-gap-us", 2000,
+                       "--events", events])
+        p50, p90, p99 = grab(lat, r"preemption latency set->last \(us\): p50 ([\d.]+) \| "
+                                  r"p90 ([\d.]+) \| p99 ([\d.]+)")
+        e50, e99 = grab(lat, r"urgent e2e set->done \(us\): p50 ([\d.]+) \| p99 ([\d.]+)")
+        out[key + "_latency_us"] = {"p50": p50, "p99": p99, "events": events,
+                                    "p50_over_tile": round(p50 / tile_us, 3)}
+        out[key + "_urgent_e2e_us"] = {"p50": e50, "p99": e99}
+    # Retreat arm: CUs handed to the urgent GEMM on its own stream.
+    rt = run_bin("urgent_baseline", CFG3 + CFG3_URGENT +
+                 ["--bg-tasks", 4096, "--urgent-blocks", 4, "--arrival", "exp",
+                  "--mean-gap-us", 2000, "--trials", trials, "--verify-rows", 64,
+                  "--yield", 1, "--retreat", 4, "--oracle", 1])
+    r50, r99 = grab(rt, r"flag raised -> urgent GEMM starts \(us\): p50 ([\d.]+) \| "
+                        r"p90 [\d.]+ \| p99 ([\d.]+)")
+    re50, re99 = grab(rt, r"urgent e2e \(us\):\s+p50 ([\d.]+) \| p90 [\d.]+ \| p99 ([\d.]+)")
+    bad, = grab(rt, r"SAFETY: (\d+) of", int)
+    oracle_ok = "ORACLE: PASS" in rt
+    out["retreat_latency_us"] = {"p50": r50, "p99": r99, "trials": trials,
+                                 "p50_over_tile": round(r50 / tile_us, 3)}
+    out["retreat_urgent_e2e_us"] = {"p50": re50, "p99": re99}
+    out["corrupt_yields"] = bad
+    out["oracle"] = "PASS" if oracle_ok else "FAIL"
+    # No preemption: the urgent GEMM waits for the background to drain.
+    nb = run_bin("urgent_baseline", CFG3 + CFG3_URGENT +
+                 ["--bg-tasks", 4096, "--urgent-blocks", 4, "--arrival", "exp",
+                  "--mean-gap-us", 2000, "--trials", trials])
+    n50, n99 = grab(nb, r"urgent e2e \(us\):\s+p50 ([\d.]+) \| p90 [\d.]+ \| p99 ([\d.]+)")
+    out["no_preempt_urgent_e2e_us"] = {"p50": n50, "p99": n99, "trials": trials}
+    return out
+
+
+def bf16_metrics():
+    """cfg5 bf16 MFMA GEMM throughput (tcyield calibrate, no yields)."""
+    t = run_bin("tcyield", ["--mode", "calibrate", "--tiles-m", 32, "--tiles-n", 32,
+                            "--gemm-k", 8192, "--k", 256, "--tasks", 2048])
+    us, gf = grab(t, r"-> ([\d.]+) us/task/block \| ([\d.]+) GFLOP/s")
+    tf = gf / 1e3
+    return {"workload": "cfg5: bf16 GEMM M=N=K=8192 (2 passes of 1024 256x256 tiles), fp32 "
+                        "accumulate, 256 workers, no yields",
+            "tflops": round(tf, 2), "peak": 2516.6, "frac": round(tf / 2516.6, 4),
+            "us_per_tile": us}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -77,6 +183,12 @@ def main():
     ap.add_argument("--k-chunk", type=int, default=32)
     ap.add_argument("--cpu-rows", type=int, default=1024)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-preempt", action="store_true",
+                    help="skip the preemption and bf16 sections")
+    ap.add_argument("--events", type=int, default=500,
+                    help="arrivals for the cooperative latency sample")
+    ap.add_argument("--trials", type=int, default=200,
+                    help="arrivals for the retreat-arm and no-preemption samples")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -178,6 +290,11 @@ def main():
             "traffic": measured_traffic() if (S, kc) == (4096, 32) else None,
         },
     }
+    if not args.no_preempt:
+        out["preemption"] = preemption_metrics(args.events, args.trials)
+        out["bf16"] = bf16_metrics()
+        log("preemption: " + json.dumps(out["preemption"]))
+        log("bf16: " + json.dumps(out["bf16"]))
     if not args.no_cpu:
         rows = args.cpu_rows
         A_host = dA[:rows].cpu().numpy()
