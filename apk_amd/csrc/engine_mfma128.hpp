@@ -93,25 +93,35 @@ struct EngMfma128 {
     return Lane{(uint32_t)(((row0 + ra) * c.K + 4 * qa) * 4),
                 (uint32_t)((rb * c.N + col0 + 4 * cq) * 4)};
   }
-  static __device__ __forceinline__ void issue_one(uint32_t ring_lds, const Ctx& c,
-                                                   const Lane& ln, int slot, int s, int i) {
-    const int w = wave_id();
-    const uint32_t stage = ring_lds + (uint32_t)(slot * STAGE);
+  // The scalar parts of the loads of stage s into ring slot `slot`, formed
+  // once per stage: this wave's 1 KiB piece of the slot (LDS) and the byte
+  // offsets of k-stage s in A (along a row) and B (down the rows).
+  struct Dst {
+    uint32_t lds, ka, kb;
+  };
+  static __device__ __forceinline__ Dst stage_dst(uint32_t ring_lds, const Ctx& c, int slot,
+                                                  int s) {
     const uint32_t k0 = (uint32_t)(s * KS);
+    return Dst{(uint32_t)__builtin_amdgcn_readfirstlane(
+                   (int)(ring_lds + (uint32_t)(slot * STAGE) + (uint32_t)(wave_id() * 1024))),
+               k0 * 4u, k0 * (uint32_t)c.N * 4u};
+  }
+  static __device__ __forceinline__ void issue_one(const Ctx& c, const Lane& ln, const Dst& d,
+                                                   int i) {
     if (i < LOADS_A)
-      dma_x4(c.ra, stage + (uint32_t)((i * 4 + w) * 1024), ln.a,
-             k0 * 4u + (uint32_t)(i * 32) * (uint32_t)c.K * 4u);
+      dma_x4(c.ra, d.lds + (uint32_t)(i * 4096), ln.a,
+             d.ka + (uint32_t)(i * 32) * (uint32_t)c.K * 4u);
     else
-      dma_x4(c.rb, stage + A_STAGE + (uint32_t)(((i - LOADS_A) * 4 + w) * 1024), ln.b,
-             (k0 + (uint32_t)((i - LOADS_A) * 8)) * (uint32_t)c.N * 4u);
+      dma_x4(c.rb, d.lds + (uint32_t)(A_STAGE + (i - LOADS_A) * 4096), ln.b,
+             d.kb + (uint32_t)((i - LOADS_A) * 8) * (uint32_t)c.N * 4u);
   }
   // All loads of stage s of the tile at (row0, col0) into ring slot `slot`.
   static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot, int row0,
                                                int col0, int s) {
     const Lane ln = lane_offsets(c, row0, col0);
-    const uint32_t rl = lds_addr_of(ring);
+    const Dst d = stage_dst(lds_addr_of(ring), c, slot, s);
 #pragma unroll
-    for (int i = 0; i < LOADS; ++i) issue_one(rl, c, ln, slot, s, i);
+    for (int i = 0; i < LOADS; ++i) issue_one(c, ln, d, i);
   }
 
   // Operands of k-group g (8 k values): one 16-byte A read per 32-row

@@ -321,13 +321,14 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
         // Stage s+2 (and the sample for a site at s+1) goes out under stage
         // s's matrix work; its slot held stage s-1, which every wave finished
         // before the barrier above.
+        const typename E::Dst d = E::stage_dst(ring_lds, ctx, ahead, s + 2);
         E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
           if (s + 2 > S) return;
           if (POLL != APK_POLL_OFF && i == 0 && carry) {
             sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)ahead);
             lastSlot = ahead;
           }
-          if (s + 2 < S) E::issue_one(ring_lds, ctx, ln, ahead, s + 2, i);
+          if (s + 2 < S) E::issue_one(ctx, ln, d, i);
         });
         slot = next_slot(slot);
         ++s;

@@ -146,9 +146,9 @@ __device__ __forceinline__ void run_stages(char* ring, const typename E::Ctx& c,
     hook(s);
     wait_landed<E>(s + 1 < S);
     lds_sync();
-    const int ahead = slot_after_next(slot);
+    const typename E::Dst d = E::stage_dst(rl, c, slot_after_next(slot), s + 2);
     E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
-      if (s + 2 < S) E::issue_one(rl, c, ln, ahead, s + 2, i);
+      if (s + 2 < S) E::issue_one(c, ln, d, i);
     });
     slot = next_slot(slot);
   }
