@@ -7,9 +7,12 @@
 // memory, in LDS and in the MFMA operand registers (8 consecutive k per lane
 // = one 16-byte LDS read). C is M x N row-major fp32.
 //
-// Block: 256 threads = 4 wave64s in a 2x2 arrangement; each wave owns a
-// 128x128 sub-tile held as 4x4 32x32 accumulators (256 fp32 per lane, in the
-// accumulation registers).
+// Block: 512 threads = 8 wave64s in a 2x4 arrangement, two per SIMD; each
+// wave owns a 128x64 sub-tile held as 4x2 32x32 accumulators (128 fp32 per
+// lane). A wave then needs ~200 of the SIMD's 512 registers per lane instead
+// of all 512: the preemptible kernel runs without spilling, and a small
+// kernel on another stream (the flag raise of the retreat arm) still finds
+// registers on every CU.
 // Stage: k depth KS=32 -> A stage 256 rows x 64 B (16 KiB) + Bt stage 256
 // rows x 64 B (16 KiB); 3 stages = 96 KiB of the 160 KiB LDS (1 block/CU).
 //
@@ -38,16 +41,17 @@ namespace apk {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 struct EngBf16x256 {
-  static constexpr int TM = 256, TN = 256, KS = 32, NS = 3, THREADS = 256;
+  static constexpr int TM = 256, TN = 256, KS = 32, NS = 3, THREADS = 512;
   static constexpr int ROW_BYTES = KS * 2;                  // 64 B
   static constexpr int A_STAGE = TM * ROW_BYTES;            // 16 KiB
   static constexpr int B_STAGE = TN * ROW_BYTES;            // 16 KiB
   static constexpr int STAGE = A_STAGE + B_STAGE;           // 32 KiB
   static constexpr int LDS_BYTES = NS * STAGE;              // 96 KiB
-  static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 4 per thread
-  static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 4 per thread
+  static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 2 per thread
+  static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 2 per thread
   static constexpr int LOADS = LOADS_A + LOADS_B;
-  static constexpr int ACC_PER_THREAD = 256;                // floats
+  static constexpr int WAVES = THREADS / 64;
+  static constexpr int ACC_PER_THREAD = 128;                // floats
   static constexpr int ELEM_BYTES = 2;                      // bf16 operands
   // Epilogue staging: STORE_PASSES passes of PASS_ROWS tile rows through LDS,
   // row stride STAGE_LD floats (4 floats of padding: the two half-waves write
@@ -55,7 +59,7 @@ struct EngBf16x256 {
   static constexpr int STORE_PASSES = 4, PASS_ROWS = 64, STAGE_LD = TN + 4;
 
   struct Acc {
-    f32x16 c[4][4];
+    f32x16 c[4][2];
   };
 
   struct Ctx {
@@ -76,7 +80,7 @@ struct EngBf16x256 {
 #pragma unroll
     for (int i = 0; i < 4; ++i)
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
         for (int r = 0; r < 16; ++r) a.c[i][j][r] = 0.0f;
   }
@@ -84,10 +88,10 @@ struct EngBf16x256 {
   static __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
 
   // Direct-to-LDS loads of one k-stage: load i (0..LOADS-1) fills the
-  // 1 KiB piece i*4 + wave of the A stage (i < 4) or of the Bt stage, i.e.
-  // 16 rows, row 64*i + 16*wave + lane/4, chunk slot lane%4. The swizzle of
-  // a row does not depend on its bit 6, so each lane's offset is fixed per
-  // tile (Lane) and load i and stage s only add scalar offsets.
+  // 1 KiB piece i*8 + wave of the A stage (i < 2) or of the Bt stage, i.e.
+  // 16 rows, row 128*i + 16*wave + lane/4, chunk slot lane%4. The swizzle of
+  // a row uses only its bits 2-3, so each lane's offset is fixed per tile
+  // (Lane) and load i and stage s only add scalar offsets.
   struct Lane {
     uint32_t a, b;
   };
@@ -113,11 +117,11 @@ struct EngBf16x256 {
   static __device__ __forceinline__ void issue_one(const Ctx& c, const Lane& ln, const Dst& d,
                                                    int i) {
     if (i < LOADS_A)
-      dma_x4(c.ra, d.lds + (uint32_t)(i * 4096), ln.a,
-             d.k + (uint32_t)(i * 64) * (uint32_t)c.K * 2u);
+      dma_x4(c.ra, d.lds + (uint32_t)(i * WAVES * 1024), ln.a,
+             d.k + (uint32_t)(i * WAVES * 16) * (uint32_t)c.K * 2u);
     else
-      dma_x4(c.rb, d.lds + (uint32_t)(A_STAGE + (i - LOADS_A) * 4096), ln.b,
-             d.k + (uint32_t)((i - LOADS_A) * 64) * (uint32_t)c.K * 2u);
+      dma_x4(c.rb, d.lds + (uint32_t)(A_STAGE + (i - LOADS_A) * WAVES * 1024), ln.b,
+             d.k + (uint32_t)((i - LOADS_A) * WAVES * 16) * (uint32_t)c.K * 2u);
   }
   // All loads of stage s of the tile at (row0, col0) into ring slot `slot`.
   static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot, int row0,
@@ -131,7 +135,7 @@ struct EngBf16x256 {
   // Operands of k-step j (16 k values): one 16-byte read per 32-row block of
   // A and per 32-column block of Bt.
   struct Frag {
-    bf16x8 a[4], b[4];
+    bf16x8 a[4], b[2];
   };
   static __device__ __forceinline__ void load_frag(const char* abase, int j, Frag& f) {
     const int w = threadIdx.x >> 6, l = lane_id();
@@ -144,8 +148,8 @@ struct EngBf16x256 {
       f.a[rb] = *(const bf16x8*)(abase + row * ROW_BYTES + ((q ^ swz(row)) << 4));
     }
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb) {
-      const int col = wn * 128 + cb * 32 + lr;
+    for (int cb = 0; cb < 2; ++cb) {
+      const int col = wn * 64 + cb * 32 + lr;
       f.b[cb] = *(const bf16x8*)(bbase + col * ROW_BYTES + ((q ^ swz(col)) << 4));
     }
   }
@@ -155,8 +159,8 @@ struct EngBf16x256 {
   // One k-stage out of ring slot `slot`. `pre` runs first (returning false
   // abandons the stage before any accumulator changes); `mid(i)`, i = 0..
   // LOADS-1, runs after MFMA 2i+1 of the first k-step -- the stage loops
-  // issue the next stage's direct-to-LDS load i there, one per two MFMAs,
-  // so the loads never hold up the matrix cores.
+  // issue the next-but-one stage's direct-to-LDS load i there, one per two
+  // MFMAs.
   template <class Pre, class Mid>
   static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
                                                  Pre&& pre, Mid&& mid) {
@@ -172,8 +176,8 @@ struct EngBf16x256 {
       if (j + 1 < J) load_frag(abase, j + 1, f[(j + 1) & 1]);
       const Frag& c = f[j & 1];
 #pragma unroll
-      for (int m = 0; m < 16; ++m) {
-        const int rb = m >> 2, cb = m & 3;
+      for (int m = 0; m < 8; ++m) {
+        const int rb = m >> 1, cb = m & 1;
         acc.c[rb][cb] =
             __builtin_amdgcn_mfma_f32_32x32x16_bf16(c.a[rb], c.b[cb], acc.c[rb][cb], 0, 0, 0);
         if (j == 0 && (m & 1) && (m >> 1) < LOADS) {
@@ -192,15 +196,15 @@ struct EngBf16x256 {
   // Output element (tile-relative row, col) of accumulator register e.
   static __device__ __forceinline__ void coord(int e, int& r, int& c) {
     const int w = threadIdx.x >> 6, l = lane_id();
-    const int wm = w & 1, wn = w >> 1, rb = e >> 6, cb = (e >> 4) & 3, i = e & 15;
+    const int wm = w & 1, wn = w >> 1, rb = e >> 5, cb = (e >> 4) & 1, i = e & 15;
     r = wm * 128 + rb * 32 + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
-    c = wn * 128 + cb * 32 + (l & 31);
+    c = wn * 64 + cb * 32 + (l & 31);
   }
   static __device__ __forceinline__ float get(const Acc& a, int e) {
-    return a.c[e >> 6][(e >> 4) & 3][e & 15];
+    return a.c[e >> 5][(e >> 4) & 1][e & 15];
   }
   static __device__ __forceinline__ void set(Acc& a, int e, float v) {
-    a.c[e >> 6][(e >> 4) & 3][e & 15] = v;
+    a.c[e >> 5][(e >> 4) & 1][e & 15] = v;
   }
 
   // Epilogue pass p: accumulator row block rb = p of every wave into LDS as
@@ -211,11 +215,11 @@ struct EngBf16x256 {
     const int wm = w & 1, wn = w >> 1;
     float* t = (float*)lds;
 #pragma unroll
-    for (int cb = 0; cb < 4; ++cb)
+    for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int rr = wm * 32 + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
-        t[rr * STAGE_LD + wn * 128 + cb * 32 + (l & 31)] = acc.c[p][cb][i];
+        t[rr * STAGE_LD + wn * 64 + cb * 32 + (l & 31)] = acc.c[p][cb][i];
       }
   }
   static __device__ __forceinline__ int pass_row(int p, int rr) {

@@ -19,7 +19,7 @@
 //  * the background is the preemptible kernel with polling off (tasks cycle
 //    the tile grid, src/urgent_baseline.cu:78-80), the urgent job is
 //    apk_persistent_gemm with --urgent-blocks workers over its own tiles.
-// Additions: --engine valu64|mfma128, --gemm-k K (background depth, walked
+// Additions: --engine valu64|mfma128|bf16x256, --gemm-k K (background depth, walked
 // in --k chunks), --urgent-m/-n/-k (urgent GEMM shape; default
 // urgent-blocks tiles of depth --gemm-k, as the reference), --arrival
 // uniform|exp with --mean-gap-us (exponential delays, redrawn until they fall
@@ -92,11 +92,12 @@ int main(int argc, char** argv) {
     return 1;
   }
 
-  const int engine = engName == "mfma128" ? APK_ENGINE_MFMA128
-                     : engName == "valu64" ? APK_ENGINE_VALU64
-                                           : -1;
+  const int engine = engName == "mfma128"    ? APK_ENGINE_MFMA128
+                     : engName == "valu64"   ? APK_ENGINE_VALU64
+                     : engName == "bf16x256" ? APK_ENGINE_BF16X256
+                                             : -1;
   if (engine < 0) {
-    fprintf(stderr, "unknown --engine %s (valu64|mfma128)\n", engName.c_str());
+    fprintf(stderr, "unknown --engine %s (valu64|mfma128|bf16x256)\n", engName.c_str());
     return 1;
   }
   apk_engine_geometry geo;
@@ -148,10 +149,30 @@ int main(int argc, char** argv) {
          engName.c_str(), urgentM, urgentN, urgentK, uTiles);
   printf("stream priorities: none (both streams at the default priority)\n");
 
+  // hA/hB (hAu/hBu): the values the float64 reference multiplies, B as
+  // K x N. dev*: the bytes the kernels read -- the same floats for the fp32
+  // engines; bf16 bit patterns with B transposed (Bt = N x K) for BF16X256.
+  const bool bf16 = geo.elem_bytes == 2;
   std::vector<float> hA((size_t)M * K), hB((size_t)K * N);
-  fill_uniform_pm1(seed, hA, hB);
   std::vector<float> hAu((size_t)urgentM * urgentK), hBu((size_t)urgentK * urgentN);
-  fill_uniform_pm1(seed + 1, hAu, hBu);
+  std::vector<uint8_t> devA, devB, devAu, devBu;
+  if (bf16) {
+    // normal(0,1) rounded to bf16 (the reference's tcyield data, src/tcyield.cu:459-473)
+    std::vector<uint16_t> a, b, au, bu;
+    fill_normal_bf16(seed, hA, a, hB, b);
+    fill_normal_bf16(seed + 1, hAu, au, hBu, bu);
+    devA = as_bytes(a);
+    devB = as_bytes(transpose_u16(b, K, N));
+    devAu = as_bytes(au);
+    devBu = as_bytes(transpose_u16(bu, urgentK, urgentN));
+  } else {
+    fill_uniform_pm1(seed, hA, hB);
+    fill_uniform_pm1(seed + 1, hAu, hBu);
+    devA = as_bytes(hA);
+    devB = as_bytes(hB);
+    devAu = as_bytes(hAu);
+    devBu = as_bytes(hBu);
+  }
 
   RigShape rs;
   rs.engine = engine;
@@ -172,19 +193,20 @@ int main(int argc, char** argv) {
     rs.hashTasks = (unsigned)bgTasks;
     if (oracle) rs.oracleTasks = (unsigned)bgTasks;
   }
-  YieldRig rig(rs, hA, hB, {}, {});
+  YieldRig rig(rs, devA, devB, {}, {});
 
-  float *dAu, *dBu, *dCu;
+  void *dAu, *dBu;
+  float* dCu;
   unsigned* dUNext;
   apk_tile_record* dULog;
   const int uChunks = 1;
-  HIP_CHECK(hipMalloc(&dAu, hAu.size() * 4));
-  HIP_CHECK(hipMalloc(&dBu, hBu.size() * 4));
+  HIP_CHECK(hipMalloc(&dAu, devAu.size()));
+  HIP_CHECK(hipMalloc(&dBu, devBu.size()));
   HIP_CHECK(hipMalloc(&dCu, (size_t)urgentM * urgentN * 4));
   HIP_CHECK(hipMalloc(&dUNext, APK_QUEUE_WORDS * sizeof(unsigned)));
   HIP_CHECK(hipMalloc(&dULog, (size_t)uTiles * uChunks * sizeof(apk_tile_record)));
-  HIP_CHECK(hipMemcpy(dAu, hAu.data(), hAu.size() * 4, hipMemcpyHostToDevice));
-  HIP_CHECK(hipMemcpy(dBu, hBu.data(), hBu.size() * 4, hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemcpy(dAu, devAu.data(), devAu.size(), hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemcpy(dBu, devBu.data(), devBu.size(), hipMemcpyHostToDevice));
   unsigned* hConsumed;  // pinned, for the mid-flight queue snapshot (per-XCD counters)
   HIP_CHECK(hipHostMalloc((void**)&hConsumed, APK_QUEUE_WORDS * sizeof(unsigned),
                           hipHostMallocDefault));
@@ -254,10 +276,13 @@ int main(int argc, char** argv) {
     for (int r = 0; r < rows; ++r) gemm_f64_rows(hA.data(), hB.data(), &ref[(size_t)r * N], N, K, r, 1);
     std::vector<double> uref((size_t)urgentM * urgentN);
     gemm_f64(hAu.data(), hBu.data(), uref.data(), urgentM, urgentN, urgentK, threads);
-    const double tol = K > 256 ? 1e-3 : 1e-4;  // elementwise gate; rel-Frobenius is the bar
+    // Elementwise gate; rel-Frobenius is the bar (fp32 1e-5, bf16 1e-2 on the
+    // bf16-rounded inputs, which the float64 reference multiplies exactly).
+    const double tol = (K > 256 || bf16) ? 1e-3 : 1e-4;
+    const double bar = bf16 ? 1e-2 : 1e-5;
     const CheckResult cb = check(hC.data(), ref.data(), (int64_t)rows * N, tol, tol);
     const CheckResult cu = check(hCu.data(), uref.data(), (int64_t)uref.size(), tol, tol);
-    if (cb.nans || cb.bad || cu.nans || cu.bad || cb.rel_frob > 1e-5 || cu.rel_frob > 1e-5) {
+    if (cb.nans || cb.bad || cu.nans || cu.bad || cb.rel_frob > bar || cu.rel_frob > bar) {
       fprintf(stderr, "FAIL: bg %lld NaN %lld bad (rel-Frob %.2e); urgent %lld NaN %lld bad "
               "(rel-Frob %.2e)\n", (long long)cb.nans, (long long)cb.bad, cb.rel_frob,
               (long long)cu.nans, (long long)cu.bad, cu.rel_frob);

@@ -33,7 +33,8 @@ enum {
  *  MFMA128  : 128x128 fp32 tile on v_mfma_f32_32x32x2_f32 (fp32 matrix
  *             cores), 256 threads, 3-stage LDS ring fed by buffer_load ... lds.
  *  BF16X256 : 256x256 tile of a bf16 GEMM with fp32 accumulation on
- *             v_mfma_f32_32x32x16_bf16 (replaces the reference's fp16 wmma
+ *             v_mfma_f32_32x32x16_bf16, 512 threads (2 waves per SIMD)
+ *             (replaces the reference's fp16 wmma
  *             tile, src/tcyield.cu:91-356). Operands are bf16 (uint16 bit
  *             patterns): A is M x K row-major and B is passed TRANSPOSED, as
  *             Bt = N x K row-major (C = A . Bt^T); C is fp32 M x N.

@@ -32,7 +32,7 @@ def test_engine_geometry():
     assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (128, 128, 32, 256)
     assert g.lds_bytes <= 160 * 1024
     g = apk_amd.geometry(apk_amd.ENGINE_BF16X256)
-    assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (256, 256, 32, 256)
+    assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (256, 256, 32, 512)
     assert (g.elem_bytes, g.b_transposed) == (2, 1)
     assert g.lds_bytes <= 160 * 1024
     with pytest.raises(apk_amd.ApkError):
@@ -106,7 +106,7 @@ def test_yield_rejects_bad_args():
     # accumulators (64 floats x 256 threads) + the two resident 32 KiB stages
     assert apk_amd.ckpt_floats(apk_amd.ENGINE_MFMA128) == 64 * 256 + 2 * 32 * 1024 // 4
     assert apk_amd.ckpt_floats(apk_amd.ENGINE_VALU64) == 16 * 256 + 2 * 16 * 1024 // 4
-    assert apk_amd.ckpt_floats(apk_amd.ENGINE_BF16X256) == 256 * 256 + 2 * 32 * 1024 // 4
+    assert apk_amd.ckpt_floats(apk_amd.ENGINE_BF16X256) == 128 * 512 + 2 * 32 * 1024 // 4
 
 
 def test_python_constants_match_header():

@@ -37,6 +37,19 @@ class _HipStream:
         self.cuda_stream = s.value
 
 
+_STREAMS = []
+
+
+def _streams():
+    """The background and urgent streams, created once per process: HIP maps
+    streams onto a few hardware queues (4 here), so a fifth stream shares a
+    queue with an earlier one and its work would wait behind that queue's
+    kernels -- the urgent stream must keep a hardware queue of its own."""
+    if not _STREAMS:
+        _STREAMS.extend([_HipStream(), _HipStream()])
+    return _STREAMS
+
+
 class RetreatJob:
     def __init__(self, torch, apk, engine, M, N, K, kc, Mu, Nu, Ku, passes, retreat, seed=21):
         T = torch
@@ -83,8 +96,7 @@ class RetreatJob:
         self.exec_count = T.zeros(self.num_tasks, dtype=i32, device="cuda")
         self.run_gt = T.zeros(2, dtype=i64, device="cuda")
         self.exit_count = T.zeros(1, dtype=i32, device="cuda")
-        self.bg = _HipStream()
-        self.us = _HipStream()
+        self.bg, self.us = _streams()
 
     def params(self, poll_every, resume, continuation, block_base):
         apk = self.apk
@@ -196,14 +208,10 @@ def test_retreat_bit_identical_exactly_once(fp32_job, apk, poll, resume, pe):
     assert (_bits(r["Cu"]) == _bits(fp32_job.uref)).all(), "urgent output differs"
 
 
-@pytest.mark.skip(reason="the bf16 preemptible kernel occupies the whole 512-register file of "
-                         "each SIMD, so the one-wave flag-raise kernel on the urgent stream is "
-                         "not dispatched until a background block exits (measured: raised after "
-                         "the background run ended)")
 def test_retreat_bf16(torch_gpu, apk):
     say("building bf16x256 retreat job M=N=1024 K=2048 kc=256")
     job = RetreatJob(torch_gpu, apk, apk.ENGINE_BF16X256, 1024, 1024, 2048, 256, 256, 256, 256,
-                     passes=64, retreat=2)
+                     passes=512, retreat=2)
     ref = job.run(apk.POLL_STAGE, apk.RESUME_CKPT_FULL, preempt=False)
     for resume in (apk.RESUME_CKPT_FULL, apk.RESUME_CKPT_ACC):
         _check(job, ref, job.run(apk.POLL_STAGE, resume))
