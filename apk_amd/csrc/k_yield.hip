@@ -323,7 +323,8 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
         // before the barrier above.
         const typename E::Dst d = E::stage_dst(ring_lds, ctx, ahead, s + 2);
         E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
-          if (s + 2 > S) return;
+          // carry implies s+1 < S: the sample is issued even when no stage
+          // s+2 exists (alone, for a site at the tile's last stage).
           if (POLL != APK_POLL_OFF && i == 0 && carry) {
             sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)ahead);
             lastSlot = ahead;
