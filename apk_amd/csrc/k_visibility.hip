@@ -17,6 +17,8 @@ __global__ void __launch_bounds__(256) k_visibility(const apk_vis_params P) {
   const int* myflag = (const int*)((const char*)P.flag + (size_t)(bid % copies) * APK_FLAG_STRIDE);
   const bool isSetter = bid == 0 && P.sched != nullptr;
   if (tid == 0) s_flag = 0;
+  if (tid == 0 && P.block_domain)
+    P.block_domain[bid] = (int)(xcc_id() * APK_SES_PER_XCD + se_id());
   pad[tid] = (float)tid;
   __syncthreads();
   int lastSeen = 0, nextEv = 0;
@@ -35,6 +37,9 @@ __global__ void __launch_bounds__(256) k_visibility(const apk_vis_params P) {
     if (tid == 0) {
       const int64_t t0 = wall_ticks();
       const int f = flag_load(myflag);
+      // The clock is read once the loaded value is in a register (the asm
+      // consumes it, so the compiler waits for the load first).
+      asm volatile("" : : "v"(f));
       const int64_t t1 = wall_ticks();
       ldSum += t1 - t0;
       ldMax = (t1 - t0) > ldMax ? (t1 - t0) : ldMax;

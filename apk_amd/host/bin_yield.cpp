@@ -240,6 +240,8 @@ int main(int argc, char** argv) {
     HIP_CHECK(hipMalloc(&dLd, (size_t)vBlocks * 16));
     HIP_CHECK(hipMalloc(&dTraffic, (size_t)trafficLen * 16));
     HIP_CHECK(hipMalloc(&dSink, (size_t)vBlocks * 256 * 4));
+    int* dDom;
+    HIP_CHECK(hipMalloc(&dDom, (size_t)vBlocks * 4));
     {
       std::vector<float> hT((size_t)trafficLen * 4);
       for (size_t i = 0; i < (size_t)trafficLen; ++i) {
@@ -272,6 +274,7 @@ int main(int argc, char** argv) {
     vp.sink = dSink;
     vp.iter_count = dIter;
     vp.load_ticks = dLd;
+    vp.block_domain = dDom;
     const int64_t t0 = now_ns();
     APK_CHECK(apk_visibility(&vp, vBlocks, ldsBytes, kStream));
     HIP_CHECK(hipStreamSynchronize(kStream));
@@ -283,6 +286,8 @@ int main(int argc, char** argv) {
     HIP_CHECK(hipMemcpy(hObs.data(), dObs, hObs.size() * 8, hipMemcpyDeviceToHost));
     HIP_CHECK(hipMemcpy(hIt.data(), dIter, (size_t)vBlocks * 8, hipMemcpyDeviceToHost));
     HIP_CHECK(hipMemcpy(hLd.data(), dLd, hLd.size() * 8, hipMemcpyDeviceToHost));
+    std::vector<int> hDom(vBlocks);
+    HIP_CHECK(hipMemcpy(hDom.data(), dDom, (size_t)vBlocks * 4, hipMemcpyDeviceToHost));
     std::vector<double> iters(hIt.begin(), hIt.end()), ldAvg, ldMax;
     for (int b = 0; b < vBlocks; ++b) {
       ldAvg.push_back(hIt[b] ? hLd[2 * b] / (double)hIt[b] / dev.wall_mhz : 0.0);
@@ -295,6 +300,8 @@ int main(int argc, char** argv) {
            percentile(ldAvg, 0.5), percentile(ldAvg, 0.99),
            *std::max_element(ldMax.begin(), ldMax.end()));
     std::vector<double> dmin, d50, d95, dmax;
+    // Per XCD: each event's latest observation among that XCD's blocks.
+    std::vector<std::vector<double>> xcdMax(APK_QUEUE_XCDS);
     int unset = 0, anomalies = 0;
     const double nsPerTick = 1000.0 / dev.wall_mhz;
     for (int e = 0; e < events; ++e) {
@@ -308,6 +315,13 @@ int main(int argc, char** argv) {
       }
       if (!complete) { ++anomalies; continue; }
       if (e < warmupEvents) continue;
+      std::vector<double> xm(APK_QUEUE_XCDS, -1.0);
+      for (int b = 0; b < vBlocks; ++b) {
+        const int x = (hDom[b] / APK_SES_PER_XCD) & (APK_QUEUE_XCDS - 1);
+        xm[x] = std::max(xm[x], d[b]);
+      }
+      for (int x = 0; x < APK_QUEUE_XCDS; ++x)
+        if (xm[x] >= 0) xcdMax[x].push_back(xm[x]);
       std::sort(d.begin(), d.end());
       dmin.push_back(d.front());
       d50.push_back(d[std::min((size_t)(0.5 * d.size()), d.size() - 1)]);
@@ -320,6 +334,15 @@ int main(int argc, char** argv) {
       printf("across-block delay (us): Dmin p50 %.2f | D50 p50 %.2f | D95 p50 %.2f | Dmax p50 "
              "%.2f | Dmax p99 %.2f\n", percentile(dmin, 0.5), percentile(d50, 0.5),
              percentile(d95, 0.5), percentile(dmax, 0.5), percentile(dmax, 0.99));
+    if (!dmax.empty()) {
+      // The setter is block 0; the flag is an agent-scope location, so every
+      // XCD's observation crosses the fabric.
+      printf("per-XCD latest observation (us, p50 over events; setter on XCD %d):",
+             (hDom[0] / APK_SES_PER_XCD) & (APK_QUEUE_XCDS - 1));
+      for (int x = 0; x < APK_QUEUE_XCDS; ++x)
+        if (!xcdMax[x].empty()) printf(" x%d %.2f", x, percentile(xcdMax[x], 0.5));
+      printf("\n");
+    }
     EventResult er;
     er.setGT = hSet;
     er.obs = hObs;

@@ -339,6 +339,7 @@ typedef struct apk_vis_params {
   float* sink;                 /* [blocks * 256] */
   long long* iter_count;       /* [blocks] iterations run */
   long long* load_ticks;       /* [blocks * 2]: sum and max of flag-load ticks */
+  int* block_domain;           /* optional [blocks]: xcd * APK_SES_PER_XCD + shader engine */
 } apk_vis_params;
 
 int apk_visibility(const apk_vis_params* params, int blocks, int lds_bytes, void* stream);
