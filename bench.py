@@ -189,6 +189,9 @@ def main():
                     help="arrivals for the cooperative latency sample")
     ap.add_argument("--trials", type=int, default=200,
                     help="arrivals for the retreat-arm and no-preemption samples")
+    ap.add_argument("--vendor-gemm", action="store_true",
+                    help="only time torch.matmul (rocBLAS/hipBLASLt) on the same shapes: bf16 "
+                         "8192^3 and fp32 4096^3, for comparison")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -205,6 +208,26 @@ def main():
     import apk_amd
 
     torch.cuda.set_device(0)
+    if args.vendor_gemm:
+        res = {}
+        for dt, n in ((torch.bfloat16, 8192), (torch.float32, 4096)):
+            a = torch.randn(n, n, device="cuda", dtype=dt)
+            b = torch.randn(n, n, device="cuda", dtype=dt)
+            for _ in range(3):
+                a @ b
+            torch.cuda.synchronize()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(10):
+                a @ b
+            e1.record()
+            torch.cuda.synchronize()
+            ms = e0.elapsed_time(e1) / 10
+            res[str(dt).split(".")[1]] = {"n": n, "ms": round(ms, 4),
+                                          "tflops": round(2 * n ** 3 / ms / 1e9, 1)}
+        print(json.dumps({"vendor_gemm": res}), flush=True)
+        return
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4
         src = torch.ones(n, dtype=torch.float32, device="cuda")
