@@ -144,15 +144,24 @@ __device__ __forceinline__ int wave_id() {
   return __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
 }
 // Direct-to-LDS 16-byte-per-lane buffer load with every address part but
-// the lane offset kept scalar: lane l's bytes land at LDS address lds + 16*l
-// (lds in M0), read from base + soff + voff. The stage loops issue eight of
-// these per k-stage between MFMAs, so each costs three scalar instructions.
-__device__ __forceinline__ void dma_x4(i32x4 rsrc, uint32_t lds, uint32_t voff, uint32_t soff) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+// the lane offset kept scalar: lane l's bytes land at LDS address
+// lds + off + 16*l, read from base + soff + voff. `off` must fold to a
+// compile-time constant (the load's place in a stage): M0 is then formed by
+// one scalar add, the only scalar instruction a load costs in the stage loops.
+__device__ __forceinline__ void dma_x4(i32x4 rsrc, uint32_t lds, uint32_t off, uint32_t voff,
+                                       uint32_t soff) {
+  asm volatile("s_add_u32 m0, %0, %1\n\tbuffer_load_dwordx4 %2, %3, %4 offen lds"
                :
-               : "s"(__builtin_amdgcn_readfirstlane(lds)), "v"(voff), "s"(rsrc),
+               : "s"(__builtin_amdgcn_readfirstlane(lds)), "i"(off), "v"(voff), "s"(rsrc),
                  "s"(__builtin_amdgcn_readfirstlane(soff))
-               : "memory");
+               : "memory", "scc");
+}
+// A scalar the optimiser must keep as computed: it can neither recompute it
+// at every use (as it would a readfirstlane of a thread-id expression inside
+// a loop) nor fold it into its uses.
+__device__ __forceinline__ uint32_t pinned_sgpr(uint32_t v) {
+  asm volatile("" : "+s"(v));
+  return v;
 }
 
 // One 16-byte-per-lane buffer load written straight into LDS: lane l's 16

@@ -90,46 +90,42 @@ struct EngBf16x256 {
   // Direct-to-LDS loads of one k-stage: load i (0..LOADS-1) fills the
   // 1 KiB piece i*8 + wave of the A stage (i < 2) or of the Bt stage, i.e.
   // 16 rows, row 128*i + 16*wave + lane/4, chunk slot lane%4. The swizzle of
-  // a row uses only its bits 2-3, so each lane's offset is fixed per tile
-  // (Lane) and load i and stage s only add scalar offsets.
+  // a row uses only its bits 2-3, so each lane's offset of load i is fixed
+  // per tile (Lane, one register per load) and stage s only adds scalar
+  // offsets.
   struct Lane {
-    uint32_t a, b;
+    uint32_t a[LOADS_A], b[LOADS_B];
   };
   static __device__ __forceinline__ Lane lane_offsets(const Ctx& c, int row0, int col0) {
     const int w = wave_id(), l = lane_id();
     const int r = w * 16 + (l >> 2);
     const int q = (l & 3) ^ swz(r);
-    return Lane{(uint32_t)(((row0 + r) * c.K + 8 * q) * 2),
-                (uint32_t)(((col0 + r) * c.K + 8 * q) * 2)};
+    const uint32_t a0 = (uint32_t)(((row0 + r) * c.K + 8 * q) * 2);
+    const uint32_t b0 = (uint32_t)(((col0 + r) * c.K + 8 * q) * 2);
+    Lane ln;
+#pragma unroll
+    for (int i = 0; i < LOADS_A; ++i) ln.a[i] = a0 + (uint32_t)(i * WAVES * 16) * (uint32_t)c.K * 2u;
+#pragma unroll
+    for (int i = 0; i < LOADS_B; ++i) ln.b[i] = b0 + (uint32_t)(i * WAVES * 16) * (uint32_t)c.K * 2u;
+    return ln;
   }
   // The scalar parts of the loads of stage s into ring slot `slot`, formed
-  // once per stage: this wave's 1 KiB piece of the slot (LDS) and the byte
-  // offset of k-stage s along a row.
+  // once per stage: this wave's 1 KiB piece of the slot (LDS; wave_lds is
+  // the piece in slot 0) and the byte offset of k-stage s along a row.
   struct Dst {
     uint32_t lds, k;
   };
-  static __device__ __forceinline__ Dst stage_dst(uint32_t ring_lds, const Ctx&, int slot,
+  static __device__ __forceinline__ Dst stage_dst(uint32_t wave_lds, const Ctx&, int slot,
                                                   int s) {
-    return Dst{(uint32_t)__builtin_amdgcn_readfirstlane(
-                   (int)(ring_lds + (uint32_t)(slot * STAGE) + (uint32_t)(wave_id() * 1024))),
-               (uint32_t)(s * KS * 2)};
+    return Dst{wave_lds + (uint32_t)(slot * STAGE), (uint32_t)(s * KS * 2)};
   }
   static __device__ __forceinline__ void issue_one(const Ctx& c, const Lane& ln, const Dst& d,
                                                    int i) {
     if (i < LOADS_A)
-      dma_x4(c.ra, d.lds + (uint32_t)(i * WAVES * 1024), ln.a,
-             d.k + (uint32_t)(i * WAVES * 16) * (uint32_t)c.K * 2u);
+      dma_x4(c.ra, d.lds, (uint32_t)(i * WAVES * 1024), ln.a[i], d.k);
     else
-      dma_x4(c.rb, d.lds + (uint32_t)(A_STAGE + (i - LOADS_A) * WAVES * 1024), ln.b,
-             d.k + (uint32_t)((i - LOADS_A) * WAVES * 16) * (uint32_t)c.K * 2u);
-  }
-  // All loads of stage s of the tile at (row0, col0) into ring slot `slot`.
-  static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot, int row0,
-                                               int col0, int s) {
-    const Lane ln = lane_offsets(c, row0, col0);
-    const Dst d = stage_dst(lds_addr_of(ring), c, slot, s);
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) issue_one(c, ln, d, i);
+      dma_x4(c.rb, d.lds, (uint32_t)(A_STAGE + (i - LOADS_A) * WAVES * 1024), ln.b[i - LOADS_A],
+             d.k);
   }
 
   // Operands of k-step j (16 k values): one 16-byte read per 32-row block of

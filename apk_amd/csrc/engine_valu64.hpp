@@ -65,47 +65,43 @@ struct EngValu64 {
   // Direct-to-LDS loads of one k-stage. A load i (< 2) fills the 1 KiB
   // piece i*4 + wave of the A stage: rows 32*i + 8*wave + lane/8, quad slot
   // lane%8; B load i fills rows 16*i + 4*wave + lane/16. The A swizzle uses
-  // row bits 2-4 only, so each lane's offset is fixed per tile (Lane) and
-  // load i and stage s only add scalar offsets.
+  // row bits 2-4 only, so each lane's offset of load i is fixed per tile
+  // (Lane, one register per load) and stage s only adds scalar offsets.
   struct Lane {
-    uint32_t a, b;
+    uint32_t a[LOADS_A], b[LOADS_B];
   };
   static __device__ __forceinline__ Lane lane_offsets(const Ctx& c, int row0, int col0) {
     const int w = wave_id(), l = lane_id();
     const int ra = w * 8 + (l >> 3);
     const int qa = (l & 7) ^ aswz(ra);
     const int rb = w * 4 + (l >> 4);
-    return Lane{(uint32_t)(((row0 + ra) * c.K + 4 * qa) * 4),
-                (uint32_t)((rb * c.N + col0 + 4 * (l & 15)) * 4)};
+    const uint32_t a0 = (uint32_t)(((row0 + ra) * c.K + 4 * qa) * 4);
+    const uint32_t b0 = (uint32_t)((rb * c.N + col0 + 4 * (l & 15)) * 4);
+    Lane ln;
+#pragma unroll
+    for (int i = 0; i < LOADS_A; ++i) ln.a[i] = a0 + (uint32_t)(i * 32) * (uint32_t)c.K * 4u;
+#pragma unroll
+    for (int i = 0; i < LOADS_B; ++i) ln.b[i] = b0 + (uint32_t)(i * 16) * (uint32_t)c.N * 4u;
+    return ln;
   }
   // The scalar parts of the loads of stage s into ring slot `slot`, formed
-  // once per stage: this wave's 1 KiB piece of the slot (LDS) and the byte
-  // offsets of k-stage s in A (along a row) and B (down the rows).
+  // once per stage: this wave's 1 KiB piece of the slot (LDS; wave_lds is
+  // the piece in slot 0) and the byte offsets of k-stage s in A (along a
+  // row) and B (down the rows).
   struct Dst {
     uint32_t lds, ka, kb;
   };
-  static __device__ __forceinline__ Dst stage_dst(uint32_t ring_lds, const Ctx& c, int slot,
+  static __device__ __forceinline__ Dst stage_dst(uint32_t wave_lds, const Ctx& c, int slot,
                                                   int s) {
     const uint32_t k0 = (uint32_t)(s * KS);
-    return Dst{(uint32_t)__builtin_amdgcn_readfirstlane(
-                   (int)(ring_lds + (uint32_t)(slot * STAGE) + (uint32_t)(wave_id() * 1024))),
-               k0 * 4u, k0 * (uint32_t)c.N * 4u};
+    return Dst{wave_lds + (uint32_t)(slot * STAGE), k0 * 4u, k0 * (uint32_t)c.N * 4u};
   }
   static __device__ __forceinline__ void issue_one(const Ctx& c, const Lane& ln, const Dst& d,
                                                    int i) {
     if (i < LOADS_A)
-      dma_x4(c.ra, d.lds + (uint32_t)(i * 4096), ln.a,
-             d.ka + (uint32_t)(i * 32) * (uint32_t)c.K * 4u);
+      dma_x4(c.ra, d.lds, (uint32_t)(i * 4096), ln.a[i], d.ka);
     else
-      dma_x4(c.rb, d.lds + (uint32_t)(A_STAGE + (i - LOADS_A) * 4096), ln.b,
-             d.kb + (uint32_t)((i - LOADS_A) * 16) * (uint32_t)c.N * 4u);
-  }
-  static __device__ __forceinline__ void issue(char* ring, const Ctx& c, int slot, int row0,
-                                               int col0, int s) {
-    const Lane ln = lane_offsets(c, row0, col0);
-    const Dst d = stage_dst(lds_addr_of(ring), c, slot, s);
-#pragma unroll
-    for (int i = 0; i < LOADS; ++i) issue_one(c, ln, d, i);
+      dma_x4(c.rb, d.lds, (uint32_t)(A_STAGE + (i - LOADS_A) * 4096), ln.b[i - LOADS_A], d.kb);
   }
 
   // One k-stage out of ring slot `slot`. `pre` runs first (flag check;

@@ -30,6 +30,7 @@ __global__ void __launch_bounds__(E::THREADS)
   const int nChunks = K / kChunk;
   const int spc = kChunk / E::KS;  // k-stages per chunk
   const typename E::Ctx ctx = E::make_ctx(A, B, M, N, K);
+  const uint32_t wl = wave_lds(ring);
 
   for (;;) {
     // Reconverge before the thread-0 pop (no thread-0 region of the previous
@@ -48,7 +49,7 @@ __global__ void __launch_bounds__(E::THREADS)
 
     typename E::Acc acc;
     E::zero(acc);
-    run_stages<E>(ring, ctx, acc, row0, col0, K / E::KS, [&](int s) {
+    run_stages<E>(ring, wl, ctx, acc, row0, col0, K / E::KS, [&](int s) {
       if (threadIdx.x == 0 && rec && s % spc == 0) {
         const int64_t now = wall_ticks();
         const int c = s / spc;

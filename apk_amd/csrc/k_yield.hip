@@ -75,7 +75,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   const bool isSetter = P().flag_set != nullptr && P().sched != nullptr && bid == 0;
   constexpr bool retreatArm = RETREAT && POLL != APK_POLL_OFF;
 
-  const uint32_t ring_lds = lds_addr_of(ring);
+  const uint32_t wl = wave_lds(ring);
   const uint32_t flag_lds = lds_addr_of(flagring);
   if (tid < E::NS) flagring[tid] = 0;
   if (tid < APK_STATS_PER_BLOCK) s_stats[tid] = 0;
@@ -247,14 +247,14 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     // costs two scalar compares. The sample a site s reads is issued
     // in front of the data loads of stage s+1, i.e. right behind stage s's
     // own loads, so the ordinary "stage s landed" wait retires it too. For a
-    // site at the tile's last stage the sample is issued alone, in place of
-    // stage S.
+    // site at the tile's last stage the sample goes out in front of the
+    // refetch that stands in for stage S.
     auto issue_stage = [&](int t, int tslot, bool carry) {
       if (POLL != APK_POLL_OFF && carry) {
         sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)tslot);
         lastSlot = tslot;
       }
-      if (t < S) E::issue(ring, ctx, tslot, row0, col0, t);
+      issue_loads<E>(ctx, ln, E::stage_dst(wl, ctx, tslot, fetched_stage(t, S)));
     };
 
     bool retreated = false, yielded = false;
@@ -268,7 +268,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
           issue_stage(s + 1, next_slot(slot), pollable);  // s is a site
           if (urgent && P().poison) {
             // Test hook: corrupt the staged B[0][col0] of the urgent tile.
-            wait_landed<E>(S > 1);
+            wait_landed<E>();
             lds_sync();
             if (tid == 0) *(float*)(ring + E::A_STAGE) += 1.0f;
             lds_sync();
@@ -282,7 +282,9 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
           const int live = (S - s) < 2 ? (S - s) : 2;
           if (srcKind == FULL) {
             Ckpt<E>::load_ring(ring, src, slot, live);
-            issue_stage(S, next_slot(slot), true);  // sample alone
+            // The sample alone: both live slots now hold restored stages.
+            sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)next_slot(slot));
+            lastSlot = next_slot(slot);
             wait_vmcnt<0>();
             __syncthreads();  // restored ring visible to all waves
           } else {
@@ -299,7 +301,7 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
       bool atSite = false;
       int fSeen = 0;
       while (s < S) {
-        wait_landed<E>(s + 1 < S);
+        wait_landed<E>();
         lds_sync();
         // Poll site: the flag sample issued in front of stage s+1's loads has
         // landed with stage s. A new generation (or the setter's turn) ends
@@ -321,15 +323,13 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
         // Stage s+2 (and the sample for a site at s+1) goes out under stage
         // s's matrix work; its slot held stage s-1, which every wave finished
         // before the barrier above.
-        const typename E::Dst d = E::stage_dst(ring_lds, ctx, ahead, s + 2);
+        const typename E::Dst d = E::stage_dst(wl, ctx, ahead, fetched_stage(s + 2, S));
         E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
-          // carry implies s+1 < S: the sample is issued even when no stage
-          // s+2 exists (alone, for a site at the tile's last stage).
           if (POLL != APK_POLL_OFF && i == 0 && carry) {
             sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)ahead);
             lastSlot = ahead;
           }
-          if (s + 2 < S) E::issue_one(ctx, ln, d, i);
+          E::issue_one(ctx, ln, d, i);
         });
         slot = next_slot(slot);
         ++s;
@@ -448,7 +448,8 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
     }
     if (retreated) break;  // the block exits; its tile waits in the resume queue
     if (yielded) continue;  // the event's urgent tiles first, then this tile again
-    lds_sync();  // every wave done with the ring; every sample has landed
+    wait_vmcnt<0>();  // the refetches past the tile's end have landed
+    lds_sync();       // every wave done with the ring; every sample has landed
     if (POLL != APK_POLL_OFF && lastSlot >= 0) fLatest = uniform(flagring[lastSlot]);
 
     // ---- epilogue: C tile, fingerprint, exactly-once count ----

@@ -117,41 +117,56 @@ __device__ __forceinline__ int rq_wait_ready(int* en) {
 //             lds_sync: stage s is visible to every wave, and every wave has
 //             finished computing stage s-1, so its slot, (s+2) % 3, is free;
 //             compute(s), with issue(s+2) folded in after its first reads.
-//   end       lds_sync before the ring is used for anything else.
-// When stage s is waited for, only the loads of stage s+1 (and nothing a
-// wave must read) have been issued after it, and vmcnt retires in issue
-// order, so "stage s landed" is vmcnt <= LOADS.
-template <class E>
-__device__ __forceinline__ void wait_landed(bool next_in_flight) {
-  static_assert(E::NS == 3, "ring of 3");
-  if (next_in_flight) wait_vmcnt<E::LOADS>();
-  else wait_vmcnt<0>();
-}
-
+//   end       wait for every load, lds_sync before the ring is used for
+//             anything else.
+// Every stage issues its LOADS loads, also past the tile's end: issue(t) for
+// t >= S fetches stage S-1 again into the free slot, where nothing reads it.
+// So the loop carries no branch per load, and when stage s is waited for,
+// exactly the loads of stage s+1 (and nothing a wave must read) have been
+// issued after it: vmcnt retires in issue order, so "stage s landed" is
+// always vmcnt <= LOADS.
 __device__ __forceinline__ int next_slot(int slot) { return slot == 2 ? 0 : slot + 1; }
 __device__ __forceinline__ int slot_after_next(int slot) { return slot == 0 ? 2 : slot - 1; }
+// The k-stage that issue(t) fetches.
+__device__ __forceinline__ int fetched_stage(int t, int S) { return t < S ? t : S - 1; }
+// This wave's 1 KiB piece of ring slot 0 (the LDS base of its stage loads),
+// formed once per kernel.
+__device__ __forceinline__ uint32_t wave_lds(const char* ring) {
+  return pinned_sgpr((uint32_t)__builtin_amdgcn_readfirstlane(
+      (int)(lds_addr_of(ring) + (uint32_t)(wave_id() * 1024))));
+}
+template <class E>
+__device__ __forceinline__ void issue_loads(const typename E::Ctx& c, const typename E::Lane& ln,
+                                            const typename E::Dst& d) {
+#pragma unroll
+  for (int i = 0; i < E::LOADS; ++i) E::issue_one(c, ln, d, i);
+}
+template <class E>
+__device__ __forceinline__ void wait_landed() {
+  static_assert(E::NS == 3, "ring of 3");
+  wait_vmcnt<E::LOADS>();
+}
 
 // Non-preemptible K loop over stages [0, S) of one tile. hook(s) runs
 // uniformly at the top of stage s.
 template <class E, class Hook>
-__device__ __forceinline__ void run_stages(char* ring, const typename E::Ctx& c,
-                                           typename E::Acc& acc, int row0, int col0,
-                                           int S, Hook&& hook) {
-  E::issue(ring, c, 0, row0, col0, 0);
-  if (S > 1) E::issue(ring, c, 1, row0, col0, 1);
+__device__ __forceinline__ void run_stages(char* ring, uint32_t wl, const typename E::Ctx& c,
+                                           typename E::Acc& acc, int row0, int col0, int S,
+                                           Hook&& hook) {
   const typename E::Lane ln = E::lane_offsets(c, row0, col0);
-  const uint32_t rl = lds_addr_of(ring);
+  issue_loads<E>(c, ln, E::stage_dst(wl, c, 0, 0));
+  issue_loads<E>(c, ln, E::stage_dst(wl, c, 1, fetched_stage(1, S)));
   int slot = 0;
   for (int s = 0; s < S; ++s) {
     hook(s);
-    wait_landed<E>(s + 1 < S);
+    wait_landed<E>();
     lds_sync();
-    const typename E::Dst d = E::stage_dst(rl, c, slot_after_next(slot), s + 2);
-    E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
-      if (s + 2 < S) E::issue_one(c, ln, d, i);
-    });
+    const typename E::Dst d =
+        E::stage_dst(wl, c, slot_after_next(slot), fetched_stage(s + 2, S));
+    E::compute(ring, slot, acc, [] { return true; }, [&](int i) { E::issue_one(c, ln, d, i); });
     slot = next_slot(slot);
   }
+  wait_vmcnt<0>();
   lds_sync();
 }
 

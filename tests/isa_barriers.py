@@ -66,8 +66,10 @@ def vm_waits_in_compute_blocks(asm_text, min_math=32):
     basic blocks that carry the k-stage math (>= min_math MFMA/FMA ops).
 
     The stage loops keep two stages of direct-to-LDS loads in flight and wait
-    for them explicitly before the barrier; a vmcnt wait inside the compute
-    block itself drains the prefetch on every stage.
+    for the oldest one explicitly, with a nonzero count, right before the
+    stage barrier; when the whole stage is one basic block that wait is in
+    it. Any other vmcnt wait in a compute block (after the barrier, a second
+    one, or a full drain) empties the prefetch on every stage.
     """
     out = []
     kernel, label, lines = None, None, []
@@ -75,9 +77,20 @@ def vm_waits_in_compute_blocks(asm_text, min_math=32):
     def flush():
         math = sum(1 for l in lines if re.search(r'\bv_(mfma|fmac_f32|fma_f32)', l))
         if math >= min_math:
+            pending, accepted, math_seen = None, False, False
             for l in lines:
-                if re.search(r's_waitcnt\b.*vmcnt', l):
-                    out.append((kernel, label, l.strip()))
+                if re.search(r'\bv_(mfma|fmac_f32|fma_f32)', l):
+                    math_seen = True
+                if re.search(r'\bs_barrier\b', l) and pending and not math_seen:
+                    pending, accepted = None, True  # the stage wait
+                m = re.search(r's_waitcnt\b.*vmcnt\((\d+)\)', l)
+                if m:
+                    if pending is None and not accepted and not math_seen and int(m.group(1)) > 0:
+                        pending = l.strip()
+                    else:
+                        out.append((kernel, label, l.strip()))
+            if pending:
+                out.append((kernel, label, pending))
 
     for l in asm_text.split('\n'):
         mk = re.match(r'^(_Z\w+):', l)
