@@ -1,6 +1,7 @@
 // engine_bf16x256.hpp -- 256x256 output tile of a bf16 GEMM with fp32
 // accumulation on the gfx950 matrix cores (v_mfma_f32_32x32x16_bf16), fed by
-// a 3-stage LDS ring of buffer_load_dwordx4 ... lds (direct-to-LDS).
+// a 4-slot LDS ring of buffer_load_dwordx4 ... lds (direct-to-LDS) that is
+// synchronised once per pair of k-stages.
 //
 // Operands: A is M x K row-major bf16; B is passed transposed, Bt = N x K
 // row-major bf16 (C = A . Bt^T), so that both operands are k-contiguous in
@@ -14,7 +15,13 @@
 // kernel on another stream (the flag raise of the retreat arm) still finds
 // registers on every CU.
 // Stage: k depth KS=32 -> A stage 256 rows x 64 B (16 KiB) + Bt stage 256
-// rows x 64 B (16 KiB); 3 stages = 96 KiB of the 160 KiB LDS (1 block/CU).
+// rows x 64 B (16 KiB); 4 slots = 128 KiB of the 160 KiB LDS (1 block/CU).
+// A k-stage is only 16 MFMAs per wave (1024 matrix-pipe cycles per SIMD),
+// and every barrier costs a fixed ~560 cycles per SIMD (all waves arrive,
+// then wait for their first operands): the stage loops therefore take the
+// stages in pairs (GROUP = 2), one barrier per pair, with the next pair's
+// loads issued under the current pair's first stage. A tile of odd length
+// ends with a pair whose second stage is all zeros.
 //
 // LDS layout (both operands): row r of a stage is 64 B = four 16-byte
 // chunks; chunk q is stored at slot q ^ swz(r), swz(r) = (r >> 2) & 3. A
@@ -29,7 +36,7 @@
 // output's sum is formed in the same order whatever worker computes it and
 // however often it is checkpointed and resumed.
 //
-// Epilogue: the fp32 tile (256 KiB) does not fit the 96 KiB ring, so it is
+// Epilogue: the fp32 tile (256 KiB) does not fit the 128 KiB ring, so it is
 // staged in 4 passes of 64 rows (32 rows of each wave row): the waves write
 // one 32x32 accumulator row block each into LDS, then the whole block moves
 // the 64 rows to C with 16-byte coalesced stores (and fingerprints them).
@@ -41,7 +48,7 @@ namespace apk {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 struct EngBf16x256 {
-  static constexpr int TM = 256, TN = 256, KS = 32, NS = 3, THREADS = 512;
+  static constexpr int TM = 256, TN = 256, KS = 32, NS = 4, GROUP = 2, THREADS = 512;
   static constexpr int ROW_BYTES = KS * 2;                  // 64 B
   static constexpr int A_STAGE = TM * ROW_BYTES;            // 16 KiB
   static constexpr int B_STAGE = TN * ROW_BYTES;            // 16 KiB
@@ -109,22 +116,32 @@ struct EngBf16x256 {
     for (int i = 0; i < LOADS_B; ++i) ln.b[i] = b0 + (uint32_t)(i * WAVES * 16) * (uint32_t)c.K * 2u;
     return ln;
   }
-  // The scalar parts of the loads of stage s into ring slot `slot`, formed
+  // The scalar parts of the loads of stage t into ring slot `slot`, formed
   // once per stage: this wave's 1 KiB piece of the slot (LDS; wave_lds is
-  // the piece in slot 0) and the byte offset of k-stage s along a row.
+  // the piece in slot 0), the byte offset of k-stage t along a row, and the
+  // operand resources. A stage past the tile's end (t >= S) is read through
+  // resources of zero length: every lane reads zeros and no memory is
+  // touched, so the slot holds a stage of zeros (the second stage of a last
+  // pair of an odd-length tile is computed on it and adds nothing).
   struct Dst {
     uint32_t lds, k;
+    i32x4 ra, rb;
   };
-  static __device__ __forceinline__ Dst stage_dst(uint32_t wave_lds, const Ctx&, int slot,
-                                                  int s) {
-    return Dst{wave_lds + (uint32_t)(slot * STAGE), (uint32_t)(s * KS * 2)};
+  static __device__ __forceinline__ Dst stage_dst(uint32_t wave_lds, const Ctx& c, int slot,
+                                                  int t, int S) {
+    const bool real = t < S;
+    i32x4 za = c.ra, zb = c.rb;
+    za.z = 0;
+    zb.z = 0;
+    return Dst{wave_lds + (uint32_t)(slot * STAGE), (uint32_t)((real ? t : 0) * KS * 2),
+               real ? c.ra : za, real ? c.rb : zb};
   }
-  static __device__ __forceinline__ void issue_one(const Ctx& c, const Lane& ln, const Dst& d,
+  static __device__ __forceinline__ void issue_one(const Ctx&, const Lane& ln, const Dst& d,
                                                    int i) {
     if (i < LOADS_A)
-      dma_x4(c.ra, d.lds, (uint32_t)(i * WAVES * 1024), ln.a[i], d.k);
+      dma_x4(d.ra, d.lds, (uint32_t)(i * WAVES * 1024), ln.a[i], d.k);
     else
-      dma_x4(c.rb, d.lds, (uint32_t)(A_STAGE + (i - LOADS_A) * WAVES * 1024), ln.b[i - LOADS_A],
+      dma_x4(d.rb, d.lds, (uint32_t)(A_STAGE + (i - LOADS_A) * WAVES * 1024), ln.b[i - LOADS_A],
              d.k);
   }
 
@@ -152,33 +169,37 @@ struct EngBf16x256 {
 
   static constexpr int J = KS / 16;  // MFMA k-steps per stage
 
-  // One k-stage out of ring slot `slot`. `pre` runs first (returning false
-  // abandons the stage before any accumulator changes); `mid(i)`, i = 0..
-  // LOADS-1, runs after MFMA 2i+1 of the first k-step -- the stage loops
-  // issue the next-but-one stage's direct-to-LDS load i there, one per two
-  // MFMAs.
+  // One group: the GROUP = 2 k-stages in ring slots slot and slot+1 (one
+  // half of the ring, contiguous in LDS), as one sequence of 2*J MFMA
+  // k-steps in ascending k, the operands of k-step j+1 read while k-step j's
+  // MFMAs run -- across the stage boundary too. `pre` runs first (returning
+  // false abandons the group before any accumulator changes); `mid(i)`,
+  // i = 0..GROUP*LOADS-1, runs after MFMA 2i+1 of the group (k-step i/4,
+  // MFMA 2(i%4)+1): the stage loops issue the next group's direct-to-LDS
+  // load i there, one per two MFMAs.
   template <class Pre, class Mid>
   static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
                                                  Pre&& pre, Mid&& mid) {
-    const char* abase = ring + slot * STAGE;
+    const char* gbase = ring + slot * STAGE;
+    constexpr int JG = J * GROUP;
     Frag f[2];
     // pre() runs before any operand is in registers: a yield inside it
     // (checkpoint, urgent tiles, restore) then needs only the accumulators
     // live, which keeps the kernel within the register file.
     if (!pre()) return false;
-    load_frag(abase, 0, f[0]);
+    load_frag(gbase, 0, f[0]);
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-      if (j + 1 < J) load_frag(abase, j + 1, f[(j + 1) & 1]);
+    for (int j = 0; j < JG; ++j) {
+      if (j + 1 < JG) load_frag(gbase + ((j + 1) / J) * STAGE, (j + 1) % J, f[(j + 1) & 1]);
       const Frag& c = f[j & 1];
 #pragma unroll
       for (int m = 0; m < 8; ++m) {
         const int rb = m >> 1, cb = m & 1;
         acc.c[rb][cb] =
             __builtin_amdgcn_mfma_f32_32x32x16_bf16(c.a[rb], c.b[cb], acc.c[rb][cb], 0, 0, 0);
-        if (j == 0 && (m & 1) && (m >> 1) < LOADS) {
+        if ((m & 1) && j * 4 + (m >> 1) < GROUP * LOADS) {
           __builtin_amdgcn_sched_barrier(0);
-          mid(m >> 1);
+          mid(j * 4 + (m >> 1));
           __builtin_amdgcn_sched_barrier(0);
         }
       }

@@ -31,7 +31,7 @@
 namespace apk {
 
 struct EngMfma128 {
-  static constexpr int TM = 128, TN = 128, KS = 32, NS = 3, THREADS = 256;
+  static constexpr int TM = 128, TN = 128, KS = 32, NS = 3, GROUP = 1, THREADS = 256;
   static constexpr int A_STAGE = TM * KS * 4;               // bytes
   static constexpr int B_STAGE = KS * TN * 4;               // bytes
   static constexpr int STAGE = A_STAGE + B_STAGE;           // 32 KiB
@@ -99,16 +99,18 @@ struct EngMfma128 {
     for (int i = 0; i < LOADS_B; ++i) ln.b[i] = b0 + (uint32_t)(i * 8) * (uint32_t)c.N * 4u;
     return ln;
   }
-  // The scalar parts of the loads of stage s into ring slot `slot`, formed
+  // The scalar parts of the loads of stage t into ring slot `slot`, formed
   // once per stage: this wave's 1 KiB piece of the slot (LDS; wave_lds is
-  // the piece in slot 0) and the byte offsets of k-stage s in A (along a
+  // the piece in slot 0) and the byte offsets of k-stage t in A (along a
   // row) and B (down the rows).
   struct Dst {
     uint32_t lds, ka, kb;
   };
+  // A stage past the tile's end (t >= S) fetches stage S-1 again: nothing
+  // reads that slot before it is refilled.
   static __device__ __forceinline__ Dst stage_dst(uint32_t wave_lds, const Ctx& c, int slot,
-                                                  int s) {
-    const uint32_t k0 = (uint32_t)(s * KS);
+                                                  int t, int S) {
+    const uint32_t k0 = (uint32_t)((t < S ? t : S - 1) * KS);
     return Dst{wave_lds + (uint32_t)(slot * STAGE), k0 * 4u, k0 * (uint32_t)c.N * 4u};
   }
   static __device__ __forceinline__ void issue_one(const Ctx& c, const Lane& ln, const Dst& d,

@@ -67,9 +67,13 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
   };
   auto copies = [&] { return P().flag_copies > 0 ? P().flag_copies : 1; };
   auto row = [&] { return P().block_base + bid; };  // this block's stats / obs column
-  const int pollStride = (POLL == APK_POLL_STAGE)
-                             ? 1
-                             : (P().k_chunk / E::KS) * (P().poll_every > 0 ? P().poll_every : 1);
+  // Poll sites sit at barriers: every GROUP-th k-stage at the finest.
+  const int pollStride = [&] {
+    const int st = (POLL == APK_POLL_STAGE)
+                       ? 1
+                       : (P().k_chunk / E::KS) * (P().poll_every > 0 ? P().poll_every : 1);
+    return (st + E::GROUP - 1) / E::GROUP * E::GROUP;
+  }();
   const i32x4 flag_rsrc =
       make_rsrc((const char*)P().flag + (size_t)(bid % copies()) * APK_FLAG_STRIDE, 4);
   const bool isSetter = P().flag_set != nullptr && P().sched != nullptr && bid == 0;
@@ -244,17 +248,22 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
 
     // Poll sites are the stages s with s % pollStride == 0; `nextSite` is the
     // next one not yet passed (an urgent tile never reaches one), so a stage
-    // costs two scalar compares. The sample a site s reads is issued
-    // in front of the data loads of stage s+1, i.e. right behind stage s's
-    // own loads, so the ordinary "stage s landed" wait retires it too. For a
-    // site at the tile's last stage the sample goes out in front of the
-    // refetch that stands in for stage S.
-    auto issue_stage = [&](int t, int tslot, bool carry) {
-      if (POLL != APK_POLL_OFF && carry) {
-        sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)tslot);
-        lastSlot = tslot;
+    // costs two scalar compares. The sample a site s reads lands in
+    // flagring[site_flag(slot of s)]: with one barrier per stage it is
+    // issued in front of the data loads of stage s+1, right behind stage s's
+    // own loads, so the ordinary "stage s landed" wait retires it too; with
+    // one barrier per pair it goes out in front of the pair's loads, which
+    // are all waited for. For a site at the tile's last stage the sample
+    // goes out in front of the refetch that stands in for stage S.
+    auto site_flag = [](int sl) { return E::GROUP == 1 ? next_slot<E>(sl) : sl; };
+    auto sample = [&](int idx) {
+      if (POLL != APK_POLL_OFF) {
+        sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)idx);
+        lastSlot = idx;
       }
-      issue_loads<E>(ctx, ln, E::stage_dst(wl, ctx, tslot, fetched_stage(t, S)));
+    };
+    auto issue_stage = [&](int t, int tslot) {
+      issue_loads<E>(ctx, ln, E::stage_dst(wl, ctx, tslot, t, S));
     };
 
     bool retreated = false, yielded = false;
@@ -264,8 +273,9 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
         const int64_t tIn = wall_ticks();
         if (srcKind == FRESH) {
           E::zero(acc);
-          issue_stage(s, slot, false);
-          issue_stage(s + 1, next_slot(slot), pollable);  // s is a site
+          issue_stage(s, slot);
+          if (pollable) sample(site_flag(slot));  // s is a site
+          issue_stage(s + 1, next_slot<E>(slot));
           if (urgent && P().poison) {
             // Test hook: corrupt the staged B[0][col0] of the urgent tile.
             wait_landed<E>();
@@ -279,17 +289,17 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
           // site at s gets a fresh sample.
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
           Ckpt<E>::load_acc(acc, src);
-          const int live = (S - s) < 2 ? (S - s) : 2;
+          const int live = (E::GROUP == 2 || S - s >= 2) ? 2 : S - s;
           if (srcKind == FULL) {
             Ckpt<E>::load_ring(ring, src, slot, live);
             // The sample alone: both live slots now hold restored stages.
-            sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)next_slot(slot));
-            lastSlot = next_slot(slot);
+            sample(site_flag(slot));
             wait_vmcnt<0>();
             __syncthreads();  // restored ring visible to all waves
           } else {
-            issue_stage(s, slot, false);
-            issue_stage(s + 1, next_slot(slot), true);
+            issue_stage(s, slot);
+            sample(site_flag(slot));
+            issue_stage(s + 1, next_slot<E>(slot));
           }
           if (tid == 0 && src == ckslot()) stat(ST_RESTORE, (uint64_t)(wall_ticks() - tIn));
         }
@@ -303,12 +313,13 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
       while (s < S) {
         wait_landed<E>();
         lds_sync();
-        // Poll site: the flag sample issued in front of stage s+1's loads has
-        // landed with stage s. A new generation (or the setter's turn) ends
-        // the loop here, before stage s is computed.
+        // Poll site: the flag sample for site s has landed with stage s (it
+        // was issued in front of the loads of stage s+1, or of the pair s).
+        // A new generation (or the setter's turn) ends the loop here, before
+        // stage s is computed.
         if (POLL != APK_POLL_OFF && s == nextSite) {
           if (s != siteDone) {
-            const int f = uniform(flagring[next_slot(slot)]);
+            const int f = uniform(flagring[site_flag(slot)]);
             fLatest = f;
             if (f != lastSeen || isSetter) {
               fSeen = f;
@@ -318,21 +329,34 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
           }
           nextSite += pollStride;
         }
-        const int ahead = slot_after_next(slot);
-        const bool carry = s + 1 == nextSite;  // s+1 is a site
-        // Stage s+2 (and the sample for a site at s+1) goes out under stage
-        // s's matrix work; its slot held stage s-1, which every wave finished
-        // before the barrier above.
-        const typename E::Dst d = E::stage_dst(wl, ctx, ahead, fetched_stage(s + 2, S));
-        E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
-          if (POLL != APK_POLL_OFF && i == 0 && carry) {
-            sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)ahead);
-            lastSlot = ahead;
-          }
-          E::issue_one(ctx, ln, d, i);
-        });
-        slot = next_slot(slot);
-        ++s;
+        if constexpr (E::GROUP == 1) {
+          const int ahead = slot_after_next(slot);
+          const bool carry = s + 1 == nextSite;  // s+1 is a site
+          // Stage s+2 (and the sample for a site at s+1) goes out under stage
+          // s's matrix work; its slot held stage s-1, which every wave
+          // finished before the barrier above.
+          const typename E::Dst d = E::stage_dst(wl, ctx, ahead, s + 2, S);
+          E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
+            if (i == 0 && carry) sample(ahead);
+            E::issue_one(ctx, ln, d, i);
+          });
+          slot = next_slot<E>(slot);
+          ++s;
+        } else {
+          // Stages s and s+1 are computed as one group; stages s+2, s+3 (and
+          // the sample for a site at s+2) go out under its first stage, into
+          // the other half of the ring, which held the previous pair.
+          const int other = slot ^ 2;
+          const bool carry = s + 2 == nextSite;
+          const typename E::Dst d0 = E::stage_dst(wl, ctx, other, s + 2, S);
+          const typename E::Dst d1 = E::stage_dst(wl, ctx, other + 1, s + 3, S);
+          E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
+            if (i == 0 && carry) sample(other);
+            issue_group_one<E>(ctx, ln, d0, d1, i);
+          });
+          slot = other;
+          s += 2;
+        }
       }
       if (!atSite) break;  // the tile is computed
 
@@ -398,7 +422,9 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
       // ---- checkpoint: accumulators and the live stages s, s+1 ----
       lds_sync();
       const int64_t tSave = wall_ticks();
-      const int live = (S - s) < 2 ? (S - s) : 2;  // resident, not computed
+      // Resident, not computed; with pairs the zero stage after an odd
+      // tile's last stage is kept too (the pair is computed as a whole).
+      const int live = (E::GROUP == 2 || S - s >= 2) ? 2 : S - s;
       if (P().resume != APK_RESUME_RESTART) {
         Ckpt<E>::save_acc(acc, dst);
         if (P().resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, dst, slot, live);
@@ -433,7 +459,8 @@ __global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield
             P().claim_site[ev] = s;
             P().u_gt[2 * (size_t)ev] = t1;
           }
-          stat(ST_INFLIGHT, live > 1 ? 1 : 0);  // stage s+1 was issued, not waited for
+          // Stage s+1 was issued, not waited for (one barrier per stage).
+          stat(ST_INFLIGHT, E::GROUP == 1 && live > 1 ? 1 : 0);
           stat(ST_SAVE, (uint64_t)(t1 - tSave));
         }
         serving = ev;

@@ -110,25 +110,33 @@ __device__ __forceinline__ int rq_wait_ready(int* en) {
 }
 
 // ---------------------------------------------------------------------------
-// The ring protocol of every stage loop here (NS = 3 slots, one barrier per
-// k-stage):
+// The ring protocol of every stage loop here. GROUP = 1 (NS = 3 slots, one
+// barrier per k-stage):
 //   prologue  issue(0), issue(1)
 //   stage s   wait until stage s has landed (stage s+1 may stay in flight);
 //             lds_sync: stage s is visible to every wave, and every wave has
 //             finished computing stage s-1, so its slot, (s+2) % 3, is free;
 //             compute(s), with issue(s+2) folded in after its first reads.
+// GROUP = 2 (NS = 4 slots in two halves, one barrier per pair of stages):
+//   prologue  issue(0), issue(1)
+//   pair s    (s even) wait until stages s and s+1 have landed (nothing else
+//             is in flight); lds_sync: both visible, and every wave has
+//             finished the previous pair, so the other half is free;
+//             compute(s, s+1) as one group, with issue(s+2) and issue(s+3)
+//             folded in. A tile of odd length S ends with the pair (S-1, S),
+//             stage S all zeros.
 //   end       wait for every load, lds_sync before the ring is used for
 //             anything else.
 // Every stage issues its LOADS loads, also past the tile's end: issue(t) for
-// t >= S fetches stage S-1 again into the free slot, where nothing reads it.
-// So the loop carries no branch per load, and when stage s is waited for,
-// exactly the loads of stage s+1 (and nothing a wave must read) have been
-// issued after it: vmcnt retires in issue order, so "stage s landed" is
-// always vmcnt <= LOADS.
-__device__ __forceinline__ int next_slot(int slot) { return slot == 2 ? 0 : slot + 1; }
+// t >= S fills a free slot that nothing reads (a refetch of stage S-1), or,
+// for GROUP = 2, with zeros that the second half of a tile's last pair may
+// be computed on. So the loops carry no branch per load, and the wait at the top is always
+// the same: vmcnt <= LOADS for GROUP = 1 (exactly the loads of stage s+1,
+// and nothing a wave must read, were issued after stage s's; vmcnt retires
+// in issue order), vmcnt = 0 for GROUP = 2.
+template <class E>
+__device__ __forceinline__ int next_slot(int slot) { return slot + 1 == E::NS ? 0 : slot + 1; }
 __device__ __forceinline__ int slot_after_next(int slot) { return slot == 0 ? 2 : slot - 1; }
-// The k-stage that issue(t) fetches.
-__device__ __forceinline__ int fetched_stage(int t, int S) { return t < S ? t : S - 1; }
 // This wave's 1 KiB piece of ring slot 0 (the LDS base of its stage loads),
 // formed once per kernel.
 __device__ __forceinline__ uint32_t wave_lds(const char* ring) {
@@ -143,28 +151,49 @@ __device__ __forceinline__ void issue_loads(const typename E::Ctx& c, const type
 }
 template <class E>
 __device__ __forceinline__ void wait_landed() {
-  static_assert(E::NS == 3, "ring of 3");
-  wait_vmcnt<E::LOADS>();
+  static_assert((E::GROUP == 1 && E::NS == 3) || (E::GROUP == 2 && E::NS == 4), "ring shape");
+  if constexpr (E::GROUP == 1) wait_vmcnt<E::LOADS>();
+  else wait_vmcnt<0>();
+}
+// Load i (< GROUP * LOADS) of the next group's stages: d0 for the first
+// stage, d1 for the second.
+template <class E>
+__device__ __forceinline__ void issue_group_one(const typename E::Ctx& c,
+                                                const typename E::Lane& ln,
+                                                const typename E::Dst& d0,
+                                                const typename E::Dst& d1, int i) {
+  if (i < E::LOADS) E::issue_one(c, ln, d0, i);
+  else E::issue_one(c, ln, d1, i - E::LOADS);
 }
 
 // Non-preemptible K loop over stages [0, S) of one tile. hook(s) runs
-// uniformly at the top of stage s.
+// uniformly before stage s is computed.
 template <class E, class Hook>
 __device__ __forceinline__ void run_stages(char* ring, uint32_t wl, const typename E::Ctx& c,
                                            typename E::Acc& acc, int row0, int col0, int S,
                                            Hook&& hook) {
   const typename E::Lane ln = E::lane_offsets(c, row0, col0);
-  issue_loads<E>(c, ln, E::stage_dst(wl, c, 0, 0));
-  issue_loads<E>(c, ln, E::stage_dst(wl, c, 1, fetched_stage(1, S)));
+  issue_loads<E>(c, ln, E::stage_dst(wl, c, 0, 0, S));
+  issue_loads<E>(c, ln, E::stage_dst(wl, c, 1, 1, S));
   int slot = 0;
-  for (int s = 0; s < S; ++s) {
+  for (int s = 0; s < S; s += E::GROUP) {
     hook(s);
     wait_landed<E>();
     lds_sync();
-    const typename E::Dst d =
-        E::stage_dst(wl, c, slot_after_next(slot), fetched_stage(s + 2, S));
-    E::compute(ring, slot, acc, [] { return true; }, [&](int i) { E::issue_one(c, ln, d, i); });
-    slot = next_slot(slot);
+    if constexpr (E::GROUP == 1) {
+      const typename E::Dst d = E::stage_dst(wl, c, slot_after_next(slot), s + 2, S);
+      E::compute(ring, slot, acc, [] { return true; },
+                 [&](int i) { E::issue_one(c, ln, d, i); });
+      slot = next_slot<E>(slot);
+    } else {
+      const int other = slot ^ 2;
+      const typename E::Dst d0 = E::stage_dst(wl, c, other, s + 2, S);
+      const typename E::Dst d1 = E::stage_dst(wl, c, other + 1, s + 3, S);
+      if (s + 1 < S) hook(s + 1);
+      E::compute(ring, slot, acc, [] { return true; },
+                 [&](int i) { issue_group_one<E>(c, ln, d0, d1, i); });
+      slot = other;
+    }
   }
   wait_vmcnt<0>();
   lds_sync();

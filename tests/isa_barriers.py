@@ -65,11 +65,13 @@ def vm_waits_in_compute_blocks(asm_text, min_math=32):
     """Return [(kernel, block, wait)] for compiler-visible vmcnt waits inside
     basic blocks that carry the k-stage math (>= min_math MFMA/FMA ops).
 
-    The stage loops keep two stages of direct-to-LDS loads in flight and wait
-    for the oldest one explicitly, with a nonzero count, right before the
-    stage barrier; when the whole stage is one basic block that wait is in
-    it. Any other vmcnt wait in a compute block (after the barrier, a second
-    one, or a full drain) empties the prefetch on every stage.
+    The stage loops keep direct-to-LDS loads in flight and wait for the
+    stage they are about to compute explicitly, once, right before the stage
+    barrier (vmcnt <= LOADS with one barrier per stage, vmcnt = 0 with one
+    per pair of stages, when nothing else is in flight); when the whole stage
+    is one basic block that wait is in it. Any other vmcnt wait in a compute
+    block (after the barrier or after the math has started, or a second one)
+    stalls the prefetch on every stage.
     """
     out = []
     kernel, label, lines = None, None, []
@@ -85,7 +87,7 @@ def vm_waits_in_compute_blocks(asm_text, min_math=32):
                     pending, accepted = None, True  # the stage wait
                 m = re.search(r's_waitcnt\b.*vmcnt\((\d+)\)', l)
                 if m:
-                    if pending is None and not accepted and not math_seen and int(m.group(1)) > 0:
+                    if pending is None and not accepted and not math_seen:
                         pending = l.strip()
                     else:
                         out.append((kernel, label, l.strip()))

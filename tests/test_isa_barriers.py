@@ -65,10 +65,12 @@ def test_vm_wait_checker_catches_the_pattern():
     assert vm_waits_in_compute_blocks(asm) == [("_Z1kv", ".LBB0_1", "s_waitcnt vmcnt(4)")]
     assert vm_waits_in_compute_blocks(asm.replace("\ts_waitcnt vmcnt(4)\n", "")) == []
     # The stage wait right before the barrier is the protocol's own; a wait
-    # after the barrier, or a full drain, is not.
+    # after the barrier, or a second one, is not.
     stage = ["_Z1kv:", ".LBB0_1:", "\ts_waitcnt vmcnt(4)", "\ts_barrier"] + body
     assert vm_waits_in_compute_blocks("\n".join(stage)) == []
     late = stage + ["\ts_waitcnt vmcnt(2)"]
     assert vm_waits_in_compute_blocks("\n".join(late)) == [("_Z1kv", ".LBB0_1", "s_waitcnt vmcnt(2)")]
-    drain = ["_Z1kv:", ".LBB0_1:", "\ts_waitcnt vmcnt(0)", "\ts_barrier"] + body
-    assert vm_waits_in_compute_blocks("\n".join(drain)) == [("_Z1kv", ".LBB0_1", "s_waitcnt vmcnt(0)")]
+    pair = ["_Z1kv:", ".LBB0_1:", "\ts_waitcnt vmcnt(0)", "\ts_barrier"] + body
+    assert vm_waits_in_compute_blocks("\n".join(pair)) == []
+    twice = ["_Z1kv:", ".LBB0_1:", "\ts_waitcnt vmcnt(4)", "\ts_waitcnt vmcnt(0)", "\ts_barrier"] + body
+    assert vm_waits_in_compute_blocks("\n".join(twice)) == [("_Z1kv", ".LBB0_1", "s_waitcnt vmcnt(0)")]
