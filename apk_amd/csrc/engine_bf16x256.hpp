@@ -49,6 +49,9 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 struct EngBf16x256 {
   static constexpr int TM = 256, TN = 256, KS = 32, NS = 4, GROUP = 2, THREADS = 512;
+  // Waves per SIMD at most (1 block of 8 waves per CU): the register budget the
+  // compiler may schedule for.
+  static constexpr int WAVES_PER_SIMD = 2;
   static constexpr int ROW_BYTES = KS * 2;                  // 64 B
   static constexpr int A_STAGE = TM * ROW_BYTES;            // 16 KiB
   static constexpr int B_STAGE = TN * ROW_BYTES;            // 16 KiB

@@ -32,6 +32,9 @@ namespace apk {
 
 struct EngMfma128 {
   static constexpr int TM = 128, TN = 128, KS = 32, NS = 3, GROUP = 1, THREADS = 256;
+  // Waves per SIMD at most (1 block per CU (LDS-bound)): the register budget the
+  // compiler may schedule for.
+  static constexpr int WAVES_PER_SIMD = 1;
   static constexpr int A_STAGE = TM * KS * 4;               // bytes
   static constexpr int B_STAGE = KS * TN * 4;               // bytes
   static constexpr int STAGE = A_STAGE + B_STAGE;           // 32 KiB

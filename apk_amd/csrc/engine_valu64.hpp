@@ -22,6 +22,9 @@ namespace apk {
 
 struct EngValu64 {
   static constexpr int TM = 64, TN = 64, KS = 32, NS = 3, GROUP = 1, THREADS = 256;
+  // Waves per SIMD at most (3 blocks per CU (LDS-bound)): the register budget the
+  // compiler may schedule for.
+  static constexpr int WAVES_PER_SIMD = 3;
   static constexpr int A_STAGE = TM * KS * 4;               // 8 KiB
   static constexpr int B_STAGE = KS * TN * 4;               // 8 KiB
   static constexpr int STAGE = A_STAGE + B_STAGE;           // 16 KiB
@@ -109,38 +112,48 @@ struct EngValu64 {
   // One k-stage out of ring slot `slot`. `pre` runs first (flag check;
   // returning false abandons the stage before any accumulator changes),
   // `mid(i)` after k step i for i < LOADS (the next stage's direct-to-LDS
-  // load i).
+  // load i). The operands of k step kk+1 are read from LDS before the 16
+  // FMAs of step kk are issued (a scheduling barrier keeps the compiler
+  // from sinking each read next to its use, where one wave per SIMD would
+  // wait out the LDS latency at every step); the FMA order is unchanged.
+  struct Ops {
+    float a[4];
+    float4 b;
+  };
   template <class Pre, class Mid>
   static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
                                                  Pre&& pre, Mid&& mid) {
     const char* abase = ring + slot * STAGE;
     const float* bs = (const float*)(abase + A_STAGE);
     const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-    auto step = [&](int kk) {
-      float a[4];
+    auto rd = [&](int kk, Ops& o) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int r = ty * 4 + i;
         const int slotq = (kk >> 2) ^ aswz(r);
-        a[i] = *(const float*)(abase + r * 128 + slotq * 16 + (kk & 3) * 4);
+        o.a[i] = *(const float*)(abase + r * 128 + slotq * 16 + (kk & 3) * 4);
       }
-      const float4 b = *(const float4*)(bs + kk * TN + tx * 4);
-      const float bb[4] = {b.x, b.y, b.z, b.w};
+      o.b = *(const float4*)(bs + kk * TN + tx * 4);
+    };
+    if (!pre()) return false;
+    Ops o[2];
+    rd(0, o[0]);
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+      if (kk + 1 < KS) rd(kk + 1, o[(kk + 1) & 1]);
+      __builtin_amdgcn_sched_barrier(0);
+      const Ops& c = o[kk & 1];
+      const float bb[4] = {c.b.x, c.b.y, c.b.z, c.b.w};
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc.v[i][j] = fmaf(a[i], bb[j], acc.v[i][j]);
-    };
-    // The first LOADS k steps are peeled so that the hooks sit outside the
-    // unrolled loop.
-    if (!pre()) return false;
-#pragma unroll
-    for (int kk = 0; kk < LOADS; ++kk) {
-      step(kk);
-      mid(kk);
+        for (int j = 0; j < 4; ++j) acc.v[i][j] = fmaf(c.a[i], bb[j], acc.v[i][j]);
+      if (kk < LOADS) {
+        __builtin_amdgcn_sched_barrier(0);
+        mid(kk);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-#pragma unroll
-    for (int kk = LOADS; kk < KS; ++kk) step(kk);
     return true;
   }
   static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {

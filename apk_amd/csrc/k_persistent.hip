@@ -16,7 +16,7 @@
 namespace apk {
 
 template <class E>
-__global__ void __launch_bounds__(E::THREADS)
+__global__ void __launch_bounds__(E::THREADS) __attribute__((amdgpu_waves_per_eu(1, E::WAVES_PER_SIMD)))
     k_persistent_gemm(const void* __restrict__ A, const void* __restrict__ B,
                       float* __restrict__ C, int M, int N, int K, int kChunk,
                       unsigned* next_task, apk_tile_record* log) {

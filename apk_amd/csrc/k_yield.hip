@@ -36,7 +36,8 @@ namespace apk {
 // cooperative instantiations carry none of its code and the retreat ones
 // none of the in-kernel urgent path.
 template <class E, int POLL, bool ORACLE, bool SYS, bool RETREAT>
-__global__ void __launch_bounds__(E::THREADS) k_persistent_yield(const apk_yield_params) {
+__global__ void __launch_bounds__(E::THREADS) __attribute__((amdgpu_waves_per_eu(1, E::WAVES_PER_SIMD)))
+k_persistent_yield(const apk_yield_params) {
   // Every parameter is re-read from the kernel-argument segment where it is
   // used (P() is opaque to the optimiser), instead of being loaded once at
   // entry and held in scalar registers for the whole kernel: the stage loop
