@@ -56,7 +56,7 @@ struct EngBf16x256 {
   static constexpr int A_STAGE = TM * ROW_BYTES;            // 16 KiB
   static constexpr int B_STAGE = TN * ROW_BYTES;            // 16 KiB
   static constexpr int STAGE = A_STAGE + B_STAGE;           // 32 KiB
-  static constexpr int LDS_BYTES = NS * STAGE;              // 96 KiB
+  static constexpr int LDS_BYTES = NS * STAGE;              // 128 KiB
   static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 2 per thread
   static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 2 per thread
   static constexpr int LOADS = LOADS_A + LOADS_B;

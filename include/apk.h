@@ -113,10 +113,12 @@ int apk_persistent_gemm(int engine, const void* A, const void* B, float* C,
  * Poll sites: APK_POLL_CHUNK polls at every poll_every-th k-chunk boundary of
  * a tile (the tile-boundary yield points of src/yield.cu:125-136 once K is
  * walked in chunks); APK_POLL_STAGE polls at every LDS k-stage (the
- * mid-pipeline points of src/midyield.cu:246-290). The flag is sampled by a
- * direct-to-LDS load issued right behind a stage's data loads and retired by
- * the same stage wait, so a poll never stalls the pipeline; the value acted
- * on is one k-stage old.
+ * mid-pipeline points of src/midyield.cu:246-290). Sites sit at the stage
+ * loop's barriers: the BF16X256 engine synchronises once per pair of
+ * k-stages, so its site stride is rounded up to 2 stages (64 k). The flag is
+ * sampled by a direct-to-LDS load issued right behind a stage's data loads
+ * and retired by the same stage wait, so a poll never stalls the pipeline;
+ * the value acted on is one k-stage (one pair) old.
  *
  * On a new generation every block logs its observation time; blocks that pop
  * an urgent tile from the event's mini-queue (src/yield.cu:155-183) yield:
