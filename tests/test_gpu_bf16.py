@@ -155,6 +155,7 @@ class Bf16Job:
             "C": self.dC.cpu().numpy(), "Cu": self.dCu.cpu().numpy()[:max(ev, 1)],
             "task_hash": self.task_hash.cpu().numpy().view(np.uint64),
             "set_gt": self.set_gt.cpu().numpy()[:ev], "claim": self.claim.cpu().numpy()[:ev],
+            "site": self.site.cpu().numpy()[:ev],
             "stats": self.stats.cpu().numpy().reshape(self.blocks, apk.STATS_PER_BLOCK),
             "exec": self.exec_count.cpu().numpy(), "u_exec": self.u_exec.cpu().numpy()[:ev],
         }
@@ -203,3 +204,38 @@ def test_bf16_float64_and_oracle(bf16_job, apk):
     assert oracle.rel_frobenius(r["C"], ref) <= 1e-5
     assert (r["exec"] == 1).all()
     assert (r["u_exec"] == j.U).all()
+
+
+@pytest.fixture(scope="module")
+def bf16_odd_job(torch_gpu, apk):
+    # K = 160 is 5 k-stages: the stage loop takes them in pairs (0,1), (2,3),
+    # (4, a stage of zeros); the urgent K = 96 (3 stages) ends the same way.
+    say("building bf16x256 odd-length yield job M=N=512 K=160 kc=32, urgent 256x256x96")
+    return Bf16Job(torch_gpu, apk, 512, 512, 160, 32, 256, 256, 96, events=24, blocks=64,
+                   passes=384)
+
+
+@pytest.mark.parametrize("resume", [0, 1, 2])
+def test_bf16_odd_length_pairs_yield(bf16_odd_job, apk, resume):
+    """Yields at every site of odd-length tiles, incl. the last pair whose second
+    stage is all zeros (checkpointed and restored with the pair): C bit-identical
+    to the unpreempted run, within tolerance of float64, urgent outputs equal the
+    non-preemptible urgent GEMM, every task and event counted once."""
+    j = bf16_odd_job
+    say(f"bf16x256 odd-length pairs, stage yields, resume={resume}")
+    ref = j.run(apk.POLL_OFF, events=0)
+    r = j.run(apk.POLL_STAGE, resume=resume, use_oracle=True)
+    fired = int((r["set_gt"] != 0).sum())
+    assert fired == j.events and int(r["stats"][:, 0].sum()) >= fired
+    assert np.array_equal(r["C"].view(np.uint32), ref["C"].view(np.uint32))
+    assert oracle.rel_frobenius(r["C"], oracle.gemm_f64(j.A, j.B, threads=8)) <= 1e-5
+    uref = run_bf16_urgent(j)
+    assert oracle.rel_frobenius(uref, oracle.gemm_f64(j.Au, j.Bu, threads=8)) <= 1e-5
+    for e in range(j.events):
+        assert np.array_equal(r["Cu"][e].view(np.uint32), uref.view(np.uint32)), e
+    assert (r["exec"] == 1).all() and (r["u_exec"] == j.U).all()
+    # sites are the pair boundaries 0, 2, 4; site 4 is the pair with the zero stage
+    assert set(np.unique(r["site"]).tolist()) <= {0, 2, 4}
+    assert (r["site"] == 4).any()
+    say(f"  fired {fired} events at sites {np.bincount(r['site'], minlength=5).tolist()}, "
+        "bit-identical, float64 within 1e-5")
