@@ -317,20 +317,23 @@ k_persistent_yield(const apk_yield_params) {
         // Poll site: the flag sample for site s has landed with stage s (it
         // was issued in front of the loads of stage s+1, or of the pair s).
         // A new generation (or the setter's turn) ends the loop here, before
-        // stage s is computed.
-        if (POLL != APK_POLL_OFF && s == nextSite) {
-          if (s != siteDone) {
-            const int f = uniform(flagring[site_flag(slot)]);
-            fLatest = f;
-            if (f != lastSeen || isSetter) {
-              fSeen = f;
-              atSite = true;
-              break;
-            }
-          }
-          nextSite += pollStride;
-        }
+        // stage s is computed. With one barrier per stage the flag is read
+        // right after the barrier; with pairs it is read in the engine's
+        // `pre` hook (measured: 10.8% -> 7-9% every-site overhead for the
+        // bf16 engine, while the same placement cost the fp32 engines 1-2%).
         if constexpr (E::GROUP == 1) {
+          if (POLL != APK_POLL_OFF && s == nextSite) {
+            if (s != siteDone) {
+              const int f = uniform(flagring[site_flag(slot)]);
+              fLatest = f;
+              if (f != lastSeen || isSetter) {
+                fSeen = f;
+                atSite = true;
+                break;
+              }
+            }
+            nextSite += pollStride;
+          }
           const int ahead = slot_after_next(slot);
           const bool carry = s + 1 == nextSite;  // s+1 is a site
           // Stage s+2 (and the sample for a site at s+1) goes out under stage
@@ -344,6 +347,20 @@ k_persistent_yield(const apk_yield_params) {
           slot = next_slot<E>(slot);
           ++s;
         } else {
+          const bool site = POLL != APK_POLL_OFF && s == nextSite;
+          const bool check = site && s != siteDone;
+          if (site) nextSite += pollStride;
+          auto poll = [&]() -> bool {
+            if (!check) return true;
+            const int f = uniform(flagring[site_flag(slot)]);
+            fLatest = f;
+            if (f != lastSeen || isSetter) {
+              fSeen = f;
+              atSite = true;
+              return false;
+            }
+            return true;
+          };
           // Stages s and s+1 are computed as one group; stages s+2, s+3 (and
           // the sample for a site at s+2) go out under its first stage, into
           // the other half of the ring, which held the previous pair.
@@ -351,10 +368,11 @@ k_persistent_yield(const apk_yield_params) {
           const bool carry = s + 2 == nextSite;
           const typename E::Dst d0 = E::stage_dst(wl, ctx, other, s + 2, S);
           const typename E::Dst d1 = E::stage_dst(wl, ctx, other + 1, s + 3, S);
-          E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
-            if (i == 0 && carry) sample(other);
-            issue_group_one<E>(ctx, ln, d0, d1, i);
-          });
+          if (!E::compute(ring, slot, acc, poll, [&](int i) {
+                if (i == 0 && carry) sample(other);
+                issue_group_one<E>(ctx, ln, d0, d1, i);
+              }))
+            break;
           slot = other;
           s += 2;
         }

@@ -164,8 +164,10 @@ class Bf16Job:
 @pytest.fixture(scope="module")
 def bf16_job(torch_gpu, apk):
     say("building bf16x256 yield job M=N=512 K=1024 kc=64, urgent 256x512x256")
+    # 144 passes = 9 tiles per block: the job outlasts the 24 events the
+    # setter (block 0) raises 3 us apart at its own poll sites.
     return Bf16Job(torch_gpu, apk, 512, 512, 1024, 64, 256, 512, 256, events=24, blocks=64,
-                   passes=48)
+                   passes=144)
 
 
 @pytest.mark.parametrize("poll,resume", [(2, 0), (2, 1), (2, 2), (1, 0)])
