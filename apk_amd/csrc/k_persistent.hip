@@ -7,6 +7,8 @@
 // k_chunk-wide chunks in order; chunk boundaries are the points where the
 // preemptible variants poll, and here they are where per-chunk timing
 // records are taken.
+#include <climits>
+
 #include "capi.hpp"
 #include "engine_bf16x256.hpp"
 #include "engine_mfma128.hpp"
@@ -49,8 +51,14 @@ __global__ void __launch_bounds__(E::THREADS) __attribute__((amdgpu_waves_per_eu
 
     typename E::Acc acc;
     E::zero(acc);
+    // The next stage that opens a chunk record (none when no log is kept):
+    // one uniform compare per stage instead of a modulo under a per-thread
+    // branch at the top of every stage.
+    int nextRec = rec ? 0 : INT_MAX;
     run_stages<E>(ring, wl, ctx, acc, row0, col0, K / E::KS, [&](int s) {
-      if (threadIdx.x == 0 && rec && s % spc == 0) {
+      if (s != nextRec) return;
+      nextRec += spc;
+      if (threadIdx.x == 0) {
         const int64_t now = wall_ticks();
         const int c = s / spc;
         if (c > 0) {
