@@ -44,10 +44,13 @@ class EngineGeometry(ctypes.Structure):
                 ("b_transposed", ctypes.c_int)]
 
 
-POLL_OFF, POLL_CHUNK, POLL_STAGE = 0, 1, 2
+POLL_OFF, POLL_CHUNK, POLL_STAGE, POLL_ISSUE = 0, 1, 2, 3
 RESUME_CKPT_FULL, RESUME_CKPT_ACC, RESUME_RESTART = 0, 1, 2
 FLAG_STRIDE, FLAG_MAX_COPIES = 4096, 256
-STATS_PER_BLOCK = 8
+STATS_PER_BLOCK = 16
+# columns of a stats row (APK_ST_* in include/apk.h)
+(ST_YIELDS, ST_SAVE, ST_URGENT, ST_RESTORE, ST_INFLIGHT, ST_RETREATS, ST_RESUMED, ST_ERRORS,
+ ST_STALE, ST_CHECKPOINTS, ST_INFLIGHT_ALL, ST_STALE_ALL) = range(12)
 QUEUE_WORDS, QUEUE_XCDS = 16, 8
 SES_PER_XCD, RETREAT_DOMAINS = 4, 32
 
@@ -106,6 +109,7 @@ _SIGNATURES = {
     "apk_yield_ckpt_floats": (ctypes.c_longlong, [_I]),
     "apk_persistent_yield_occupancy": (_I, [_I, _I, ctypes.POINTER(_I)]),
     "apk_raise_flag": (_I, [_P, _I, _I, _P, _P]),
+    "apk_spin_flag": (_I, [_P, _I, ctypes.c_longlong, _P, _P]),
     "apk_tiny_oracle": (_I, [ctypes.POINTER(TinyParams), _I, _P]),
 }
 
@@ -181,6 +185,13 @@ def raise_flag(flag, copies, value, set_gt=None, stream=0):
     """Queue apk_raise_flag on `stream`: store `value` into every flag copy
     and the device tick into *set_gt. Asynchronous."""
     check(load().apk_raise_flag(flag, copies, value, set_gt, stream))
+
+
+def spin_flag(flag, system_scope, max_ticks, out, stream=0):
+    """Queue apk_spin_flag: one wave spins (bounded by max_ticks) until *flag
+    reads non-zero; out[0] = device tick of that read (-1 on timeout),
+    out[1] = the value. Asynchronous."""
+    check(load().apk_spin_flag(flag, 1 if system_scope else 0, max_ticks, out, stream))
 
 
 def persistent_yield(engine, poll, oracle, params, blocks, stream=0):

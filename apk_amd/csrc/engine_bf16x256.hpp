@@ -139,13 +139,17 @@ struct EngBf16x256 {
     return Dst{wave_lds + (uint32_t)(slot * STAGE), (uint32_t)((real ? t : 0) * KS * 2),
                real ? c.ra : za, real ? c.rb : zb};
   }
+  // Byte offset inside a ring slot of load i's piece: thread t's 16 bytes of
+  // load i land at slot + dma_lds_off(i) + 16 t.
+  static constexpr uint32_t dma_lds_off(int i) {
+    return (uint32_t)(i < LOADS_A ? i * WAVES * 1024 : A_STAGE + (i - LOADS_A) * WAVES * 1024);
+  }
   static __device__ __forceinline__ void issue_one(const Ctx&, const Lane& ln, const Dst& d,
                                                    int i) {
     if (i < LOADS_A)
-      dma_x4(d.ra, d.lds, (uint32_t)(i * WAVES * 1024), ln.a[i], d.k);
+      dma_x4(d.ra, d.lds, dma_lds_off(i), ln.a[i], d.k);
     else
-      dma_x4(d.rb, d.lds, (uint32_t)(A_STAGE + (i - LOADS_A) * WAVES * 1024), ln.b[i - LOADS_A],
-             d.k);
+      dma_x4(d.rb, d.lds, dma_lds_off(i), ln.b[i - LOADS_A], d.k);
   }
 
   // Operands of k-step j (16 k values): one 16-byte read per 32-row block of

@@ -116,12 +116,17 @@ struct EngMfma128 {
     const uint32_t k0 = (uint32_t)((t < S ? t : S - 1) * KS);
     return Dst{wave_lds + (uint32_t)(slot * STAGE), k0 * 4u, k0 * (uint32_t)c.N * 4u};
   }
+  // Byte offset inside a ring slot of load i's piece: thread t's 16 bytes of
+  // load i land at slot + dma_lds_off(i) + 16 t.
+  static constexpr uint32_t dma_lds_off(int i) {
+    return (uint32_t)(i < LOADS_A ? i * 4096 : A_STAGE + (i - LOADS_A) * 4096);
+  }
   static __device__ __forceinline__ void issue_one(const Ctx& c, const Lane& ln, const Dst& d,
                                                    int i) {
     if (i < LOADS_A)
-      dma_x4(c.ra, d.lds, (uint32_t)(i * 4096), ln.a[i], d.ka);
+      dma_x4(c.ra, d.lds, dma_lds_off(i), ln.a[i], d.ka);
     else
-      dma_x4(c.rb, d.lds, (uint32_t)(A_STAGE + (i - LOADS_A) * 4096), ln.b[i - LOADS_A], d.kb);
+      dma_x4(c.rb, d.lds, dma_lds_off(i), ln.b[i - LOADS_A], d.kb);
   }
 
   // Operands of k-group g (8 k values): one 16-byte A read per 32-row

@@ -70,7 +70,7 @@ k_persistent_yield(const apk_yield_params) {
   auto row = [&] { return P().block_base + bid; };  // this block's stats / obs column
   // Poll sites sit at barriers: every GROUP-th k-stage at the finest.
   const int pollStride = [&] {
-    const int st = (POLL == APK_POLL_STAGE)
+    const int st = (POLL == APK_POLL_STAGE || POLL == APK_POLL_ISSUE)
                        ? 1
                        : (P().k_chunk / E::KS) * (P().poll_every > 0 ? P().poll_every : 1);
     return (st + E::GROUP - 1) / E::GROUP * E::GROUP;
@@ -103,8 +103,11 @@ k_persistent_yield(const apk_yield_params) {
     if (f0 < 0) fLatest = f0;
     else lastSeen = f0 < P().num_events ? f0 : P().num_events;
   }
-  enum { ST_YIELDS, ST_SAVE, ST_URGENT, ST_RESTORE, ST_INFLIGHT, ST_RETREATS, ST_RESUMED,
-         ST_ERRORS };
+  enum { ST_YIELDS = APK_ST_YIELDS, ST_SAVE = APK_ST_SAVE, ST_URGENT = APK_ST_URGENT,
+         ST_RESTORE = APK_ST_RESTORE, ST_INFLIGHT = APK_ST_INFLIGHT,
+         ST_RETREATS = APK_ST_RETREATS, ST_RESUMED = APK_ST_RESUMED, ST_ERRORS = APK_ST_ERRORS,
+         ST_STALE = APK_ST_STALE, ST_CHECKPOINTS = APK_ST_CHECKPOINTS,
+         ST_INFLIGHT_ALL = APK_ST_INFLIGHT_ALL, ST_STALE_ALL = APK_ST_STALE_ALL };
   auto stat = [&](int k, uint64_t v) { s_stats[k] += v; };  // thread 0 only
 
   auto set_flag = [&](int v) {
@@ -268,10 +271,27 @@ k_persistent_yield(const apk_yield_params) {
     };
 
     bool retreated = false, yielded = false;
+    // Issue sites (APK_POLL_ISSUE): right after the barrier of stage s the
+    // loads of stage s+2 (pair s+2, s+3) go out at once, and the site is
+    // polled right behind them -- the window-forcing geometry of
+    // src/midyield.cu:246-258: a checkpoint here holds a stage whose loads
+    // were issued nanoseconds earlier. `ahead`: that issue is already done
+    // for the current s (re-entry after a site, or a restored ring).
+    bool ahead = false;
+    // Stages resident or in flight, not yet computed, at a site before stage
+    // st: what a FULL checkpoint keeps. With pairs the zero stage after an
+    // odd tile's last stage is kept too (the pair is computed as a whole).
+    auto live_at = [&](int st) -> int {
+      if constexpr (POLL == APK_POLL_ISSUE)
+        return E::GROUP == 2 ? E::NS : (S - st < E::NS ? S - st : E::NS);
+      else
+        return (E::GROUP == 2 || S - st >= 2) ? 2 : S - st;
+    };
     for (;;) {  // (re)entries of the stage loop of this job
       if (srcKind != AS_IS) {
         nextSite = !pollable ? S + 2 : (s + pollStride - 1) / pollStride * pollStride;
         const int64_t tIn = wall_ticks();
+        ahead = POLL == APK_POLL_ISSUE && srcKind == FULL;
         if (srcKind == FRESH) {
           E::zero(acc);
           issue_stage(s, slot);
@@ -285,16 +305,20 @@ k_persistent_yield(const apk_yield_params) {
             lds_sync();
           }
         } else {
-          // Accumulators hold stages [0, s); stages s, s+1 go to ring slots
-          // slot, slot+1 (from the checkpoint, or fetched again), and the
-          // site at s gets a fresh sample.
+          // Accumulators hold stages [0, s); stages s, s+1 (issue sites: every
+          // live stage) go to ring slots slot, slot+1, ... (from the
+          // checkpoint, or s, s+1 fetched again), and the site at s gets a
+          // fresh sample.
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
           Ckpt<E>::load_acc(acc, src);
-          const int live = (E::GROUP == 2 || S - s >= 2) ? 2 : S - s;
           if (srcKind == FULL) {
-            Ckpt<E>::load_ring(ring, src, slot, live);
-            // The sample alone: both live slots now hold restored stages.
+            Ckpt<E>::load_ring(ring, src, slot, live_at(s));
+            // The sample alone: the live slots now hold restored stages.
             sample(site_flag(slot));
+            // Issue sites: the restored ring includes the stage(s) the next
+            // iteration would issue; send the sample that goes with them.
+            if constexpr (POLL == APK_POLL_ISSUE)
+              sample(E::GROUP == 1 ? slot_after_next(slot) : (slot ^ 2));
             wait_vmcnt<0>();
             __syncthreads();  // restored ring visible to all waves
           } else {
@@ -322,6 +346,16 @@ k_persistent_yield(const apk_yield_params) {
         // `pre` hook (measured: 10.8% -> 7-9% every-site overhead for the
         // bf16 engine, while the same placement cost the fp32 engines 1-2%).
         if constexpr (E::GROUP == 1) {
+          if constexpr (POLL == APK_POLL_ISSUE) {
+            // Stage s+2 (and the sample for the site at s+1) at once, into the
+            // slot of stage s-1, which every wave finished before the barrier.
+            if (!ahead) {
+              const int a = slot_after_next(slot);
+              if (pollable) sample(a);
+              issue_loads<E>(ctx, ln, E::stage_dst(wl, ctx, a, s + 2, S));
+            }
+            ahead = false;
+          }
           if (POLL != APK_POLL_OFF && s == nextSite) {
             if (s != siteDone) {
               const int f = uniform(flagring[site_flag(slot)]);
@@ -329,20 +363,23 @@ k_persistent_yield(const apk_yield_params) {
               if (f != lastSeen || isSetter) {
                 fSeen = f;
                 atSite = true;
+                ahead = POLL == APK_POLL_ISSUE;
                 break;
               }
             }
             nextSite += pollStride;
           }
-          const int ahead = slot_after_next(slot);
+          const int aheadSlot = slot_after_next(slot);
           const bool carry = s + 1 == nextSite;  // s+1 is a site
           // Stage s+2 (and the sample for a site at s+1) goes out under stage
           // s's matrix work; its slot held stage s-1, which every wave
           // finished before the barrier above.
-          const typename E::Dst d = E::stage_dst(wl, ctx, ahead, s + 2, S);
+          const typename E::Dst d = E::stage_dst(wl, ctx, aheadSlot, s + 2, S);
           E::compute(ring, slot, acc, [] { return true; }, [&](int i) {
-            if (i == 0 && carry) sample(ahead);
-            E::issue_one(ctx, ln, d, i);
+            if constexpr (POLL != APK_POLL_ISSUE) {
+              if (i == 0 && carry) sample(aheadSlot);
+              E::issue_one(ctx, ln, d, i);
+            }
           });
           slot = next_slot<E>(slot);
           ++s;
@@ -368,11 +405,26 @@ k_persistent_yield(const apk_yield_params) {
           const bool carry = s + 2 == nextSite;
           const typename E::Dst d0 = E::stage_dst(wl, ctx, other, s + 2, S);
           const typename E::Dst d1 = E::stage_dst(wl, ctx, other + 1, s + 3, S);
-          if (!E::compute(ring, slot, acc, poll, [&](int i) {
-                if (i == 0 && carry) sample(other);
-                issue_group_one<E>(ctx, ln, d0, d1, i);
-              }))
-            break;
+          if constexpr (POLL == APK_POLL_ISSUE) {
+            // Issue sites: the next pair goes out at once, then the poll.
+            if (!ahead) {
+              if (carry) sample(other);
+#pragma unroll
+              for (int i = 0; i < E::GROUP * E::LOADS; ++i) issue_group_one<E>(ctx, ln, d0, d1, i);
+            }
+            ahead = false;
+            if (!poll()) {
+              ahead = true;
+              break;
+            }
+            E::compute(ring, slot, acc);
+          } else {
+            if (!E::compute(ring, slot, acc, poll, [&](int i) {
+                  if (i == 0 && carry) sample(other);
+                  issue_group_one<E>(ctx, ln, d0, d1, i);
+                }))
+              break;
+          }
           slot = other;
           s += 2;
         }
@@ -411,10 +463,51 @@ k_persistent_yield(const apk_yield_params) {
       const int ev = f - 1;
       lastSeen = f;
 
-      // Does this block hand over its CU (retreat) or run urgent tiles?
-      float* dst;
-      unsigned tk = RQ_NONE;
+      // ---- checkpoint: accumulators and the live stages (live_at) ----
+      const int live = live_at(s);
+      // `observe`: before the drain, each thread reads its 16 bytes of the
+      // last load of the newest stage issued (slot `newest`), and reads them
+      // again once every load has landed: a difference means that stage was
+      // still in flight when the drain (naive: the save) began. With
+      // `naive`, the saved stages are also compared with the landed ring: a
+      // difference is a stale checkpoint, which the resumed tile inherits.
+      int ckMoved = 0, ckStale = 0;  // uniform: what `observe` found
+      auto save_state = [&](float* dst, bool drain, bool observe) -> int64_t {
+        // the slot of the most recently issued stage
+        const int newest = POLL == APK_POLL_ISSUE ? (slot + E::NS - 1) % E::NS : next_slot<E>(slot);
+        uint4 before = {0, 0, 0, 0};
+        if (observe) before = probe_last_load<E>(ring, newest);
+        // drain: every wave's loads landed, then a barrier makes them visible
+        // to every thread. naive: no wait and no barrier -- the ring is read
+        // as it stands (no wave writes LDS here; only loads may still land).
+        if (drain) {
+          wait_vmcnt<0>();
+          lds_sync();
+        }
+        const int64_t t0 = wall_ticks();
+        if (P().resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, dst, slot, live);
+        if (P().resume != APK_RESUME_RESTART) Ckpt<E>::save_acc(acc, dst);
+        if (observe) {
+          wait_vmcnt<0>();  // every load landed, every checkpoint store done
+          lds_sync();
+          const uint4 after = probe_last_load<E>(ring, newest);
+          const bool moved = (before.x != after.x) | (before.y != after.y) |
+                             (before.z != after.z) | (before.w != after.w);
+          const bool stale = !drain && P().resume == APK_RESUME_CKPT_FULL &&
+                             Ckpt<E>::ring_differs(ring, dst, slot, live);
+          ckMoved = uniform(__syncthreads_or(moved ? 1 : 0) ? 1 : 0);
+          ckStale = uniform(__syncthreads_or(stale ? 1 : 0) ? 1 : 0);
+          if (tid == 0) {
+            stat(ST_INFLIGHT_ALL, (uint64_t)ckMoved);
+            stat(ST_STALE_ALL, (uint64_t)ckStale);
+            stat(ST_CHECKPOINTS, 1);
+          }
+        }
+        return t0;
+      };
+
       if constexpr (retreatArm) {
+        // ---- retreat: hand this block's CU to the kernel on the other stream ----
         // The hardware deals a kernel's workgroups round-robin to the XCDs
         // and their shader engines from wherever its pointers stand, and a
         // workgroup runs only on a CU of its own shader engine: the urgent
@@ -426,31 +519,11 @@ k_persistent_yield(const apk_yield_params) {
         if (tid == 0 &&
             fetch_add_i32(&P().retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + dom], 1) < quota)
           t = rq_reserve(P().rq_ctl, P().rq_capacity);
-        tk = bcast(t);
+        const unsigned tk = bcast(t);
         if (tk == RQ_NONE) continue;  // quota taken (or queue full): keep working
-        dst = P().rq_slots + (size_t)tk * Ckpt<E>::SLOT_FLOATS;
-        wait_vmcnt<0>();  // always drain: nothing may land in LDS after the block exits
-      } else {
-        const int U = nU();
-        uidx = U > 0 ? pop_urgent(ev) : U;
-        if (uidx >= U) continue;
-        dst = ckslot();
-        if (!P().naive) wait_vmcnt<0>();  // drain: stage s+1 has landed
-      }
-
-      // ---- checkpoint: accumulators and the live stages s, s+1 ----
-      lds_sync();
-      const int64_t tSave = wall_ticks();
-      // Resident, not computed; with pairs the zero stage after an odd
-      // tile's last stage is kept too (the pair is computed as a whole).
-      const int live = (E::GROUP == 2 || S - s >= 2) ? 2 : S - s;
-      if (P().resume != APK_RESUME_RESTART) {
-        Ckpt<E>::save_acc(acc, dst);
-        if (P().resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, dst, slot, live);
-      }
-
-      if constexpr (retreatArm) {
-        // ---- retreat: publish resume entry tk and exit, handing the CU on ----
+        float* dst = P().rq_slots + (size_t)tk * Ckpt<E>::SLOT_FLOATS;
+        // always drain: nothing may land in LDS after the block exits
+        const int64_t tSave = save_state(dst, true, false);
         const int rkind = P().resume == APK_RESUME_RESTART ? 0
                           : P().resume == APK_RESUME_CKPT_FULL ? 2 : 1;
         __threadfence();  // this thread's checkpoint stores are visible device-wide
@@ -468,7 +541,35 @@ k_persistent_yield(const apk_yield_params) {
         }
         retreated = true;
       } else {
-        // ---- cooperative yield: this block serves the event next ----
+        // ---- cooperative yield: pop the event's mini-queue, checkpoint, serve ----
+        const int U = nU();
+        const bool drain = !P().naive;
+        int64_t tSave;
+        if constexpr (POLL == APK_POLL_ISSUE) {
+          // Window-forcing order (src/midyield.cu:246-258): checkpoint right
+          // after the flag read, before any further wait or atomic, then pop.
+          // A block that gets no urgent tile goes on with its state intact.
+          tSave = save_state(ckslot(), drain, true);
+          uidx = U > 0 ? pop_urgent(ev) : U;
+          if (uidx >= U) {
+            // No urgent tile: resume from the checkpoint just taken all the
+            // same, so that every checkpoint taken here is tested on resume.
+            if (tid == 0) {
+              stat(ST_INFLIGHT, (uint64_t)ckMoved);
+              stat(ST_STALE, (uint64_t)ckStale);
+            }
+            srcKind = P().resume == APK_RESUME_RESTART   ? FRESH
+                      : P().resume == APK_RESUME_CKPT_FULL ? FULL
+                                                            : ACC;
+            src = ckslot();
+            if (srcKind == FRESH) s = 0;
+            continue;
+          }
+        } else {
+          uidx = U > 0 ? pop_urgent(ev) : U;
+          if (uidx >= U) continue;
+          tSave = save_state(ckslot(), drain, true);
+        }
         lds_sync();  // ring reads (checkpoint) done before the urgent tiles overwrite it
         if (tid == 0) {
           const int64_t t1 = wall_ticks();
@@ -478,9 +579,9 @@ k_persistent_yield(const apk_yield_params) {
             P().claim_site[ev] = s;
             P().u_gt[2 * (size_t)ev] = t1;
           }
-          // Stage s+1 was issued, not waited for (one barrier per stage).
-          stat(ST_INFLIGHT, E::GROUP == 1 && live > 1 ? 1 : 0);
           stat(ST_SAVE, (uint64_t)(t1 - tSave));
+          stat(ST_INFLIGHT, (uint64_t)ckMoved);
+          stat(ST_STALE, (uint64_t)ckStale);
         }
         serving = ev;
         savedTask = task;
@@ -517,8 +618,11 @@ k_persistent_yield(const apk_yield_params) {
   if (P().run_gt && tid == 0 && fetch_add_u32(P().exit_count, 1u) == gridDim.x - 1)
     P().run_gt[1] = wall_ticks();
   if (P().stats && tid == 0) {
+    // Added, not stored: relaunches (retreat-arm continuations) may share rows.
     unsigned long long* st = P().stats + (size_t)row() * APK_STATS_PER_BLOCK;
-    for (int k = 0; k < APK_STATS_PER_BLOCK; ++k) st[k] = s_stats[k];
+    for (int k = 0; k < APK_STATS_PER_BLOCK; ++k)
+      if (s_stats[k])
+        __hip_atomic_fetch_add(&st[k], s_stats[k], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -536,7 +640,10 @@ static int validate(const apk_yield_params* p, int poll, int oracle, int blocks)
               "persistent_yield: operands above 2 GiB are not supported");
   APK_REQUIRE(blocks > 0, "persistent_yield: blocks=%d", blocks);
   APK_REQUIRE(p->num_tasks < (1u << 31), "persistent_yield: num_tasks=%u", p->num_tasks);
-  APK_REQUIRE(poll >= APK_POLL_OFF && poll <= APK_POLL_STAGE, "persistent_yield: poll=%d", poll);
+  APK_REQUIRE(poll >= APK_POLL_OFF && poll <= APK_POLL_ISSUE, "persistent_yield: poll=%d", poll);
+  if (poll == APK_POLL_ISSUE)
+    APK_REQUIRE(p->retreat == 0 && p->flag_system == 0,
+                "persistent_yield: issue sites are for the cooperative arm on a device flag");
   APK_REQUIRE(p->num_events >= 0, "persistent_yield: num_events < 0");
   if (poll != APK_POLL_OFF) {
     APK_REQUIRE(p->flag != nullptr, "persistent_yield: polling needs a flag");
@@ -594,15 +701,20 @@ static int launch_t(const apk_yield_params* p, int blocks, hipStream_t st) {
 template <class E, int POLL>
 static int launch_p(const apk_yield_params* p, int oracle, int blocks, hipStream_t st) {
   const bool sys = p->flag_system != 0;
-  if constexpr (POLL != APK_POLL_OFF) {
-    if (p->retreat > 0)  // device-memory flag only (validated)
-      return oracle ? launch_t<E, POLL, true, false, true>(p, blocks, st)
-                    : launch_t<E, POLL, false, false, true>(p, blocks, st);
+  if constexpr (POLL == APK_POLL_ISSUE) {  // cooperative arm, device flag (validated)
+    return oracle ? launch_t<E, POLL, true, false>(p, blocks, st)
+                  : launch_t<E, POLL, false, false>(p, blocks, st);
+  } else {
+    if constexpr (POLL != APK_POLL_OFF) {
+      if (p->retreat > 0)  // device-memory flag only (validated)
+        return oracle ? launch_t<E, POLL, true, false, true>(p, blocks, st)
+                      : launch_t<E, POLL, false, false, true>(p, blocks, st);
+    }
+    if (oracle) return sys ? launch_t<E, POLL, true, true>(p, blocks, st)
+                           : launch_t<E, POLL, true, false>(p, blocks, st);
+    return sys ? launch_t<E, POLL, false, true>(p, blocks, st)
+               : launch_t<E, POLL, false, false>(p, blocks, st);
   }
-  if (oracle) return sys ? launch_t<E, POLL, true, true>(p, blocks, st)
-                         : launch_t<E, POLL, true, false>(p, blocks, st);
-  return sys ? launch_t<E, POLL, false, true>(p, blocks, st)
-             : launch_t<E, POLL, false, false>(p, blocks, st);
 }
 
 template <class E>
@@ -613,7 +725,8 @@ static int launch_e(int poll, int oracle, const apk_yield_params* p, int blocks,
   switch (poll) {
     case APK_POLL_OFF: return launch_p<E, APK_POLL_OFF>(p, oracle, blocks, st);
     case APK_POLL_CHUNK: return launch_p<E, APK_POLL_CHUNK>(p, oracle, blocks, st);
-    default: return launch_p<E, APK_POLL_STAGE>(p, oracle, blocks, st);
+    case APK_POLL_STAGE: return launch_p<E, APK_POLL_STAGE>(p, oracle, blocks, st);
+    default: return launch_p<E, APK_POLL_ISSUE>(p, oracle, blocks, st);
   }
 }
 
@@ -646,30 +759,44 @@ extern "C" long long apk_yield_ckpt_floats(int engine) {
   }
 }
 
-extern "C" int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_per_cu) {
-  using namespace apk;
-  APK_REQUIRE(blocks_per_cu != nullptr, "occupancy: out is NULL");
+namespace apk {
+
+// Resident blocks per CU of the instantiation a launch with these settings
+// uses (the cooperative, device-flag one; its oracle, host-flag and retreat
+// twins differ only off the stage loop), at the engine's block size.
+template <class E>
+static int yield_occupancy_of(int poll, int* out) {
   int n = 0;
-  auto q = [&](auto kern, int threads) -> int {
-    APK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, threads, 0));
+  auto q = [&](auto kern) -> int {
+    APK_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, E::THREADS, 0));
     return APK_OK;
   };
   int rc;
-  switch (engine * 3 + poll) {
-    case 0: rc = q(k_persistent_yield<EngValu64, 0, false, false, false>, 256); break;
-    case 1: rc = q(k_persistent_yield<EngValu64, 1, false, false, false>, 256); break;
-    case 2: rc = q(k_persistent_yield<EngValu64, 2, false, false, false>, 256); break;
-    case 3: rc = q(k_persistent_yield<EngMfma128, 0, false, false, false>, 256); break;
-    case 4: rc = q(k_persistent_yield<EngMfma128, 1, false, false, false>, 256); break;
-    case 5: rc = q(k_persistent_yield<EngMfma128, 2, false, false, false>, 256); break;
-    case 6: rc = q(k_persistent_yield<EngBf16x256, 0, false, false, false>, 256); break;
-    case 7: rc = q(k_persistent_yield<EngBf16x256, 1, false, false, false>, 256); break;
-    case 8: rc = q(k_persistent_yield<EngBf16x256, 2, false, false, false>, 256); break;
+  switch (poll) {
+    case APK_POLL_OFF: rc = q(k_persistent_yield<E, APK_POLL_OFF, false, false, false>); break;
+    case APK_POLL_CHUNK: rc = q(k_persistent_yield<E, APK_POLL_CHUNK, false, false, false>); break;
+    case APK_POLL_STAGE: rc = q(k_persistent_yield<E, APK_POLL_STAGE, false, false, false>); break;
+    case APK_POLL_ISSUE: rc = q(k_persistent_yield<E, APK_POLL_ISSUE, false, false, false>); break;
     default:
-      set_error("occupancy: engine %d poll %d", engine, poll);
+      set_error("occupancy: poll %d", poll);
       return APK_EINVAL;
   }
   if (rc != APK_OK) return rc;
-  *blocks_per_cu = n;
+  *out = n;
   return APK_OK;
+}
+
+}  // namespace apk
+
+extern "C" int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_per_cu) {
+  using namespace apk;
+  APK_REQUIRE(blocks_per_cu != nullptr, "occupancy: out is NULL");
+  switch (engine) {
+    case APK_ENGINE_VALU64: return yield_occupancy_of<EngValu64>(poll, blocks_per_cu);
+    case APK_ENGINE_MFMA128: return yield_occupancy_of<EngMfma128>(poll, blocks_per_cu);
+    case APK_ENGINE_BF16X256: return yield_occupancy_of<EngBf16x256>(poll, blocks_per_cu);
+    default:
+      set_error("occupancy: engine %d", engine);
+      return APK_EINVAL;
+  }
 }

@@ -282,12 +282,14 @@ __device__ __forceinline__ uint64_t block_sum_u64(uint64_t v, uint64_t* red) {
 // Checkpoint slot layout (per slot, floats):
 //   [0, ACC_PER_THREAD*THREADS)        accumulators: float4 j of thread t at
 //                                      (j*THREADS + t)*4 -> coalesced 16 B/lane
-//   [ACC.., ACC.. + 2*STAGE/4)         the resident stages s, s+1 of the
-//                                      ring (positions 0, 1), byte for byte
+//   [ACC.., ACC.. + NS*STAGE/4)        the live stages s, s+1, ... of the ring
+//                                      (positions 0, 1, ...), byte for byte: two
+//                                      at a stage site, up to NS at an issue
+//                                      site
 template <class E>
 struct Ckpt {
   static constexpr int ACC_FLOATS = E::ACC_PER_THREAD * E::THREADS;
-  static constexpr int RING_FLOATS = 2 * E::STAGE / 4;
+  static constexpr int RING_FLOATS = E::NS * E::STAGE / 4;
   static constexpr int SLOT_FLOATS = ACC_FLOATS + RING_FLOATS;
 
   // Buffer stores/loads: one lane offset register, the float4 index in the
@@ -335,12 +337,14 @@ struct Ckpt {
     // drain the prefetched stages on every k-stage of every tile.
     wait_vmcnt<0>();
   }
-  // Copy n (<= 2) ring slots first, first+1 (mod NS) to / from checkpoint
-  // positions 0, 1.
+  // Copy n (<= NS) ring slots first, first+1, ... (mod NS) to / from
+  // checkpoint positions 0, 1, ...
+  // save_ring copies the newest stage (position n-1) first: without a drain
+  // it is the one whose loads may still be landing.
   static __device__ __forceinline__ void save_ring(const char* ring, float* slot,
                                                    int first, int n) {
     char* dst = (char*)(slot + ACC_FLOATS);
-    for (int k = 0; k < n; ++k) {
+    for (int k = n - 1; k >= 0; --k) {
       const int b = (first + k) % E::NS;
       for (int i = threadIdx.x * 16; i < E::STAGE; i += E::THREADS * 16)
         *(float4*)(dst + k * E::STAGE + i) = *(const float4*)(ring + b * E::STAGE + i);
@@ -355,6 +359,38 @@ struct Ckpt {
         *(float4*)(ring + b * E::STAGE + i) = *(const float4*)(src + k * E::STAGE + i);
     }
   }
+  // Whether any of the 16-byte pieces this thread saved with save_ring
+  // (same first, n) differs from the ring as it stands now. Call after every
+  // load into the ring has landed and the thread's own checkpoint stores
+  // have completed.
+  static __device__ __forceinline__ bool ring_differs(const char* ring, const float* slot,
+                                                      int first, int n) {
+    const char* src = (const char*)(slot + ACC_FLOATS);
+    bool d = false;
+    for (int k = 0; k < n; ++k) {
+      const int b = (first + k) % E::NS;
+      for (int i = threadIdx.x * 16; i < E::STAGE; i += E::THREADS * 16) {
+        const uint4 x = *(const uint4*)(ring + b * E::STAGE + i);
+        const uint4 y = *(const uint4*)(src + k * E::STAGE + i);
+        d |= (x.x != y.x) | (x.y != y.y) | (x.z != y.z) | (x.w != y.w);
+      }
+    }
+    return d;
+  }
 };
+
+// This thread's 16 bytes of the last direct-to-LDS load of the stage in ring
+// slot `sl`, read as they stand (a load still in flight has not yet written
+// them). The read completes before the function returns.
+template <class E>
+__device__ __forceinline__ uint4 probe_last_load(const char* ring, int sl) {
+  const volatile uint4* p = (const volatile uint4*)(ring + sl * E::STAGE +
+                                                    E::dma_lds_off(E::LOADS - 1) +
+                                                    16 * threadIdx.x);
+  const uint4 v = {p->x, p->y, p->z, p->w};
+  wait_lgkmcnt0();
+  asm volatile("" ::: "memory");
+  return v;
+}
 
 }  // namespace apk

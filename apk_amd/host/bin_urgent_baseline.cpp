@@ -384,10 +384,10 @@ int main(int argc, char** argv) {
       const EventResult er = rig.readEvents(0);
       for (int b = 0; b < blocks + retreatBlocks; ++b) {
         const unsigned long long* st = &er.stats[(size_t)b * APK_STATS_PER_BLOCK];
-        retreats += st[5];
-        resumed += st[6];
-        errors += st[7];
-        saveTicks += st[1];
+        retreats += st[APK_ST_RETREATS];
+        resumed += st[APK_ST_RESUMED];
+        errors += st[APK_ST_ERRORS];
+        saveTicks += st[APK_ST_SAVE];
       }
       const std::vector<unsigned long long> h = rig.readTaskHash((unsigned)bgTasks);
       for (int i = 0; i < bgTasks; ++i) hashBad += h[i] != refHash[i];

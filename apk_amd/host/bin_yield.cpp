@@ -21,9 +21,14 @@
 //                             tile_n x --k: urgent-tiles tiles of depth --k)
 //   --seed s                  glibc seed of A, B (21); schedule seed (21)
 //   --flag-copies c           replicas of the flag (block b polls b % c)
-// Host-set events (--set host) need a host-mapped flag and are not built in
-// this binary yet; the device setter (--set dev) is the primary mode, as in
-// the reference.
+// --set host (latency mode): the host raises each event itself (the
+// reference's registered definition, src/yield.cu:837-858). The flag lives in
+// host-mapped coherent memory (hipHostMalloc), the host stores the new
+// generation into it and the kernel samples it at system scope. Host times
+// are mapped onto the device clock with the spin_flag calibration
+// (src/yield.cu:782-813): 300 times, a one-wave kernel spins on the flag, the
+// host stores 1 and the kernel records the device tick at which it reads it;
+// the p50 of (device time - host time) is added to every host set time.
 #include <omp.h>
 
 #include <algorithm>
@@ -83,11 +88,13 @@ int main(int argc, char** argv) {
     fprintf(stderr, "bad --engine, --poll or --resume\n");
     return 1;
   }
-  if (setBy != "dev") {
-    fprintf(stderr, "--set %s: only the device setter (--set dev) is available\n",
-            setBy.c_str());
+  if (setBy != "dev" && setBy != "host") {
+    fprintf(stderr, "--set %s: expected dev or host\n", setBy.c_str());
     return 1;
   }
+  // Host-set events exist in latency mode only (src/yield.cu:836-858); the
+  // other modes use the device setter whatever --set says.
+  const bool hostSet = setBy == "host" && mode == "latency";
   if (pollEvery != 1 && pollEvery != 2 && pollEvery != 4 && pollEvery != 8) {
     fprintf(stderr, "--poll-every must be 1, 2, 4, or 8\n");
     return 1;
@@ -144,6 +151,7 @@ int main(int argc, char** argv) {
   shape.events = evCap;
   shape.hashTasks = (mode == "verify") ? tasks : 0;
   shape.flagCopies = flagCopies;
+  shape.hostFlag = hostSet;
   YieldRig rig(shape, hA, hB, hAu, hBu);
   hipStream_t kStream;
   HIP_CHECK(hipStreamCreateWithFlags(&kStream, hipStreamNonBlocking));
@@ -387,7 +395,7 @@ int main(int argc, char** argv) {
     for (size_t t = 0; t < hNow.size(); ++t)
       if (hNow[t] != hRef[t]) ++hashBad;
     uint64_t yields = 0;
-    for (int b = 0; b < blocks; ++b) yields += r.stats[(size_t)b * APK_STATS_PER_BLOCK];
+    for (int b = 0; b < blocks; ++b) yields += r.stats[(size_t)b * APK_STATS_PER_BLOCK + APK_ST_YIELDS];
     printf("yields taken: %llu | C bit-identical to the unpreempted run: %s | task "
            "fingerprints differing: %lld\n",
            (unsigned long long)yields, bitsSame ? "yes" : "NO", (long long)hashBad);
@@ -506,11 +514,72 @@ int main(int argc, char** argv) {
   printf("latency: probe %.3f us/task (%.2f TFLOP/s) | schedule %.1f ms, %d events (%s) | "
          "task bound %u\n", usPerTask, flopTask / (usPerTask * 1e-6) / 1e12, schedUs / 1e3,
          events, arrival.c_str(), lTasks);
+  const double nsPerTick = 1000.0 / dev.wall_mhz;
+  // Host<->device clock calibration (host-set mode), on the idle GPU.
+  long long offP50 = 0;
+  if (hostSet) {
+    long long* dOut;
+    HIP_CHECK(hipMalloc(&dOut, 2 * sizeof(long long)));
+    std::vector<double> offs;
+    const int calReps = 300;
+    const long long maxTicks = (long long)(100000.0 * dev.wall_mhz);  // 100 ms bound
+    for (int rep = 0; rep < calReps; ++rep) {
+      rig.hostSetFlag(0);
+      APK_CHECK(apk_spin_flag(rig.dFlag(), 1, maxTicks, dOut, kStream));
+      spin_for_ns(200000);  // let the spin kernel start
+      const int64_t h0 = now_ns();
+      rig.hostSetFlag(1);
+      HIP_CHECK(hipStreamSynchronize(kStream));
+      long long out[2];
+      HIP_CHECK(hipMemcpy(out, dOut, sizeof out, hipMemcpyDeviceToHost));
+      if (out[0] < 0) {
+        fprintf(stderr, "FAIL: calibration: the device did not see the host's flag store\n");
+        return 1;
+      }
+      offs.push_back((double)out[0] * nsPerTick - (double)h0);
+    }
+    const double offMin = percentile(offs, 0.0), p50 = percentile(offs, 0.5),
+                 p90 = percentile(offs, 0.9);
+    offP50 = (long long)p50;
+    // The absolute offset is the epoch difference of the two clocks; only
+    // its spread above the minimum is meaningful to read.
+    printf("host->device flag visibility (%d reps, min-referenced): p50 +%.1f us | p90 "
+           "+%.1f us\n", calReps, (p50 - offMin) / 1e3, (p90 - offMin) / 1e3);
+    HIP_CHECK(hipFree(dOut));
+  }
   rig.reset(false);
-  rig.setSchedule(gaps, dev.wall_mhz);
-  const long long stopTicks = (long long)(2000.0 * dev.wall_mhz);  // 2 ms after the last event
-  const auto [kernMs, hostMs] = timed_run(poll, lTasks, true, events, false, stopTicks);
-  const EventResult r = rig.readEvents(events);
+  std::vector<int64_t> hSet(events, 0);  // host-set times (host ns)
+  double kernMs = 0;
+  if (hostSet) {
+    hipEvent_t a, b;
+    HIP_CHECK(hipEventCreate(&a));
+    HIP_CHECK(hipEventCreate(&b));
+    HIP_CHECK(hipEventRecord(a, kStream));
+    rig.launch(poll, pollEvery, resume, 0, lTasks, false, events, false, kStream, 0);
+    HIP_CHECK(hipEventRecord(b, kStream));
+    spin_for_ns(50LL * 1000 * 1000);  // settle into steady state
+    const int64_t t0 = now_ns();
+    for (int e = 0; e < events; ++e) {
+      spin_until_ns(t0 + gaps[e]);
+      hSet[e] = now_ns();
+      rig.hostSetFlag(e + 1);
+    }
+    spin_for_ns(5LL * 1000 * 1000);
+    rig.hostSetFlag(-1);  // stop sentinel
+    HIP_CHECK(hipStreamSynchronize(kStream));
+    HIP_CHECK(hipGetLastError());
+    float ms = 0;
+    HIP_CHECK(hipEventElapsedTime(&ms, a, b));
+    kernMs = ms;
+  } else {
+    rig.setSchedule(gaps, dev.wall_mhz);
+    const long long stopTicks = (long long)(2000.0 * dev.wall_mhz);  // 2 ms after the last event
+    kernMs = timed_run(poll, lTasks, true, events, false, stopTicks).first;
+  }
+  EventResult r = rig.readEvents(events);
+  if (hostSet)  // host clock mapped onto the device clock
+    for (int e = 0; e < events; ++e)
+      r.setGT[e] = (long long)std::llround(((double)hSet[e] + (double)offP50) / nsPerTick);
   dump_obs1(dumpObsPath, r, events, blocks, dev.wall_mhz);
   const std::vector<EventRow> rows = summarize_events(r, events, blocks, dev.wall_mhz);
 
@@ -543,23 +612,25 @@ int main(int argc, char** argv) {
   if (csv) fclose(csv);
   uint64_t yields = 0, tSave = 0, tUrg = 0, tRest = 0;
   for (int b = 0; b < blocks; ++b) {
-    yields += r.stats[(size_t)b * APK_STATS_PER_BLOCK];
-    tSave += r.stats[(size_t)b * APK_STATS_PER_BLOCK + 1];
-    tUrg += r.stats[(size_t)b * APK_STATS_PER_BLOCK + 2];
-    tRest += r.stats[(size_t)b * APK_STATS_PER_BLOCK + 3];
+    yields += r.stats[(size_t)b * APK_STATS_PER_BLOCK + APK_ST_YIELDS];
+    tSave += r.stats[(size_t)b * APK_STATS_PER_BLOCK + APK_ST_SAVE];
+    tUrg += r.stats[(size_t)b * APK_STATS_PER_BLOCK + APK_ST_URGENT];
+    tRest += r.stats[(size_t)b * APK_STATS_PER_BLOCK + APK_ST_RESTORE];
   }
   printf("\n--- latency (%s-set, poll-every=%d, %d blocks): %zu events (%d warmup discarded, "
          "%d anomalies, %d unset) ---\n", setBy.c_str(), pollEvery, blocks, lat.size(),
          std::min(warmupEvents, events), anomalies, unset);
   printf("kernel %.1f ms for the %.1f ms schedule\n", kernMs, schedUs / 1e3);
   if (!lat.empty()) {
-    printf("setter (block 0) was last observer in %.1f%% of events; its own delay p50 %.2f us\n",
-           100.0 * lastIsSetter / lat.size(), percentile(b0Delay, 0.5));
+    if (!hostSet)
+      printf("setter (block 0) was last observer in %.1f%% of events; its own delay p50 %.2f "
+             "us\n", 100.0 * lastIsSetter / lat.size(), percentile(b0Delay, 0.5));
     printf("preemption latency set->last (us): p50 %.2f | p90 %.2f | p99 %.2f | max %.2f\n",
            percentile(lat, 0.5), percentile(lat, 0.9), percentile(lat, 0.99),
            *std::max_element(lat.begin(), lat.end()));
-    printf("  excluding setter block 0:       p50 %.2f | p90 %.2f | p99 %.2f\n",
-           percentile(latX0, 0.5), percentile(latX0, 0.9), percentile(latX0, 0.99));
+    if (!hostSet)
+      printf("  excluding setter block 0:       p50 %.2f | p90 %.2f | p99 %.2f\n",
+             percentile(latX0, 0.5), percentile(latX0, 0.9), percentile(latX0, 0.99));
     printf("first observer delay (us):        p50 %.2f | p99 %.2f\n",
            percentile(firstDelay, 0.5), percentile(firstDelay, 0.99));
     printf("observation spread first->last (us): p50 %.2f | p99 %.2f\n",

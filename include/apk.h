@@ -131,13 +131,44 @@ int apk_persistent_gemm(int engine, const void* A, const void* B, float* C,
  *   APK_RESUME_RESTART   : abandon the tile, restart it from k = 0 (the
  *                          reference's semantics, src/midyield.cu:237-258)
  * All three produce bit-identical C: the per-tile k order never changes.
+ *
+ * APK_POLL_ISSUE is the window-forcing site of the drain experiment
+ * (src/midyield.cu:246-258): the flag is sampled as for APK_POLL_STAGE, but a
+ * new generation is acted on at the top of the NEXT stage iteration, right
+ * after the compute that issued the following stage's loads and before any
+ * wait, so both live stages may still be in flight. Every block that sees
+ * the generation checkpoints at once (drain: after vmcnt(0); naive: without
+ * it) and only then pops the event's mini-queue; blocks that get no urgent
+ * tile continue with their state intact. Cooperative arm only, device flag
+ * only.
  */
-enum { APK_POLL_OFF = 0, APK_POLL_CHUNK = 1, APK_POLL_STAGE = 2 };
+enum { APK_POLL_OFF = 0, APK_POLL_CHUNK = 1, APK_POLL_STAGE = 2, APK_POLL_ISSUE = 3 };
 /* The flag may be replicated so that no single address is polled by every
  * CU: copy c lives at byte offset c * APK_FLAG_STRIDE. */
 #define APK_FLAG_STRIDE 4096
 #define APK_FLAG_MAX_COPIES 256
-#define APK_STATS_PER_BLOCK 8
+/* Per-block statistics of the yield kernel, APK_STATS_PER_BLOCK u64 each. */
+#define APK_STATS_PER_BLOCK 16
+enum {
+  APK_ST_YIELDS = 0,    /* cooperative yields served */
+  APK_ST_SAVE = 1,      /* ticks spent checkpointing */
+  APK_ST_URGENT = 2,    /* ticks spent on urgent tiles */
+  APK_ST_RESTORE = 3,   /* ticks spent restoring */
+  APK_ST_INFLIGHT = 4,  /* resumed checkpoints (served yields; at issue sites
+                           every observer) at which a live stage was observed
+                           still in flight when the drain (naive: the save)
+                           began: the last direct-to-LDS load of the newest
+                           stage had not yet written its LDS bytes */
+  APK_ST_RETREATS = 5,  /* retreats (retreat arm) */
+  APK_ST_RESUMED = 6,   /* resume-queue entries taken */
+  APK_ST_ERRORS = 7,    /* resume entries never published in time (lost) */
+  APK_ST_STALE = 8,     /* resumed checkpoints holding LDS stages that differ
+                           from the stages once every load had landed (naive
+                           only); each resumes a wrong tile */
+  APK_ST_CHECKPOINTS = 9, /* checkpoints taken (issue sites: every observer) */
+  APK_ST_INFLIGHT_ALL = 10, /* APK_ST_INFLIGHT over every checkpoint taken */
+  APK_ST_STALE_ALL = 11     /* APK_ST_STALE over every checkpoint taken */
+};
 
 /* Work queue: every persistent kernel pops tasks from APK_QUEUE_WORDS
  * unsigned counters (zero at launch). The tiles are split into
@@ -197,9 +228,9 @@ typedef struct apk_yield_params {
   /* verification and statistics (each may be NULL) */
   unsigned long long* task_hash; /* [num_tasks] fingerprint of each completed task */
   unsigned long long* u_hash;    /* [events * urgent tiles] */
-  unsigned long long* stats;     /* [blocks * APK_STATS_PER_BLOCK]: yields, save,
-                                    urgent, restore ticks, yields that drained a
-                                    stage still in flight, 3 reserved */
+  unsigned long long* stats;     /* [blocks * APK_STATS_PER_BLOCK], APK_ST_*;
+                                    added to (atomically) at block exit, so
+                                    launches may share rows; 0 at launch */
   /* exactly-once oracle (used by the oracle instantiation only) */
   int* exec_count;             /* [num_tasks] */
   int* u_exec_count;           /* [events] */
@@ -209,7 +240,8 @@ typedef struct apk_yield_params {
   long long cu_event_stride;
   /* 1 = skip the drain (vmcnt 0) before the checkpoint -- the reference's
    * "naive" discipline (src/midyield.cu:180-200) as a control experiment:
-   * a live stage still in flight is checkpointed stale. 0 = drain. */
+   * a live stage still in flight is checkpointed stale (APK_ST_STALE counts
+   * it; the resumed tile then differs). 0 = drain. */
   int naive;
   /* run timeline (src/urgent_baseline.cu:66-88), may be NULL: run_gt[0] =
    * block 0's start, run_gt[1] = exit of the last block; exit_count must be
@@ -267,6 +299,16 @@ long long apk_yield_ckpt_floats(int engine);
  * Replaces the reference's host flag write (cudaMemcpyAsync of the flag on a
  * control stream, src/yield.cu:845-858). */
 int apk_raise_flag(int* flag, int flag_copies, int value, long long* set_gt, void* stream);
+
+/* Host<->device clock calibration probe (spin_flag, src/yield.cu:206-214):
+ * one wave spins on *flag until it reads non-zero and stores the device
+ * wall-clock tick of that read into out[0] and the value read into out[1].
+ * system_scope = 1 for a host-mapped flag (the host-set mode), 0 for device
+ * memory. The spin is bounded: after max_ticks (> 0) without a non-zero read
+ * it stores out[0] = -1 and returns, so a flag the host never writes cannot
+ * hang the GPU. out: 2 device (or host-mapped) long longs. */
+int apk_spin_flag(const int* flag, int system_scope, long long max_ticks, long long* out,
+                  void* stream);
 
 /* Resident blocks per CU of the preemptible kernel. */
 int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_per_cu);

@@ -63,7 +63,7 @@ class Job:
         self.u_exec = T.zeros(E, dtype=i32, device="cuda")
 
     def run(self, poll, resume=0, gap_ticks=300, poison=0, use_oracle=False, events=None,
-            copies=1, poll_every=1):
+            copies=1, poll_every=1, naive=0):
         T, apk = self.t, self.apk
         ev = self.events if events is None else events
         for x in (self.nxt, self.flag, self.set_gt, self.obs, self.claim, self.u_gt,
@@ -89,7 +89,7 @@ class Job:
         p.set_gt, p.obs_gt = self.set_gt.data_ptr(), self.obs.data_ptr()
         p.claim, p.claim_site = self.claim.data_ptr(), self.site.data_ptr()
         p.u_gt, p.u_end_max = self.u_gt.data_ptr(), self.u_end.data_ptr()
-        p.resume, p.ckpt, p.poison = resume, self.ckpt.data_ptr(), poison
+        p.resume, p.ckpt, p.poison, p.naive = resume, self.ckpt.data_ptr(), poison, naive
         p.task_hash, p.u_hash, p.stats = (self.task_hash.data_ptr(), self.u_hash.data_ptr(),
                                           self.stats.data_ptr())
         p.exec_count = self.exec_count.data_ptr() if use_oracle else None
@@ -225,3 +225,57 @@ def test_mfma128_sparse_polls_and_flag_copies(torch_gpu, apk, mfma_job, poll_eve
     _assert_run_exact(j, r, off["C"], ref_h, u_ref_h)
     sites = r["site"][r["set_gt"] != 0]
     assert (sites % poll_every == 0).all(), sites   # yields only at poll sites
+
+
+def _stat(r, apk, col):
+    return int(r["stats"][:, col].sum())
+
+
+def test_mfma128_issue_site_drain(torch_gpu, apk, mfma_job):
+    """Issue sites (checkpoint before any wait, then pop): with the drain the
+    result stays bit-identical and no checkpoint is ever stale."""
+    say("mfma128 issue-site yields, drain")
+    j = mfma_job
+    off = j.run(apk.POLL_OFF, events=0)
+    ref_h = j.tile_hashes(off["C"])
+    _, u_ref_h = j.urgent_reference()
+    # Events far enough apart that a block is back at a site before the next
+    # one: every observer checkpoints and restores (~10 us), and a block that
+    # sees several new generations serves only the newest (src/yield.cu:155-183).
+    r = j.run(apk.POLL_ISSUE, resume=apk.RESUME_CKPT_FULL, gap_ticks=2000, use_oracle=True)
+    fired = _assert_run_exact(j, r, off["C"], ref_h, u_ref_h)
+    dup, missed, _ = oracle.count_tasks(r["exec"])
+    assert (dup, missed) == (0, 0)
+    assert _stat(r, apk, apk.ST_STALE_ALL) == 0
+    # every block that sees an event checkpoints at the issue site and resumes
+    assert _stat(r, apk, apk.ST_CHECKPOINTS) >= fired
+    assert _stat(r, apk, apk.ST_INFLIGHT) == _stat(r, apk, apk.ST_INFLIGHT_ALL)
+    say(f"  fired {fired}, checkpoints {_stat(r, apk, apk.ST_CHECKPOINTS)}, in flight at the "
+        f"drain {_stat(r, apk, apk.ST_INFLIGHT_ALL)}")
+
+
+def test_mfma128_issue_site_naive_control(torch_gpu, apk, mfma_job):
+    """Naive at issue sites: the checkpoint may capture a stage still in
+    flight; a resumed task differs from the unpreempted tile only if a
+    checkpoint it resumed from was observed stale (a task resumed stale twice
+    differs once). Urgent tiles are never affected (their loads land after the
+    stale ones)."""
+    say("mfma128 issue-site yields, naive")
+    j = mfma_job
+    off = j.run(apk.POLL_OFF, events=0)
+    ref_h = j.tile_hashes(off["C"])
+    _, u_ref_h = j.urgent_reference()
+    r = j.run(apk.POLL_ISSUE, resume=apk.RESUME_CKPT_FULL, gap_ticks=2000, naive=1)
+    ok = r["set_gt"] != 0
+    fired = int(ok.sum())
+    assert fired >= 5
+    uh = r["u_hash"][:len(r["set_gt"]) * j.U].reshape(-1, j.U)[ok]
+    assert (uh == u_ref_h[None, :]).all(), "urgent tile differs"
+    want = ref_h[np.arange(j.num_tasks) % j.tiles]
+    bad = int((r["task_hash"] != want).sum())
+    stale = _stat(r, apk, apk.ST_STALE)
+    assert bad <= stale and (bad == 0) == (stale == 0), (bad, stale)
+    assert stale == _stat(r, apk, apk.ST_STALE_ALL)  # every checkpoint is resumed
+    say(f"  fired {fired}, checkpoints {_stat(r, apk, apk.ST_CHECKPOINTS)}, in flight "
+        f"{_stat(r, apk, apk.ST_INFLIGHT_ALL)}, stale {_stat(r, apk, apk.ST_STALE_ALL)}, "
+        f"stale resumed {stale} = corrupted tasks {bad}")
