@@ -103,10 +103,11 @@ def test_yield_rejects_bad_args():
     p.Mu, p.Nu, p.Ku = 100, 128, 32
     rc = lib.apk_persistent_yield(apk_amd.ENGINE_MFMA128, apk_amd.POLL_STAGE, 0, ctypes.byref(p), 1, None)
     assert rc == apk_amd.APK_EINVAL and b"urgent" in lib.apk_last_error()
-    # accumulators (64 floats x 256 threads) + the two resident 32 KiB stages
-    assert apk_amd.ckpt_floats(apk_amd.ENGINE_MFMA128) == 64 * 256 + 2 * 32 * 1024 // 4
-    assert apk_amd.ckpt_floats(apk_amd.ENGINE_VALU64) == 16 * 256 + 2 * 16 * 1024 // 4
-    assert apk_amd.ckpt_floats(apk_amd.ENGINE_BF16X256) == 128 * 512 + 2 * 32 * 1024 // 4
+    # accumulators (floats per thread x threads) + every ring slot (an issue
+    # site keeps up to NS live stages: 3 x 32 KiB, 3 x 16 KiB, 4 x 32 KiB)
+    assert apk_amd.ckpt_floats(apk_amd.ENGINE_MFMA128) == 64 * 256 + 3 * 32 * 1024 // 4
+    assert apk_amd.ckpt_floats(apk_amd.ENGINE_VALU64) == 16 * 256 + 3 * 16 * 1024 // 4
+    assert apk_amd.ckpt_floats(apk_amd.ENGINE_BF16X256) == 128 * 512 + 4 * 32 * 1024 // 4
 
 
 def test_python_constants_match_header():
