@@ -105,6 +105,7 @@ _SIGNATURES = {
     "apk_engine_geometry_of": (_I, [_I, ctypes.POINTER(EngineGeometry)]),
     "apk_persistent_gemm_occupancy": (_I, [_I, ctypes.POINTER(_I)]),
     "apk_persistent_gemm": (_I, [_I, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
+    "apk_persistent_gemm_noalloc": (_I, [_I, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P]),
     "apk_persistent_yield": (_I, [_I, _I, _I, ctypes.POINTER(YieldParams), _I, _P]),
     "apk_yield_ckpt_floats": (ctypes.c_longlong, [_I]),
     "apk_persistent_yield_occupancy": (_I, [_I, _I, ctypes.POINTER(_I)]),
@@ -169,6 +170,13 @@ def persistent_gemm(engine, A, B, C, M, N, K, k_chunk, next_task, log, blocks,
     """Launch apk_persistent_gemm on device pointers (ints). Asynchronous."""
     check(load().apk_persistent_gemm(engine, A, B, C, M, N, K, k_chunk,
                                      next_task, log, blocks, stream))
+
+
+def persistent_gemm_noalloc(engine, A, B, C, M, N, K, k_chunk, log, blocks, stream=0):
+    """Launch apk_persistent_gemm_noalloc (queue counters in the library's own
+    device array; no allocation). Asynchronous."""
+    check(load().apk_persistent_gemm_noalloc(engine, A, B, C, M, N, K, k_chunk, log,
+                                             blocks, stream))
 
 
 def yield_occupancy(engine, poll):

@@ -8,6 +8,7 @@
 // preemptible variants poll, and here they are where per-chunk timing
 // records are taken.
 #include <climits>
+#include <mutex>
 
 #include "capi.hpp"
 #include "engine_bf16x256.hpp"
@@ -82,11 +83,9 @@ __global__ void __launch_bounds__(E::THREADS) __attribute__((amdgpu_waves_per_eu
 }
 
 template <class E>
-static int launch_persistent_gemm(const void* A, const void* B, float* C,
-                                  int M, int N, int K, int kChunk,
-                                  unsigned* next, apk_tile_record* log,
-                                  int blocks, hipStream_t st) {
-  APK_REQUIRE(A && B && C && next, "persistent_gemm: NULL pointer");
+static int validate_persistent_gemm(const void* A, const void* B, float* C, int M, int N, int K,
+                                    int kChunk, int blocks) {
+  APK_REQUIRE(A && B && C, "persistent_gemm: NULL pointer");
   APK_REQUIRE(M > 0 && N > 0 && K > 0, "persistent_gemm: empty shape");
   APK_REQUIRE(M % E::TM == 0 && N % E::TN == 0,
               "persistent_gemm: M=%d N=%d not multiples of the %dx%d tile", M, N,
@@ -99,9 +98,54 @@ static int launch_persistent_gemm(const void* A, const void* B, float* C,
                   (size_t)M * N < (1ull << 31),
               "persistent_gemm: operands above 2 GiB are not supported");
   APK_REQUIRE(blocks > 0, "persistent_gemm: blocks=%d", blocks);
+  return APK_OK;
+}
+
+template <class E>
+static int launch_persistent_gemm(const void* A, const void* B, float* C,
+                                  int M, int N, int K, int kChunk,
+                                  unsigned* next, apk_tile_record* log,
+                                  int blocks, hipStream_t st) {
+  const int rc = validate_persistent_gemm<E>(A, B, C, M, N, K, kChunk, blocks);
+  if (rc != APK_OK) return rc;
+  APK_REQUIRE(next != nullptr, "persistent_gemm: next_task is NULL");
   hipLaunchKernelGGL(k_persistent_gemm<E>, dim3(blocks), dim3(E::THREADS), 0, st,
                      A, B, C, M, N, K, kChunk, next, log);
   APK_LAUNCHED();
+  return APK_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free variant (apk_persistent_gemm_noalloc): the work-queue
+// counters live in this file-scope array instead of a caller buffer. In host
+// code `scratch` only names the variable; its device address, one per GPU,
+// comes from hipGetSymbolAddress on the first call made with that GPU
+// current and is the only form in which host code uses it.
+static __device__ __align__(256) unsigned scratch[APK_NOALLOC_SCRATCH_WORDS];
+static_assert(APK_QUEUE_WORDS <= APK_NOALLOC_SCRATCH_WORDS, "queue counters must fit scratch");
+
+constexpr int kMaxDevices = 64;
+static unsigned* g_scratch[kMaxDevices];  // device address of `scratch`, per GPU
+static std::mutex g_scratch_mu;
+
+// The counters start every launch at zero. A kernel, not hipMemsetAsync, so
+// that the sequence can be captured into a graph and replayed.
+__global__ void __launch_bounds__(64) k_zero_words(unsigned* p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
+static int scratch_of_current_device(unsigned** out) {
+  int dev = -1;
+  APK_HIP(hipGetDevice(&dev));
+  APK_REQUIRE(dev >= 0 && dev < kMaxDevices, "persistent_gemm_noalloc: device %d", dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    void* p = nullptr;
+    APK_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+    APK_REQUIRE(p != nullptr, "persistent_gemm_noalloc: no device address for scratch");
+    g_scratch[dev] = (unsigned*)p;
+  }
+  *out = g_scratch[dev];
   return APK_OK;
 }
 
@@ -151,4 +195,33 @@ extern "C" int apk_persistent_gemm_occupancy(int engine, int* blocks_per_cu) {
       set_error("occupancy: unknown engine %d", engine);
       return APK_EINVAL;
   }
+}
+
+extern "C" int apk_persistent_gemm_noalloc(int engine, const void* A, const void* B, float* C,
+                                           int M, int N, int K, int k_chunk,
+                                           apk_tile_record* log, int blocks, void* stream) {
+  using namespace apk;
+  int rc;
+  switch (engine) {
+    case APK_ENGINE_VALU64:
+      rc = validate_persistent_gemm<EngValu64>(A, B, C, M, N, K, k_chunk, blocks);
+      break;
+    case APK_ENGINE_MFMA128:
+      rc = validate_persistent_gemm<EngMfma128>(A, B, C, M, N, K, k_chunk, blocks);
+      break;
+    case APK_ENGINE_BF16X256:
+      rc = validate_persistent_gemm<EngBf16x256>(A, B, C, M, N, K, k_chunk, blocks);
+      break;
+    default:
+      set_error("persistent_gemm_noalloc: unknown engine %d", engine);
+      return APK_EINVAL;
+  }
+  if (rc != APK_OK) return rc;
+  unsigned* q = nullptr;
+  rc = scratch_of_current_device(&q);
+  if (rc != APK_OK) return rc;
+  hipLaunchKernelGGL(k_zero_words, dim3(1), dim3(64), 0, as_stream(stream), q,
+                     (int)APK_QUEUE_WORDS);
+  APK_LAUNCHED();
+  return apk_persistent_gemm(engine, A, B, C, M, N, K, k_chunk, q, log, blocks, stream);
 }

@@ -107,6 +107,25 @@ int apk_persistent_gemm(int engine, const void* A, const void* B, float* C,
                         unsigned int* next_task, apk_tile_record* log,
                         int blocks, void* stream);
 
+/* Allocation-free variant of apk_persistent_gemm. No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops). Same arguments and results as
+ * apk_persistent_gemm minus next_task: the work-queue counters (APK_QUEUE_WORDS
+ * unsigned) live in a file-scope device array of APK_NOALLOC_SCRATCH_WORDS
+ * words (256 bytes) that every GPU the library runs on holds until the process
+ * ends. Its size does not depend on the GEMM, so no input can exceed it; the
+ * arguments are checked as for apk_persistent_gemm (same errors). Each call
+ * first clears the counters with a one-wave kernel on `stream`, then launches
+ * the GEMM on it; the function calls no hipMalloc, hipFree or other allocating
+ * routine (the first call on a device looks up the array's device address
+ * with hipGetSymbolAddress). All calls on one GPU share the array: calls that
+ * overlap on one GPU (different streams, or different host threads) race and
+ * must be serialised by the caller; calls in order on one stream are safe. */
+#define APK_NOALLOC_SCRATCH_WORDS 64
+int apk_persistent_gemm_noalloc(int engine, const void* A, const void* B, float* C,
+                                int M, int N, int K, int k_chunk, apk_tile_record* log,
+                                int blocks, void* stream);
+
 /* ------------------------------------------------------------------------
  * Preemptible persistent GEMM (cooperative arm).
  *
