@@ -81,6 +81,7 @@ class YieldParams(ctypes.Structure):
         ("rq_entry", ctypes.c_void_p), ("rq_slots", ctypes.c_void_p),
         ("rq_capacity", ctypes.c_uint), ("continuation", ctypes.c_int),
         ("block_base", ctypes.c_int), ("obs_stride", ctypes.c_int),
+        ("launch_epoch", ctypes.c_int),
     ]
 
 
@@ -111,6 +112,7 @@ _SIGNATURES = {
     "apk_persistent_yield_occupancy": (_I, [_I, _I, ctypes.POINTER(_I)]),
     "apk_raise_flag": (_I, [_P, _I, _I, _P, _P]),
     "apk_spin_flag": (_I, [_P, _I, ctypes.c_longlong, _P, _P]),
+    "apk_clock_probe": (_I, [_P, _I, ctypes.c_longlong, _P]),
     "apk_tiny_oracle": (_I, [ctypes.POINTER(TinyParams), _I, _P]),
 }
 
@@ -200,6 +202,13 @@ def spin_flag(flag, system_scope, max_ticks, out, stream=0):
     reads non-zero; out[0] = device tick of that read (-1 on timeout),
     out[1] = the value. Asynchronous."""
     check(load().apk_spin_flag(flag, 1 if system_scope else 0, max_ticks, out, stream))
+
+
+def clock_probe(out, blocks, window_ticks, stream=0):
+    """Queue apk_clock_probe: `blocks` one-wave blocks count shader-clock
+    cycles and wall ticks over window_ticks; out = 4 long longs per block
+    (cycles, ticks, xcd, start tick). Asynchronous."""
+    check(load().apk_clock_probe(out, blocks, window_ticks, stream))
 
 
 def persistent_yield(engine, poll, oracle, params, blocks, stream=0):

@@ -100,8 +100,11 @@ k_persistent_yield(const apk_yield_params) {
     __syncthreads();
     const int f0 = (int)uniform(s_u32);
     __syncthreads();
+    // A retreat-arm continuation starts from the generation it follows
+    // (launch_epoch), so that one raised before it got its CUs still counts.
+    const int seen = P().launch_epoch > 0 ? P().launch_epoch : f0;
     if (f0 < 0) fLatest = f0;
-    else lastSeen = f0 < P().num_events ? f0 : P().num_events;
+    else lastSeen = seen < P().num_events ? seen : P().num_events;
   }
   enum { ST_YIELDS = APK_ST_YIELDS, ST_SAVE = APK_ST_SAVE, ST_URGENT = APK_ST_URGENT,
          ST_RESTORE = APK_ST_RESTORE, ST_INFLIGHT = APK_ST_INFLIGHT,
@@ -164,6 +167,7 @@ k_persistent_yield(const apk_yield_params) {
     int srcKind = FRESH, s = 0, siteDone = -1;
     const float* src = nullptr;
     bool urgent = false;
+    int rqHeld = -1;  // resume ticket whose checkpoint this job reads back
     if (!RETREAT && serving >= 0) {
       if (uidx < nU()) {
         urgent = true;
@@ -197,13 +201,16 @@ k_persistent_yield(const apk_yield_params) {
         if constexpr (retreatArm) {
           const unsigned q = rq_pop(P().rq_ctl);
           if (q != RQ_NONE) {
-            const int ready = rq_wait_ready(P().rq_entry + (size_t)q * 4);
+            int* en = P().rq_entry + (size_t)(q % P().rq_capacity) * 4;
+            const int ready = rq_wait_ready(en, q);
             if (ready > 0) {
-              t = (unsigned)P().rq_entry[(size_t)q * 4];
-              st = P().rq_entry[(size_t)q * 4 + 1];
+              t = (unsigned)en[0];
+              st = en[1];
               kind = ready - 1;
               tk = (int)q;
               stat(ST_RESUMED, 1);
+              // a restart entry carries no checkpoint: free it at once
+              if (kind == 0) rq_release(en, q, P().rq_capacity);
             } else {
               stat(ST_ERRORS, 1);  // never published within the deadline: the task is lost
               t = 0xfffffffeu;
@@ -226,9 +233,10 @@ k_persistent_yield(const apk_yield_params) {
       if (task == 0xfffffffeu) continue;  // lost resume entry (counted)
       if (task >= P().num_tasks) break;
       if (retreatArm && kind > 0) {
-        src = P().rq_slots + (size_t)qTicket * Ckpt<E>::SLOT_FLOATS;
+        src = P().rq_slots + (size_t)((unsigned)qTicket % P().rq_capacity) * Ckpt<E>::SLOT_FLOATS;
         s = qStage;
         srcKind = kind;
+        rqHeld = qTicket;
       }
     }
 
@@ -327,6 +335,17 @@ k_persistent_yield(const apk_yield_params) {
             issue_stage(s + 1, next_slot<E>(slot));
           }
           if (tid == 0 && src == ckslot()) stat(ST_RESTORE, (uint64_t)(wall_ticks() - tIn));
+          if constexpr (retreatArm) {
+            if (rqHeld >= 0) {
+              // every thread's reads of the entry's checkpoint have completed
+              // (load_acc / the ring restore wait for them): free the entry
+              __syncthreads();
+              if (tid == 0)
+                rq_release(P().rq_entry + (size_t)((unsigned)rqHeld % P().rq_capacity) * 4,
+                           (unsigned)rqHeld, P().rq_capacity);
+              rqHeld = -1;
+            }
+          }
         }
       }
 
@@ -513,23 +532,48 @@ k_persistent_yield(const apk_yield_params) {
         // workgroup runs only on a CU of its own shader engine: the urgent
         // kernel's R workgroups land in R domains the host cannot name, so
         // free ceil(R / 32) CUs in every (XCD, shader engine) domain.
+        // Which blocks retreat at generation f (launch_epoch in the params):
+        // the first grid by quota at f = 1; a continuation that follows an
+        // earlier generation, all of it -- it holds the CUs the previous
+        // generation freed, and it must complete for the next continuation
+        // (queued behind it) to start.
         const int quota = (P().retreat + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS;
         const int dom = (int)xcc_id() * APK_SES_PER_XCD + (int)se_id();
+        const bool cont = P().continuation != 0;
+        const bool newest = cont && P().launch_epoch > 0 && f > P().launch_epoch;
+        if (!newest && (cont || f != 1)) continue;  // not this block's turn: keep working
         unsigned t = RQ_NONE;
-        if (tid == 0 &&
-            fetch_add_i32(&P().retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + dom], 1) < quota)
-          t = rq_reserve(P().rq_ctl, P().rq_capacity);
+        if (tid == 0) {
+          int* rc = &P().retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + dom];
+          int c = 0;
+          if (newest)  // counted, but the count decides nothing: no round trip
+            __hip_atomic_fetch_add(rc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          else
+            c = fetch_add_i32(rc, 1);
+          if (newest || c < quota) {
+            t = rq_reserve(P().rq_ctl, P().rq_capacity, P().rq_entry);
+            if (t & RQ_FULL) {  // the ring stayed full: keep working
+              stat(ST_ERRORS, 1);
+              t = RQ_NONE;
+            }
+          }
+        }
         const unsigned tk = bcast(t);
         if (tk == RQ_NONE) continue;  // quota taken (or queue full): keep working
-        float* dst = P().rq_slots + (size_t)tk * Ckpt<E>::SLOT_FLOATS;
+        float* dst = P().rq_slots + (size_t)(tk % P().rq_capacity) * Ckpt<E>::SLOT_FLOATS;
         // always drain: nothing may land in LDS after the block exits
         const int64_t tSave = save_state(dst, true, false);
         const int rkind = P().resume == APK_RESUME_RESTART ? 0
                           : P().resume == APK_RESUME_CKPT_FULL ? 2 : 1;
-        __threadfence();  // this thread's checkpoint stores are visible device-wide
-        __syncthreads();
+        // Every thread's checkpoint stores have completed at this XCD's L2;
+        // after the barrier, the agent-scope release in rq_publish (one L2
+        // write-back, by thread 0 alone) makes all of them visible device-wide
+        // before the entry is published.
+        wait_vmcnt<0>();
+        lds_sync();
         if (tid == 0) {
-          rq_publish(P().rq_entry + (size_t)tk * 4, (int)task, rkind > 0 ? s : 0, rkind,
+          rq_publish(P().rq_entry + (size_t)(tk % P().rq_capacity) * 4, tk, (int)task,
+                     rkind > 0 ? s : 0, rkind,
                      (int)xcc_id() * APK_SES_PER_XCD + (int)se_id());
           const int64_t t1 = wall_ticks();
           stat(ST_RETREATS, 1);

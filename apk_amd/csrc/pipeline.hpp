@@ -55,25 +55,45 @@ struct TaskQueue {
 };
 
 // ---------------------------------------------------------------------------
-// Resume queue of the retreat arm: tickets [head, tail) in rq_ctl[0..1],
-// entry t = {task, stage, ready, domain} (ready = checkpoint kind + 1, written
-// last with a release), checkpoint slot t in a separate array. Tickets are
-// never reused within a job (capacity = retreats the job may take), so a
-// producer never waits; a consumer that has claimed ticket h waits for its
-// producer (a resident block on its exit path) with a bounded spin.
+// Resume queue of the retreat arm: a bounded ring of `cap` entries, tickets
+// [head, tail) in rq_ctl[0..1]. Entry i = {task, stage, seq, kind << 8 |
+// domain} with its checkpoint slot i; ticket t uses entry t % cap. `seq`
+// orders the entry's rounds (bounded MPMC ring with per-slot sequence
+// numbers): seq == t means free for ticket t, t + 1 published by ticket t's
+// producer, and the consumer of ticket t sets it to t + cap once it has read
+// the checkpoint back. A producer reserves a ticket only when its entry is
+// free (otherwise the ring is full and it declines the retreat), so it never
+// waits; a consumer claims the oldest reserved ticket and waits for its
+// producer (a resident block on its exit path) with a bounded spin. The host
+// sets seq = i for every entry before a job.
 constexpr unsigned RQ_NONE = 0xffffffffu;
 // Longest wait for a claimed entry to be published: 20 ms at the 100 MHz
 // wall clock. A producer publishes within microseconds; running out means a
 // lost task, which the exactly-once counts then report.
 constexpr int64_t RQ_WAIT_TICKS = 2000000;
 
-// Thread-0 only. Claims ticket `tail` unless the job's capacity is used up.
-__device__ __forceinline__ unsigned rq_reserve(unsigned* ctl, unsigned cap) {
-  for (;;) {
-    const unsigned t = __hip_atomic_load(&ctl[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (t >= cap) return RQ_NONE;
-    if (cas_u32(&ctl[1], t, t + 1) == t) return t;
+__device__ __forceinline__ int rq_seq_load(const int* en) {
+  return __hip_atomic_load(&en[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Thread-0 only. Takes the next ticket with one fetch-add (no CAS loop: the
+// producers of one generation arrive together, and a CAS loop would
+// serialise them round trip by round trip) and waits, bounded, for its entry
+// to be free. The ring holds several generations' retreats, so the entry is
+// free at once unless consumers have stalled; a ticket whose entry stays
+// taken for RQ_WAIT_TICKS is returned with RQ_FULL set: the caller does not
+// retreat and counts an error (that ticket's consumer then reports it lost
+// after its own bounded wait; no task is lost, the producer keeps its tile).
+constexpr unsigned RQ_FULL = 0x80000000u;
+__device__ __forceinline__ unsigned rq_reserve(unsigned* ctl, unsigned cap, const int* entries) {
+  const unsigned t = fetch_add_u32(&ctl[1], 1u);
+  const int* en = entries + (size_t)(t % cap) * 4;
+  if (rq_seq_load(en) == (int)t) return t;
+  const int64_t deadline = wall_ticks() + RQ_WAIT_TICKS;
+  while (rq_seq_load(en) != (int)t) {
+    if (wall_ticks() > deadline) return t | RQ_FULL;
+    __builtin_amdgcn_s_sleep(8);
   }
+  return t;
 }
 // Thread-0 only. Claims the oldest reserved ticket, or RQ_NONE if none.
 __device__ __forceinline__ unsigned rq_pop(unsigned* ctl) {
@@ -84,29 +104,36 @@ __device__ __forceinline__ unsigned rq_pop(unsigned* ctl) {
     if (cas_u32(&ctl[0], h, h + 1) == h) return h;
   }
 }
-// Thread-0 only, after every thread's checkpoint stores were fenced and a
-// barrier: entry fields, then `ready` with release semantics.
-__device__ __forceinline__ void rq_publish(int* en, int task, int stage, int kind,
-                                           int domain) {
+// Thread-0 only, after every thread's checkpoint stores have completed and a
+// barrier: entry fields, an agent-scope release (it writes back this XCD's
+// L2, which holds every thread's checkpoint stores, so one release by one
+// thread covers the block), then seq = ticket + 1.
+__device__ __forceinline__ void rq_publish(int* en, unsigned ticket, int task, int stage,
+                                           int kind, int domain) {
   en[0] = task;
   en[1] = stage;
-  en[3] = domain;  // where the retreat freed a CU: xcd * 4 + shader engine
-  __threadfence();
-  __hip_atomic_store(&en[2], kind + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  en[3] = (kind << 8) | domain;  // domain: where the retreat freed a CU (xcd * 4 + se)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __hip_atomic_store(&en[2], (int)(ticket + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Thread-0 only. Waits (bounded) for a claimed entry; returns ready (kind +
-// 1), or 0 if it was not published within RQ_WAIT_TICKS.
-__device__ __forceinline__ int rq_wait_ready(int* en) {
+// Thread-0 only. Waits (bounded) for claimed ticket h to be published;
+// returns its kind + 1, or 0 if it was not published within RQ_WAIT_TICKS.
+__device__ __forceinline__ int rq_wait_ready(const int* en, unsigned h) {
   const int64_t deadline = wall_ticks() + RQ_WAIT_TICKS;
   for (;;) {
-    const int r = __hip_atomic_load(&en[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (r != 0) {
+    if (rq_seq_load(en) == (int)(h + 1)) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      return r;
+      return (en[3] >> 8) + 1;
     }
     if (wall_ticks() > deadline) return 0;
     __builtin_amdgcn_s_sleep(8);
   }
+}
+// Thread-0 only, once every thread has read the entry's checkpoint back (a
+// barrier after the reads completed): frees the entry for ticket h + cap.
+__device__ __forceinline__ void rq_release(int* en, unsigned h, unsigned cap) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __hip_atomic_store(&en[2], (int)(h + cap), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // ---------------------------------------------------------------------------

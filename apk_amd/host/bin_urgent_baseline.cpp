@@ -81,6 +81,9 @@ int main(int argc, char** argv) {
   const std::string resumeS = parse_str(argc, argv, "--resume", "ckpt");
   const int retreatN = (int)parse_arg(argc, argv, "--retreat", urgentBlocks);
   const bool oracle = parse_arg(argc, argv, "--oracle", 0) != 0;
+  // --continuous 1 (with --yield 1): one background job, --events arrivals
+  const bool continuous = parse_arg(argc, argv, "--continuous", 0) != 0;
+  const int events = (int)parse_arg(argc, argv, "--events", 10000);
   const int poll = pollS == "stage" ? APK_POLL_STAGE : pollS == "chunk" ? APK_POLL_CHUNK : -1;
   const int resume = resumeS == "ckpt"      ? APK_RESUME_CKPT_FULL
                      : resumeS == "acc"     ? APK_RESUME_CKPT_ACC
@@ -181,14 +184,17 @@ int main(int argc, char** argv) {
   rs.K = K;
   rs.kChunk = kChunk;
   rs.blocks = blocks;
-  rs.events = 1;
+  rs.events = (yieldArm && continuous) ? std::max(events, 1) : 1;
   rs.runTimes = true;
   // Blocks that retreat per event: ceil(R / 32) in each of the 32 (XCD,
   // shader engine) dispatch domains.
   const int retreatBlocks =
       APK_RETREAT_DOMAINS * ((retreatN + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS);
   if (yieldArm) {
-    rs.retreatCap = (unsigned)retreatBlocks;
+    // one event's retreats per trial; a continuous job keeps four events'
+    // worth of entries in its ring (each event's are read back well before
+    // the next arrival)
+    rs.retreatCap = (unsigned)(continuous ? 4 * retreatBlocks : retreatBlocks);
     rs.extraRows = retreatBlocks + blocks;  // continuation + drain relaunch
     rs.hashTasks = (unsigned)bgTasks;
     if (oracle) rs.oracleTasks = (unsigned)bgTasks;
@@ -300,6 +306,216 @@ int main(int argc, char** argv) {
   const double drainEstUs = (be0 - bs0) * tickUs;
   printf("bg drain, no urgent: %.0f us for %d tasks on %d blocks\n", drainEstUs, bgTasks,
          blocks);
+
+  if (yieldArm && continuous) {
+    // --- Retreat arm, continuous: one background job on all workers, and the
+    // host raises each of `events` arrivals (exponential gaps, --mean-gap-us)
+    // as it falls due: [raise flag -> urgent GEMM] on the urgent stream, then
+    // the continuation that brings the retreated workers back on a third
+    // stream ordered after the urgent GEMM. The urgent GEMM is launched with
+    // apk_persistent_gemm_noalloc (no per-arrival counter buffer or memset).
+    const int T = tilesM * tilesN;
+    const std::vector<unsigned long long> tileHash = [&] {
+      rig.reserveTasks((unsigned)T, 0);
+      rig.reset(false);
+      rig.launchRetreat(poll, pollEvery, resume, (unsigned)T, retreatN, events, false, blocks, 0,
+                        false, rig.dRunGT(), rig.dExitCount(), bgStream);
+      HIP_CHECK(hipStreamSynchronize(bgStream));
+      return rig.readTaskHash((unsigned)T);
+    }();
+    std::vector<float> uRefBits((size_t)urgentM * urgentN);
+    {
+      HIP_CHECK(hipMemsetAsync(dUNext, 0, APK_QUEUE_WORDS * sizeof(unsigned), uStream));
+      APK_CHECK(apk_persistent_gemm(engine, dAu, dBu, dCu, urgentM, urgentN, urgentK, urgentK,
+                                    dUNext, nullptr, urgentBlocks, uStream));
+      HIP_CHECK(hipStreamSynchronize(uStream));
+      HIP_CHECK(hipMemcpy(uRefBits.data(), dCu, uRefBits.size() * 4, hipMemcpyDeviceToHost));
+    }
+    const std::vector<long long> gaps = arrival == "exp"
+                                            ? exp_schedule(seed, meanGapUs, events)
+                                            : uniform_schedule(seed, 150, 400, events);
+    const double settleUs = 20000.0, schedUs = gaps.back() / 1e3;
+    const double usPerTask = drainEstUs / bgTasks;
+    // Sized to outlast the schedule with margin; arrivals that still find the
+    // job finished are reported and left out of the latency.
+    const unsigned jobTasks =
+        (unsigned)std::min(1.3 * (settleUs + schedUs + 20000.0) / usPerTask, 2.0e9);
+    rig.reserveTasks(jobTasks, oracle ? jobTasks : 0);
+    const int keepCu = std::min(events, 64);  // urgent outputs kept per event
+    float* dCuAll;
+    long long* dRunC;
+    unsigned* dExitC;
+    apk_tile_record* dULogAll;
+    HIP_CHECK(hipMalloc(&dCuAll, (size_t)(keepCu + 1) * urgentM * urgentN * 4));
+    HIP_CHECK(hipMalloc(&dRunC, 2 * (size_t)events * sizeof(long long)));
+    HIP_CHECK(hipMalloc(&dExitC, (size_t)events * sizeof(unsigned)));
+    HIP_CHECK(hipMalloc(&dULogAll, (size_t)events * uTiles * sizeof(apk_tile_record)));
+    HIP_CHECK(hipMemset(dCuAll, 0xFF, (size_t)(keepCu + 1) * urgentM * urgentN * 4));
+    HIP_CHECK(hipMemset(dRunC, 0, 2 * (size_t)events * sizeof(long long)));
+    HIP_CHECK(hipMemset(dExitC, 0, (size_t)events * sizeof(unsigned)));
+    HIP_CHECK(hipMemset(dULogAll, 0, (size_t)events * uTiles * sizeof(apk_tile_record)));
+    hipStream_t cStream;
+    HIP_CHECK(hipStreamCreateWithFlags(&cStream, hipStreamNonBlocking));
+    hipEvent_t evU;
+    HIP_CHECK(hipEventCreateWithFlags(&evU, hipEventDisableTiming));
+    printf("continuous retreat arm: %d arrivals (%s, mean %.0f us) over one job of %u tasks "
+           "(%.0f us/task aggregate), %d retreats per arrival, resume ring of %u entries\n",
+           events, arrival.c_str(), meanGapUs, jobTasks, usPerTask, retreatBlocks,
+           rig.shape().retreatCap);
+
+    rig.reset(false);
+    rig.launchRetreat(poll, pollEvery, resume, jobTasks, retreatN, events, oracle, blocks, 0,
+                      false, rig.dRunGT(), rig.dExitCount(), bgStream);
+    spin_for_ns((int64_t)(settleUs * 1e3));
+    const int64_t t0 = now_ns();
+    for (int e = 0; e < events; ++e) {
+      spin_until_ns(t0 + gaps[e]);
+      float* cu = dCuAll + (size_t)std::min(e, keepCu) * urgentM * urgentN;
+      APK_CHECK(apk_raise_flag(rig.dFlag(), 1, e + 1, rig.dSetGT() + e, uStream));
+      APK_CHECK(apk_persistent_gemm_noalloc(engine, dAu, dBu, cu, urgentM, urgentN, urgentK,
+                                            urgentK, dULogAll + (size_t)e * uTiles,
+                                            urgentBlocks, uStream));
+      HIP_CHECK(hipEventRecord(evU, uStream));
+      HIP_CHECK(hipStreamWaitEvent(cStream, evU, 0));
+      rig.launchRetreat(poll, pollEvery, resume, jobTasks, retreatN, events, oracle,
+                        retreatBlocks, blocks, true, dRunC + 2 * (size_t)e, dExitC + e, cStream,
+                        e + 1);
+    }
+    HIP_CHECK(hipStreamSynchronize(uStream));
+    HIP_CHECK(hipStreamSynchronize(cStream));
+    HIP_CHECK(hipStreamSynchronize(bgStream));
+    RetreatResult rr = rig.readRetreat(events);
+    int lateDrains = 0;
+    while (rr.tail > rr.head && lateDrains < 4) {
+      // a block retreated after every worker had left: finish its tile
+      ++lateDrains;
+      rig.launchRetreat(poll, pollEvery, resume, jobTasks, retreatN, events, oracle, blocks,
+                        blocks, true, nullptr, nullptr, bgStream, events);
+      HIP_CHECK(hipStreamSynchronize(bgStream));
+      rr = rig.readRetreat(events);
+    }
+    HIP_CHECK(hipGetLastError());
+
+    auto [jobStart, bgEnd] = rig.readRunGT();
+    std::vector<long long> runC(2 * (size_t)events);
+    HIP_CHECK(hipMemcpy(runC.data(), dRunC, runC.size() * 8, hipMemcpyDeviceToHost));
+    long long jobEnd = bgEnd;
+    for (int e = 0; e < events; ++e) jobEnd = std::max(jobEnd, runC[2 * (size_t)e + 1]);
+    std::vector<apk_tile_record> ulog((size_t)events * uTiles);
+    HIP_CHECK(hipMemcpy(ulog.data(), dULogAll, ulog.size() * sizeof(apk_tile_record),
+                        hipMemcpyDeviceToHost));
+    std::vector<double> raise, uend, rfirst, rlast, cont;
+    int afterJob = 0, noRetreat = 0, notRun = 0;
+    FILE* csv = csvPath[0] ? fopen(csvPath, "w") : nullptr;
+    if (csv)
+      fprintf(csv, "event,set_ns,raise_to_ustart_us,urgent_end_us,retreat_first_us,"
+                   "retreat_last_us,retreats,cont_start_us,in_job\n");
+    for (int e = 0; e < events; ++e) {
+      const long long set = rr.setGT[e];
+      long long us = INT64_MAX, ue = 0;
+      for (int u = 0; u < uTiles; ++u) {
+        us = std::min<long long>(us, ulog[(size_t)e * uTiles + u].start);
+        ue = std::max<long long>(ue, ulog[(size_t)e * uTiles + u].end);
+      }
+      if (set == 0 || ue == 0) {
+        ++notRun;
+        continue;
+      }
+      int nr = 0;
+      for (int d = 0; d < APK_RETREAT_DOMAINS; ++d)
+        nr += std::min(rr.count[(size_t)e * APK_RETREAT_DOMAINS + d],
+                       retreatBlocks / APK_RETREAT_DOMAINS);
+      const bool inJob = set < jobEnd;
+      const double rf = nr ? (rr.retreatGT[2 * (size_t)e] - set) * tickUs : -1.0;
+      const double rl = nr ? (rr.retreatGT[2 * (size_t)e + 1] - set) * tickUs : -1.0;
+      const double cs = runC[2 * (size_t)e] ? (runC[2 * (size_t)e] - set) * tickUs : -1.0;
+      if (!inJob) {
+        ++afterJob;
+      } else {
+        if (nr == 0) ++noRetreat;
+        raise.push_back((us - set) * tickUs);
+        uend.push_back((ue - set) * tickUs);
+        if (nr) {
+          rfirst.push_back(rf);
+          rlast.push_back(rl);
+        }
+        if (cs >= 0) cont.push_back(cs);
+      }
+      if (csv)
+        fprintf(csv, "%d,%lld,%.2f,%.2f,%.2f,%.2f,%d,%.2f,%d\n", e,
+                (long long)(set * tickUs * 1e3), (us - set) * tickUs, (ue - set) * tickUs, rf,
+                rl, nr, cs, inJob ? 1 : 0);
+    }
+    if (csv) fclose(csv);
+
+    // Safety: every task's fingerprint against its tile's unpreempted one,
+    // every task exactly once, the kept urgent outputs bit for bit.
+    const std::vector<unsigned long long> h = rig.readTaskHash(jobTasks);
+    long long hashBad = 0, oracleBad = 0, uBad = 0;
+    for (unsigned i = 0; i < jobTasks; ++i) hashBad += h[i] != tileHash[i % (unsigned)T];
+    if (oracle) {
+      const std::vector<int> ex = rig.readExec(jobTasks);
+      for (unsigned i = 0; i < jobTasks; ++i) oracleBad += ex[i] != 1;
+    }
+    {
+      std::vector<float> cu((size_t)(keepCu + 1) * urgentM * urgentN);
+      HIP_CHECK(hipMemcpy(cu.data(), dCuAll, cu.size() * 4, hipMemcpyDeviceToHost));
+      const size_t n = (size_t)urgentM * urgentN;
+      for (int k = 0; k <= keepCu; ++k)
+        if (k < events) uBad += memcmp(cu.data() + k * n, uRefBits.data(), n * 4) != 0;
+    }
+    const EventResult er = rig.readEvents(0);
+    unsigned long long retreats = 0, resumed = 0, errors = 0, saveTicks = 0;
+    for (int b = 0; b < blocks + rs.extraRows; ++b) {
+      const unsigned long long* st = &er.stats[(size_t)b * APK_STATS_PER_BLOCK];
+      retreats += st[APK_ST_RETREATS];
+      resumed += st[APK_ST_RESUMED];
+      errors += st[APK_ST_ERRORS];
+      saveTicks += st[APK_ST_SAVE];
+    }
+    const double jobUs = (jobEnd - jobStart) * tickUs;
+    const double flopTask = 2.0 * geo.tile_m * geo.tile_n * (double)K;
+    const double tfJob = flopTask * jobTasks / (jobUs * 1e-6) / 1e12;
+    const double tfAlone = flopTask / (usPerTask * 1e-6) / 1e12;
+    const double tileUs = usPerTask * blocks / (K / kChunk);
+    printf("\n--- continuous retreat arm: %zu arrivals within the job (%d after it ended, %d "
+           "not run), poll %s every %d, %d retreats per arrival, resume %s ---\n",
+           raise.size(), afterJob, notRun, pollS.c_str(), pollEvery, retreatBlocks,
+           resumeS.c_str());
+    if (!raise.empty()) {
+      printf("preempt latency, flag raised -> urgent GEMM starts (us): p50 %.2f | p90 %.2f | "
+             "p99 %.2f | max %.2f\n", percentile(raise, 0.50), percentile(raise, 0.90),
+             percentile(raise, 0.99), *std::max_element(raise.begin(), raise.end()));
+      printf("urgent GEMM done after the flag (us): p50 %.2f | p99 %.2f\n",
+             percentile(uend, 0.5), percentile(uend, 0.99));
+    }
+    if (!rfirst.empty())
+      printf("retreat after the flag (us): first checkpoint start p50 %.2f | last exit p50 "
+             "%.2f p99 %.2f\n", percentile(rfirst, 0.5), percentile(rlast, 0.5),
+             percentile(rlast, 0.99));
+    if (!cont.empty())
+      printf("continuation starts after the flag (us): p50 %.2f | p99 %.2f\n",
+             percentile(cont, 0.5), percentile(cont, 0.99));
+    printf("tile (k-chunk) time at full residency: %.2f us -> p50 latency = %.3f tiles\n",
+           tileUs, raise.empty() ? -1.0 : percentile(raise, 0.5) / tileUs);
+    printf("background: %.2f TFLOP/s over the job with arrivals vs %.2f alone -> retreat "
+           "overhead %.2f%%\n", tfJob, tfAlone, (tfAlone / tfJob - 1.0) * 100.0);
+    printf("retreats %llu | resumed %llu | save %.2f us per retreat | arrivals without a "
+           "retreat %d | late drains %d | resume errors %llu | lost %u\n", retreats, resumed,
+           retreats ? saveTicks * tickUs / retreats : 0.0, noRetreat, lateDrains, errors,
+           rr.tail - rr.head);
+    printf("SAFETY: %lld of %u task fingerprints differ from the unpreempted tile | urgent "
+           "outputs not bit-identical: %lld of %d kept\n", hashBad, jobTasks, uBad,
+           std::min(events, keepCu + 1));
+    if (oracle)
+      printf("ORACLE: %s (%lld tasks not executed exactly once)\n",
+             oracleBad == 0 ? "PASS" : "FAIL", oracleBad);
+    if (csvPath[0]) printf("raw per-arrival records: %s\n", csvPath);
+    const bool pass = hashBad == 0 && uBad == 0 && rr.tail == rr.head && errors == 0 &&
+                      oracleBad == 0 && !raise.empty();
+    printf("yield: %s\n", pass ? "PASS" : "FAIL");
+    return pass ? 0 : 1;
+  }
 
   if (yieldArm) {
     // --- Retreat arm. Reference fingerprints of every task, unpreempted.

@@ -8,6 +8,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstring>
+#include <numeric>
 #include <string>
 #include <thread>
 #include <vector>
@@ -167,14 +168,44 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
   // Tile throughput with polling off (src/tcyield.cu:637-651).
   if (mode == "calibrate") {
     rig.reset(false);
-    timed_run(APK_POLL_OFF, (unsigned)blocks, false, 0, false);  // warm-up
+    const double warmMs = timed_run(APK_POLL_OFF, (unsigned)blocks, false, 0, false);
     rig.reset(false);
-    const double ms = timed_run(APK_POLL_OFF, tasks, false, 0, false);
+    // Engine clock during the timed run: one-wave probes on a side stream
+    // over 80% of the run's expected length (apk_clock_probe).
+    const int probes = 32;
+    long long* dProbe;
+    HIP_CHECK(hipMalloc(&dProbe, (size_t)probes * 4 * sizeof(long long)));
+    HIP_CHECK(hipMemset(dProbe, 0, (size_t)probes * 4 * sizeof(long long)));
+    hipStream_t side;
+    HIP_CHECK(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
+    const long long window = std::max(
+        1LL, (long long)(0.8 * warmMs * ((double)tasks / blocks) * 1e3 * dev.wall_mhz));
+    hipEvent_t a, b;
+    HIP_CHECK(hipEventCreate(&a));
+    HIP_CHECK(hipEventCreate(&b));
+    HIP_CHECK(hipEventRecord(a, kStream));
+    rig.launch(APK_POLL_OFF, 1, resume, 0, tasks, false, 0, false, kStream, 0, 0);
+    HIP_CHECK(hipEventRecord(b, kStream));
+    APK_CHECK(apk_clock_probe(dProbe, probes, window, side));
+    HIP_CHECK(hipDeviceSynchronize());
+    HIP_CHECK(hipGetLastError());
+    float fms = 0;
+    HIP_CHECK(hipEventElapsedTime(&fms, a, b));
+    const double ms = fms;
+    std::vector<long long> pr((size_t)probes * 4);
+    HIP_CHECK(hipMemcpy(pr.data(), dProbe, pr.size() * 8, hipMemcpyDeviceToHost));
+    std::vector<double> mhz;
+    for (int i = 0; i < probes; ++i)
+      if (pr[4 * i + 1] > 0) mhz.push_back((double)pr[4 * i] / pr[4 * i + 1] * dev.wall_mhz);
     const double flop = 2.0 * geo.tile_m * geo.tile_n * (double)K * tasks;
     const double peak = bf16 ? kPeakBf16TF : kPeakFp32TF;
     printf("calibrate K=%d: %u tasks on %d blocks in %.3f ms -> %.2f us/task/block | %.1f "
            "GFLOP/s (%.1f%% of %.1f TFLOP/s)\n", K, tasks, blocks, ms, ms * 1e3 * blocks / tasks,
            flop / (ms * 1e6), 100.0 * flop / (ms * 1e9) / peak, peak);
+    if (!mhz.empty())
+      printf("engine clock during the run (%zu probes): mean %.0f MHz | min %.0f | max %.0f\n",
+             mhz.size(), std::accumulate(mhz.begin(), mhz.end(), 0.0) / mhz.size(),
+             *std::min_element(mhz.begin(), mhz.end()), *std::max_element(mhz.begin(), mhz.end()));
     return 0;
   }
 

@@ -206,14 +206,17 @@ void YieldRig::resetRetreat() {
   for (int e = 0; e < E; ++e) gt[2 * (size_t)e] = INT64_MAX;
   HIP_CHECK(hipMemcpy(dRetreatGT_, gt.data(), gt.size() * 8, hipMemcpyHostToDevice));
   HIP_CHECK(hipMemset(dRqCtl_, 0, 2 * sizeof(unsigned)));
-  HIP_CHECK(hipMemset(dRqEntry_, 0, (size_t)s_.retreatCap * 4 * sizeof(int)));
+  // entry i = {task, stage, seq, kind << 8 | domain}; seq = i: free for ticket i
+  std::vector<int> en((size_t)s_.retreatCap * 4, 0);
+  for (unsigned i = 0; i < s_.retreatCap; ++i) en[(size_t)i * 4 + 2] = (int)i;
+  HIP_CHECK(hipMemcpy(dRqEntry_, en.data(), en.size() * sizeof(int), hipMemcpyHostToDevice));
   HIP_CHECK(hipMemset(dSet_, 0, E * sizeof(long long)));
 }
 
 void YieldRig::launchRetreat(int poll, int pollEvery, int resume, unsigned numTasks,
                              int retreat, int nEvents, bool oracle, int blocks, int blockBase,
                              bool continuation, long long* runGT, unsigned* exitCount,
-                             hipStream_t stream) {
+                             hipStream_t stream, int launchEpoch) {
   if (!s_.retreatCap || blockBase + blocks > s_.blocks + s_.extraRows) {
     fprintf(stderr, "launchRetreat: no resume queue, or stats rows %d..%d beyond %d\n",
             blockBase, blockBase + blocks, s_.blocks + s_.extraRows);
@@ -256,6 +259,7 @@ void YieldRig::launchRetreat(int poll, int pollEvery, int resume, unsigned numTa
   p.rq_slots = dRqSlots_;
   p.rq_capacity = s_.retreatCap;
   p.continuation = continuation ? 1 : 0;
+  p.launch_epoch = launchEpoch;
   p.block_base = blockBase;
   APK_CHECK(apk_persistent_yield(s_.engine, poll, oracle ? 1 : 0, &p, blocks, stream));
 }
@@ -274,10 +278,12 @@ RetreatResult YieldRig::readRetreat(int nEvents) const {
   HIP_CHECK(hipMemcpy(ctl, dRqCtl_, sizeof ctl, hipMemcpyDeviceToHost));
   r.head = ctl[0];
   r.tail = ctl[1];
+  // the domains of the last min(tail, capacity) retreats, oldest first
   const unsigned n4 = std::min(r.tail, s_.retreatCap);
-  std::vector<int> en((size_t)n4 * 4);
-  if (n4) HIP_CHECK(hipMemcpy(en.data(), dRqEntry_, en.size() * sizeof(int), hipMemcpyDeviceToHost));
-  for (unsigned t = 0; t < n4; ++t) r.xcd.push_back(en[(size_t)t * 4 + 3]);
+  std::vector<int> en((size_t)s_.retreatCap * 4);
+  HIP_CHECK(hipMemcpy(en.data(), dRqEntry_, en.size() * sizeof(int), hipMemcpyDeviceToHost));
+  for (unsigned t = r.tail - n4; t < r.tail; ++t)
+    r.xcd.push_back(en[(size_t)(t % s_.retreatCap) * 4 + 3] & 0xff);
   return r;
 }
 

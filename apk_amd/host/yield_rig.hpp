@@ -81,7 +81,8 @@ class YieldRig {
   // be NULL.
   void launchRetreat(int poll, int pollEvery, int resume, unsigned numTasks, int retreat,
                      int nEvents, bool oracle, int blocks, int blockBase, bool continuation,
-                     long long* runGT, unsigned* exitCount, hipStream_t stream);
+                     long long* runGT, unsigned* exitCount, hipStream_t stream,
+                     int launchEpoch = 0);
   // Zero the resume queue and the per-event retreat bookkeeping of a job.
   void resetRetreat();
   RetreatResult readRetreat(int nEvents) const;

@@ -8,19 +8,22 @@ the 1024 output tiles; inputs are resident in HBM before the timed region.
 
 Also reported (same line): the roofline of the GEMM kernel (fp32 MFMA dense
 peak 157.3 TFLOP/s; per-launch duration from HIP events on the launch stream),
-and the CPU baseline: the reference's float64 host GEMM (i-k-j,
-src/persistent.cu:221-227, restated in oracle/) timed on this host on a
-bounded sample of the same GEMM's rows.
+the engine clock the launches ran at (device-side probe), and the CPU
+baseline: the reference's float64 host GEMM (i-k-j, src/persistent.cu:221-227,
+restated in oracle/) timed on this host -- the whole GEMM with OpenMP on the
+host threads this process may use, and a 1024-row sample on one thread -- whose
+result also checks the whole GPU C.
 
 The same line carries `preemption`: the cfg3 experiment (background fp32
 SGEMM M=N=8192, K=4096, 128x128 tiles, k-chunk 128, on all 256 CUs; urgent
 fp32 GEMM 256x256x256 at exponential arrivals, mean 2 ms) run by the
-product binaries on a bounded sample of arrivals -- cooperative tile-boundary
-yield latency (flag set -> last block observes, the reference's latency),
-the retreat arm (flag raised -> urgent GEMM starts on its own stream), the
-no-preemption baseline, the tile-boundary polling overhead (ABAB drains) and
-the tile time at full residency they are measured against -- and `bf16`: the
-cfg5 bf16 MFMA GEMM throughput (M=N=K=8192, 256x256 tiles, no yields).
+product binaries, 10,000 arrivals for every latency -- cooperative yield
+latency at k-stage and tile-boundary polls (flag set -> last block observes,
+the reference's latency), the retreat arm (one background job; flag raised ->
+urgent GEMM starts on its own stream), the no-preemption baseline, the polling
+overhead (ABAB drains) and the tile time at full residency they are measured
+against -- and `bf16`: the cfg5 bf16 MFMA GEMM throughput (M=N=K=8192,
+256x256 tiles, no yields) with its engine clock.
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-preempt]
 """
@@ -44,27 +47,61 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def cpu_baseline(A_host, B_host, C_gpu_rows, rows):
-    """Reference float64 host GEMM on `rows` rows (single thread), timed; the
-    same rows double as a correctness check of the GPU output."""
-    import numpy as np
+def host_threads():
+    """Threads for the all-core host baseline: the CPU share this process may
+    use (OMP_NUM_THREADS when set, else the affinity mask)."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return len(os.sched_getaffinity(0))
+
+
+def cpu_baseline(A_host, B_host, C_gpu, rows_1t):
+    """The reference's float64 host GEMM (i-k-j, src/persistent.cu:221-227,
+    restated in oracle/) on this host: the whole GEMM on every host thread
+    (OpenMP over rows), and rows 0..rows_1t-1 on one thread as the reference
+    runs it. The all-core result checks the whole GPU C."""
     import oracle
-    t0 = time.perf_counter()
-    ref = oracle.gemm_f64_rows(A_host, B_host, 0, rows)
-    dt = time.perf_counter() - t0
-    K = A_host.shape[1]
+    M, K = A_host.shape
     N = B_host.shape[1]
-    flop = 2.0 * rows * N * K
-    frob = oracle.rel_frobenius(C_gpu_rows, ref)
+    threads = host_threads()
+    t0 = time.perf_counter()
+    ref = oracle.gemm_f64(A_host, B_host, threads=threads)
+    dt_all = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    ref1 = oracle.gemm_f64_rows(A_host, B_host, 0, rows_1t)
+    dt_1 = time.perf_counter() - t0
+    assert (ref1 == ref[:rows_1t]).all(), "float64 rows differ between thread counts"
+    frob = oracle.rel_frobenius(C_gpu, ref)
     return {
-        "value": flop / dt / 1e12,
+        "value": 2.0 * M * N * K / dt_all / 1e12,
         "unit": "TFLOP/s",
-        "cores": 1,
+        "cores": threads,
         "kind": "port",
-        "sample": (f"rows 0..{rows - 1} of the {A_host.shape[0]}x{N}x{K} GEMM in float64, "
-                   f"i-k-j order (src/persistent.cu:221-227), 1 thread, {dt:.1f} s"),
-        "seconds": dt,
+        "sample": (f"the whole {M}x{N}x{K} GEMM in float64, i-k-j order "
+                   f"(src/persistent.cu:221-227), OpenMP over rows on {threads} host threads, "
+                   f"{dt_all:.1f} s"),
+        "host_cores": os.cpu_count(),
+        "single_thread": {
+            "value": 2.0 * rows_1t * N * K / dt_1 / 1e12, "unit": "TFLOP/s", "cores": 1,
+            "sample": f"rows 0..{rows_1t - 1} of the same GEMM, 1 thread, {dt_1:.1f} s"},
+        "seconds": dt_all + dt_1,
     }, frob
+
+
+def clock_summary(raw, wall_mhz):
+    """Engine clock from apk_clock_probe records (cycles, ticks, xcd, start)."""
+    import numpy as np
+    r = raw.reshape(-1, 4)
+    ok = r[:, 1] > 0
+    mhz = r[ok, 0] / r[ok, 1] * wall_mhz
+    per_xcd = {}
+    for x, f in zip(r[ok, 2], mhz):
+        per_xcd.setdefault(int(x), []).append(float(f))
+    return {"mean": round(float(mhz.mean()), 1), "min": round(float(mhz.min()), 1),
+            "max": round(float(mhz.max()), 1),
+            "per_xcd": {str(k): round(float(np.mean(v)), 1) for k, v in sorted(per_xcd.items())},
+            "probes": int(ok.sum())}
 
 
 def measured_traffic(profile="profiles/persistent_gemm_mfma128_cfg2.md"):
@@ -129,34 +166,43 @@ def preemption_metrics(events, trials):
     # latency); urgent e2e. Flag polled at every k-stage, and at tile
     # boundaries only.
     for poll, key in (("stage", "coop"), ("chunk", "coop_tile_boundary")):
+        # 100 more arrivals than reported: the first 100 are warm-up (discarded)
         lat = run_bin("yield", ["--mode", "latency"] + CFG3 + CFG3_URGENT +
                       ["--poll", poll, "--arrival", "exp", "--mean-gap-us", 2000,
-                       "--events", events])
+                       "--events", events + 100], timeout=600)
         p50, p90, p99 = grab(lat, r"preemption latency set->last \(us\): p50 ([\d.]+) \| "
                                   r"p90 ([\d.]+) \| p99 ([\d.]+)")
         e50, e99 = grab(lat, r"urgent e2e set->done \(us\): p50 ([\d.]+) \| p99 ([\d.]+)")
-        out[key + "_latency_us"] = {"p50": p50, "p99": p99, "events": events,
+        n_ev, = grab(lat, r"blocks\): (\d+) events \(", int)
+        out[key + "_latency_us"] = {"p50": p50, "p99": p99, "events": n_ev,
                                     "p50_over_tile": round(p50 / tile_us, 3)}
         out[key + "_urgent_e2e_us"] = {"p50": e50, "p99": e99}
-    # Retreat arm: CUs handed to the urgent GEMM on its own stream.
+    # Retreat arm: CUs handed to the urgent GEMM on its own stream. One
+    # background job on all workers; the host raises each arrival as it falls
+    # due; accumulator-only checkpoints (the live stages are re-fetched).
     rt = run_bin("urgent_baseline", CFG3 + CFG3_URGENT +
                  ["--bg-tasks", 4096, "--urgent-blocks", 4, "--arrival", "exp",
-                  "--mean-gap-us", 2000, "--trials", trials, "--verify-rows", 64,
-                  "--yield", 1, "--retreat", 4, "--oracle", 1])
+                  "--mean-gap-us", 2000, "--yield", 1, "--retreat", 4, "--oracle", 1,
+                  "--continuous", 1, "--events", events, "--resume", "acc"], timeout=600)
     r50, r99 = grab(rt, r"flag raised -> urgent GEMM starts \(us\): p50 ([\d.]+) \| "
                         r"p90 [\d.]+ \| p99 ([\d.]+)")
-    re50, re99 = grab(rt, r"urgent e2e \(us\):\s+p50 ([\d.]+) \| p90 [\d.]+ \| p99 ([\d.]+)")
-    bad, = grab(rt, r"SAFETY: (\d+) of", int)
-    oracle_ok = "ORACLE: PASS" in rt
-    out["retreat_latency_us"] = {"p50": r50, "p99": r99, "trials": trials,
-                                 "p50_over_tile": round(r50 / tile_us, 3)}
-    out["retreat_urgent_e2e_us"] = {"p50": re50, "p99": re99}
+    n_in, = grab(rt, r"continuous retreat arm: (\d+) arrivals within the job", int)
+    re50, re99 = grab(rt, r"urgent GEMM done after the flag \(us\): p50 ([\d.]+) \| p99 ([\d.]+)")
+    bad, total = grab(rt, r"SAFETY: (\d+) of (\d+) task fingerprints", int)
+    tf_job, = grab(rt, r"background: ([\d.]+) TFLOP/s over the job")
+    out["retreat_latency_us"] = {"p50": r50, "p99": r99, "events": n_in,
+                                 "p50_over_tile": round(r50 / tile_us, 3),
+                                 "mode": "continuous job, accumulator-only checkpoints"}
+    out["retreat_urgent_done_us"] = {"p50": re50, "p99": re99}
+    out["retreat_background_tflops"] = tf_job
     out["corrupt_yields"] = bad
-    out["oracle"] = "PASS" if oracle_ok else "FAIL"
-    # No preemption: the urgent GEMM waits for the background to drain.
+    out["retreat_tasks_checked"] = total
+    out["oracle"] = "PASS" if ("ORACLE: PASS" in rt and "yield: PASS" in rt) else "FAIL"
+    # No preemption: the urgent GEMM waits for the background to drain (one
+    # background launch per arrival, src/urgent_baseline.cu:309-343).
     nb = run_bin("urgent_baseline", CFG3 + CFG3_URGENT +
                  ["--bg-tasks", 4096, "--urgent-blocks", 4, "--arrival", "exp",
-                  "--mean-gap-us", 2000, "--trials", trials])
+                  "--mean-gap-us", 2000, "--trials", trials], timeout=900)
     n50, n99 = grab(nb, r"urgent e2e \(us\):\s+p50 ([\d.]+) \| p90 [\d.]+ \| p99 ([\d.]+)")
     out["no_preempt_urgent_e2e_us"] = {"p50": n50, "p99": n99, "trials": trials}
     return out
@@ -167,10 +213,13 @@ def bf16_metrics():
     t = run_bin("tcyield", ["--mode", "calibrate", "--tiles-m", 32, "--tiles-n", 32,
                             "--gemm-k", 8192, "--k", 256, "--tasks", 2048])
     us, gf = grab(t, r"-> ([\d.]+) us/task/block \| ([\d.]+) GFLOP/s")
+    mhz, = grab(t, r"engine clock during the run \(\d+ probes\): mean ([\d.]+) MHz")
     tf = gf / 1e3
     return {"workload": "cfg5: bf16 GEMM M=N=K=8192 (2 passes of 1024 256x256 tiles), fp32 "
                         "accumulate, 256 workers, no yields",
             "tflops": round(tf, 2), "peak": 2516.6, "frac": round(tf / 2516.6, 4),
+            "engine_clock_mhz": mhz,
+            "frac_at_measured_clock": round(tf / (2516.6 * mhz / 2400.0), 4),
             "us_per_tile": us}
 
 
@@ -185,10 +234,10 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-preempt", action="store_true",
                     help="skip the preemption and bf16 sections")
-    ap.add_argument("--events", type=int, default=500,
-                    help="arrivals for the cooperative latency sample")
-    ap.add_argument("--trials", type=int, default=200,
-                    help="arrivals for the retreat-arm and no-preemption samples")
+    ap.add_argument("--events", type=int, default=10000,
+                    help="arrivals for the cooperative and retreat latencies")
+    ap.add_argument("--trials", type=int, default=10000,
+                    help="arrivals (one background launch each) for the no-preemption baseline")
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="only time torch.matmul (rocBLAS/hipBLASLt) on the same shapes: bf16 "
                          "8192^3 and fp32 4096^3, for comparison")
@@ -271,18 +320,33 @@ def main():
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
+    # Engine clock during the timed steps: one-wave probes on a side stream
+    # (default priority), beside the GEMM grid, over 80% of the expected
+    # timed region (from the warm-up launches).
+    # The window is shorter than the timed region, and the timed region waits
+    # for the GEMM stream alone, so the probe never lengthens it.
+    wall_mhz = info.wall_clock_khz / 1e3
+    warm_ms = float(np.min([starts[i].elapsed_time(ends[i]) for i in range(args.warmup)]))
+    window = max(1, int(0.6 * args.steps * warm_ms * 1e3 * wall_mhz))
+    probes = torch.zeros(32 * 4, dtype=torch.int64, device="cuda")
+    side = torch.cuda.Stream()
     t0 = time.perf_counter()
     for i in range(args.warmup, total):
         step(i)
-    torch.cuda.synchronize()
+        if i == args.warmup:
+            apk_amd.clock_probe(probes.data_ptr(), 32, window, side.cuda_stream)
+    stream.synchronize()
     wall = time.perf_counter() - t0
+    side.synchronize()
     ms_per_step = wall * 1e3 / args.steps
     launch_ms = [starts[i].elapsed_time(ends[i]) for i in range(args.warmup, total)]
     avg_launch_ms = float(np.mean(launch_ms))
     value = flop / (ms_per_step * 1e-3) / 1e12
     achieved = flop / (avg_launch_ms * 1e-3) / 1e12
+    clock = clock_summary(probes.cpu().numpy(), wall_mhz)
     log(f"GEMM {M}x{N}x{K} kc={kc}: {ms_per_step:.3f} ms/step wall, "
-        f"{avg_launch_ms:.3f} ms/launch (events) -> {value:.1f} TFLOP/s")
+        f"{avg_launch_ms:.3f} ms/launch (events) -> {value:.1f} TFLOP/s; engine clock "
+        f"{clock['mean']:.0f} MHz (min {clock['min']:.0f}, max {clock['max']:.0f})")
 
     out = {
         "metric": METRIC,
@@ -310,6 +374,9 @@ def main():
             "peak": PEAK_FP32_TF,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_FP32_TF, 4),
+            # the peak is quoted at 2.4 GHz; the clock the launches ran at:
+            "engine_clock_mhz": clock,
+            "frac_at_measured_clock": round(achieved / (PEAK_FP32_TF * clock["mean"] / 2400.0), 4),
             "traffic": measured_traffic() if (S, kc) == (4096, 32) else None,
         },
     }
@@ -319,16 +386,15 @@ def main():
         log("preemption: " + json.dumps(out["preemption"]))
         log("bf16: " + json.dumps(out["bf16"]))
     if not args.no_cpu:
-        rows = args.cpu_rows
-        A_host = dA[:rows].cpu().numpy()
+        A_host = dA.cpu().numpy()
         B_host = dB.cpu().numpy()
-        C_rows = dC[:rows].cpu().numpy()
-        cb, frob = cpu_baseline(A_host, B_host, C_rows, rows)
+        C_gpu = dC.cpu().numpy()
+        cb, frob = cpu_baseline(A_host, B_host, C_gpu, args.cpu_rows)
         out["cpu_baseline"] = {k: v for k, v in cb.items() if k != "seconds"}
-        out["check"] = {"rows": rows, "rel_frobenius_vs_f64": frob, "tol": 1e-5,
+        out["check"] = {"rows": M, "rel_frobenius_vs_f64": frob, "tol": 1e-5,
                         "pass": bool(frob <= 1e-5)}
-        log(f"cpu baseline {cb['value'] * 1e3:.3f} GFLOP/s ({cb['seconds']:.1f} s); "
-            f"GPU rows rel-Frobenius {frob:.2e}")
+        log(f"cpu baseline {cb['value'] * 1e3:.1f} GFLOP/s on {cb['cores']} threads "
+            f"({cb['single_thread']['value'] * 1e3:.2f} on 1); whole C rel-Frobenius {frob:.2e}")
     print(json.dumps(out), flush=True)
 
 

@@ -288,15 +288,29 @@ typedef struct apk_yield_params {
   long long* retreat_gt;         /* [2 * events] or NULL: [2e] earliest checkpoint
                                     start (host sets INT64_MAX), [2e+1] latest exit (0) */
   unsigned int* rq_ctl;          /* resume queue tickets: [0] head, [1] tail; 0 at job start */
-  int* rq_entry;                 /* [rq_capacity * 4]: task, stage, ready (kind + 1), the
-                                    retreating block's domain (xcd * 4 + shader engine);
-                                    0 at job start */
+  int* rq_entry;                 /* [rq_capacity * 4], a ring: ticket t uses entry t %
+                                    rq_capacity = {task, stage, seq, kind << 8 | domain
+                                    (xcd * 4 + shader engine of the retreating block)};
+                                    seq = t: free, t + 1: published, set to t + capacity
+                                    once read back. At job start entry i holds seq = i. */
   float* rq_slots;               /* rq_capacity * apk_yield_ckpt_floats(engine) floats */
-  unsigned int rq_capacity;      /* tickets in this job; a retreat beyond it is declined */
+  unsigned int rq_capacity;      /* entries in the ring; a retreat that finds its entry
+                                    still in use (ring full) is declined */
   int continuation;              /* 1: a relaunch joining a running job -- generations
                                     already raised when it starts are not acted on */
   int block_base;                /* this launch's first row in obs_gt columns and stats */
   int obs_stride;                /* obs_gt row length (0 = gridDim); obs_gt may be NULL */
+  /* Retreat arm, which blocks hand over their CU at generation g: a launch
+   * with continuation = 0 (the job's first grid) by the per-domain quota at
+   * g = 1 only; a continuation with launch_epoch > 0 all of its blocks at the
+   * first generation after launch_epoch (its blocks sit on the CUs the
+   * previous generation freed, one per dispatch domain; it must complete for
+   * the next continuation, queued behind it on one stream, to start); a
+   * continuation with launch_epoch = 0 never. Set it to the generation a
+   * continuation follows (the flag value when it is queued): the
+   * continuation treats generations up to it as seen, even if a later one was
+   * raised before it got its CUs. */
+  int launch_epoch;
 } apk_yield_params;
 
 /* persistent_yield / persistent_midyield (src/yield.cu:95-204,
@@ -328,6 +342,16 @@ int apk_raise_flag(int* flag, int flag_copies, int value, long long* set_gt, voi
  * hang the GPU. out: 2 device (or host-mapped) long longs. */
 int apk_spin_flag(const int* flag, int system_scope, long long max_ticks, long long* out,
                   void* stream);
+
+/* Engine clock under load (the read-back of scripts/lock_clocks.sh:15-25,
+ * taken on the device): `blocks` one-wave blocks, dealt round-robin to the
+ * XCDs, each count shader-clock cycles (s_memtime) and wall-clock ticks
+ * (s_memrealtime) over a window of window_ticks wall ticks, sleeping between
+ * reads. out[4 b .. 4 b + 3] = cycles, ticks, XCD, start tick; the mean clock
+ * of block b's CU is cycles / ticks x the wall-clock rate. Queue it on a
+ * second stream while the kernel to be measured runs: it needs no LDS and one
+ * wave, so it is dispatched beside a fully resident grid. */
+int apk_clock_probe(long long* out, int blocks, long long window_ticks, void* stream);
 
 /* Resident blocks per CU of the preemptible kernel. */
 int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_per_cu);

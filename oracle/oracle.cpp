@@ -95,34 +95,22 @@ void apko_fill_uniform_pm1(uint32_t seed, float* A, int64_t nA, float* B,
 // ---------------------------------------------------------------------------
 // float64 host reference GEMM, i-k-j loop order with a double accumulator per
 // output (src/persistent.cu:221-227). A is MxK row-major, B is KxN row-major,
-// C is MxN row-major. `threads` > 1 splits rows across std::threads; each
-// output's summation order (k ascending) is unchanged, so the result does not
-// depend on the thread count.
+// C is MxN row-major. `threads` > 1 splits rows over an OpenMP team of that
+// many threads (the all-core host baseline); each output's summation order
+// (k ascending) is unchanged, so the result does not depend on the thread
+// count.
 void apko_gemm_f64(const float* A, const float* B, double* C, int M, int N,
                    int K, int threads) {
-  auto rows = [&](int r0, int r1) {
-    for (int i = r0; i < r1; ++i) {
-      double* crow = C + (size_t)i * N;
-      for (int j = 0; j < N; ++j) crow[j] = 0.0;
-      for (int k = 0; k < K; ++k) {
-        const double a = A[(size_t)i * K + k];
-        const float* brow = B + (size_t)k * N;
-        for (int j = 0; j < N; ++j) crow[j] += a * brow[j];
-      }
+#pragma omp parallel for num_threads(threads > 1 ? threads : 1) schedule(static)
+  for (int i = 0; i < M; ++i) {
+    double* crow = C + (size_t)i * N;
+    for (int j = 0; j < N; ++j) crow[j] = 0.0;
+    for (int k = 0; k < K; ++k) {
+      const double a = A[(size_t)i * K + k];
+      const float* brow = B + (size_t)k * N;
+      for (int j = 0; j < N; ++j) crow[j] += a * brow[j];
     }
-  };
-  if (threads <= 1) {
-    rows(0, M);
-    return;
   }
-  std::vector<std::thread> pool;
-  const int per = (M + threads - 1) / threads;
-  for (int t = 0; t < threads; ++t) {
-    const int r0 = t * per, r1 = std::min(M, r0 + per);
-    if (r0 >= r1) break;
-    pool.emplace_back(rows, r0, r1);
-  }
-  for (auto& th : pool) th.join();
 }
 
 // Same product on bf16-quantized inputs given as float (src/tcyield.cu:

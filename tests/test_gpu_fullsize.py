@@ -116,3 +116,20 @@ def test_cfg3_no_preemption_baseline_8192():
                   "--verify-rows", 64)
     assert "PASS:" in out
     assert "urgent e2e (us)" in out
+
+
+@pytest.mark.parametrize("resume", ["ckpt", "acc"])
+def test_cfg3_retreat_arm_continuous(resume):
+    """cfg3 retreat arm as one background job (M=N=8192, K=4096 on all 256
+    CUs) with 400 exponential arrivals raised by the host: every task's
+    fingerprint matches its unpreempted tile, every task runs exactly once,
+    the kept urgent outputs are bit-identical, no resume entry is lost."""
+    out = run_bin("urgent_baseline", *CFG3, "--bg-tasks", 4096, "--urgent-blocks", 4,
+                  "--arrival", "exp", "--mean-gap-us", 2000, "--yield", 1, "--retreat", 4,
+                  "--oracle", 1, "--continuous", 1, "--events", 400, "--resume", resume)
+    bad, = grab(out, r"SAFETY: (\d+) of \d+ task fingerprints")
+    assert bad == 0
+    n_in, = grab(out, r"continuous retreat arm: (\d+) arrivals within the job")
+    assert n_in == 400
+    assert "arrivals without a retreat 0" in out
+    assert "ORACLE: PASS" in out and "yield: PASS" in out

@@ -121,6 +121,9 @@ class RetreatJob:
                   self.rq_entry, self.stats, self.task_hash, self.exec_count, self.run_gt,
                   self.exit_count):
             x.zero_()
+        # resume ring: entry i starts free for ticket i (seq = i)
+        self.rq_entry.view(self.RB, 4)[:, 2] = self.t.arange(self.RB, dtype=self.t.int32,
+                                                             device="cuda")
         self.rgt[0] = np.iinfo(np.int64).max
         self.rgt[1] = 0
         self.dC.fill_(float("nan"))
