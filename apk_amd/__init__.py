@@ -17,8 +17,9 @@ BIN_DIR = os.path.join(_HERE, "bin")
 HEADER = os.path.join(ROOT, "include", "apk.h")
 
 APK_OK, APK_EINVAL, APK_EHIP, APK_ERANGE = 0, 1, 2, 3
-ENGINE_VALU64, ENGINE_MFMA128, ENGINE_BF16X256 = 0, 1, 2
-ENGINES = {"valu64": ENGINE_VALU64, "mfma128": ENGINE_MFMA128, "bf16x256": ENGINE_BF16X256}
+ENGINE_VALU64, ENGINE_MFMA128, ENGINE_BF16X256, ENGINE_BF16X128 = 0, 1, 2, 3
+ENGINES = {"valu64": ENGINE_VALU64, "mfma128": ENGINE_MFMA128, "bf16x256": ENGINE_BF16X256,
+           "bf16x128": ENGINE_BF16X128}
 
 
 class ApkError(RuntimeError):

@@ -2,6 +2,7 @@
 #include <stdarg.h>
 #include <string.h>
 #include "capi.hpp"
+#include "engine_bf16x128.hpp"
 #include "engine_bf16x256.hpp"
 #include "engine_mfma128.hpp"
 #include "engine_valu64.hpp"
@@ -51,6 +52,10 @@ extern "C" int apk_engine_geometry_of(int engine, apk_engine_geometry* out) {
     case APK_ENGINE_BF16X256:
       *out = {apk::EngBf16x256::TM, apk::EngBf16x256::TN, apk::EngBf16x256::KS,
               apk::EngBf16x256::THREADS, apk::EngBf16x256::LDS_BYTES, 2, 1};
+      return APK_OK;
+    case APK_ENGINE_BF16X128:
+      *out = {apk::EngBf16x128::TM, apk::EngBf16x128::TN, apk::EngBf16x128::KS,
+              apk::EngBf16x128::THREADS, apk::EngBf16x128::LDS_BYTES, 2, 1};
       return APK_OK;
     default:
       apk::set_error("unknown engine %d", engine);

@@ -1,0 +1,224 @@
+// engine_bf16x128.hpp -- 128x128 output tile of a bf16 GEMM with fp32
+// accumulation on the gfx950 matrix cores (v_mfma_f32_32x32x16_bf16), sized
+// so that 2 and 4 blocks share a CU: the occupancy points at which the
+// 256x256 tile cannot run (its fp32 accumulator is half of a CU's register
+// file and its ring 128 KiB of the 160 KiB LDS).
+//
+// Operands as for the 256x256 engine: A is M x K row-major bf16, B is passed
+// transposed (Bt = N x K row-major bf16, C = A . Bt^T), both k-contiguous in
+// memory, LDS and operand registers. C is M x N row-major fp32.
+//
+// Block: 256 threads = 4 wave64s in a 2x2 arrangement; each wave owns a
+// 64x64 sub-tile held as 2x2 32x32 accumulators (64 fp32 per lane). At 4
+// blocks per CU a SIMD holds 4 waves, so a wave has 128 registers per lane:
+// 64 accumulators, two operand fragments of 16 and the addresses.
+// Stage: k depth KS=16 (one MFMA k-step) -> A stage 128 rows x 32 B (4 KiB)
+// + Bt stage 128 rows x 32 B (4 KiB); 4 slots = 32 KiB, synchronised once
+// per pair of stages (GROUP = 2) as in the 256x256 engine. The LDS block is
+// 33 KiB (the epilogue's staging of 64 padded rows), so 4 blocks take 132
+// KiB of the CU's 160 KiB.
+//
+// LDS layout (both operands): row r of a stage is 32 B = two 16-byte chunks;
+// chunk q is stored at slot q ^ swz(r), swz(r) = (r >> 3) & 1. A ds_read_b128
+// is served 16 lanes per cycle (256 B); 16 consecutive rows reading chunk q
+// then fall on 16 different 16-byte bank groups, where the unswizzled layout
+// puts rows r and r+8 on the same group.
+//
+// k order: one MFMA k-step of 16 per stage, in ascending k; every output's
+// sum is formed in the same order whatever worker computes it and however
+// often it is checkpointed and resumed.
+//
+// Epilogue: the fp32 tile (64 KiB) is staged in 2 passes of 64 rows (32 rows
+// of each wave row), row stride TN + 4 floats.
+#pragma once
+#include "device.hpp"
+
+namespace apk {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+
+struct EngBf16x128 {
+  static constexpr int TM = 128, TN = 128, KS = 16, NS = 4, GROUP = 2, THREADS = 256;
+  // 4 blocks of 4 waves per CU: every instantiation must fit 128 registers
+  // per lane (accumulators included), so the compiler is held to 4 waves.
+  static constexpr int WAVES_PER_SIMD = 4;
+  static constexpr int MIN_WAVES_PER_SIMD = 4;
+  static constexpr int ROW_BYTES = KS * 2;                  // 32 B
+  static constexpr int A_STAGE = TM * ROW_BYTES;            // 4 KiB
+  static constexpr int B_STAGE = TN * ROW_BYTES;            // 4 KiB
+  static constexpr int STAGE = A_STAGE + B_STAGE;           // 8 KiB
+  static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 1 per thread
+  static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 1 per thread
+  static constexpr int LOADS = LOADS_A + LOADS_B;
+  static constexpr int WAVES = THREADS / 64;
+  static constexpr int ACC_PER_THREAD = 64;                 // floats
+  static constexpr int ELEM_BYTES = 2;                      // bf16 operands
+  static constexpr int STORE_PASSES = 2, PASS_ROWS = 64, STAGE_LD = TN + 4;
+  static constexpr int RING_BYTES = NS * STAGE;             // 32 KiB
+  static constexpr int EPI_BYTES = PASS_ROWS * STAGE_LD * 4;
+  static constexpr int LDS_BYTES = RING_BYTES > EPI_BYTES ? RING_BYTES : EPI_BYTES;
+
+  struct Acc {
+    f32x16 c[2][2];
+  };
+
+  struct Ctx {
+    i32x4 ra, rb;
+    int K;
+  };
+
+  static __device__ __forceinline__ Ctx make_ctx(const void* A, const void* Bt, int M, int N,
+                                                 int K) {
+    Ctx c;
+    c.ra = make_rsrc(A, (uint32_t)((size_t)M * K * 2));
+    c.rb = make_rsrc(Bt, (uint32_t)((size_t)N * K * 2));
+    c.K = K;
+    return c;
+  }
+
+  static __device__ __forceinline__ void zero(Acc& a) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a.c[i][j][r] = 0.0f;
+  }
+
+  static __device__ __forceinline__ int swz(int r) { return (r >> 3) & 1; }
+
+  // Direct-to-LDS loads of one k-stage: load 0 fills rows 32*wave + lane/2
+  // of the A stage (this wave's 1 KiB piece), load 1 the same rows of the Bt
+  // stage; lane l writes slot l & 1 of its row, so it reads the row's chunk
+  // (l & 1) ^ swz(row) from memory. Fixed per tile (one register per load);
+  // stage t only adds the scalar k offset.
+  struct Lane {
+    uint32_t a[LOADS_A], b[LOADS_B];
+  };
+  static __device__ __forceinline__ Lane lane_offsets(const Ctx& c, int row0, int col0) {
+    const int w = wave_id(), l = lane_id();
+    const int r = w * 32 + (l >> 1);
+    const int q = (l & 1) ^ swz(r);
+    Lane ln;
+    ln.a[0] = (uint32_t)(((row0 + r) * c.K + 8 * q) * 2);
+    ln.b[0] = (uint32_t)(((col0 + r) * c.K + 8 * q) * 2);
+    return ln;
+  }
+  // Scalar parts of stage t's loads into ring slot `slot` (as in the 256x256
+  // engine): t >= S reads through zero-length resources, i.e. zeros.
+  struct Dst {
+    uint32_t lds, k;
+    i32x4 ra, rb;
+  };
+  static __device__ __forceinline__ Dst stage_dst(uint32_t wave_lds, const Ctx& c, int slot,
+                                                  int t, int S) {
+    const bool real = t < S;
+    i32x4 za = c.ra, zb = c.rb;
+    za.z = 0;
+    zb.z = 0;
+    return Dst{wave_lds + (uint32_t)(slot * STAGE), (uint32_t)((real ? t : 0) * KS * 2),
+               real ? c.ra : za, real ? c.rb : zb};
+  }
+  // Byte offset inside a ring slot of load i's piece (thread t's 16 bytes of
+  // load i land at slot + dma_lds_off(i) + 16 t).
+  static constexpr uint32_t dma_lds_off(int i) { return i == 0 ? 0u : (uint32_t)A_STAGE; }
+  static __device__ __forceinline__ void issue_one(const Ctx&, const Lane& ln, const Dst& d,
+                                                   int i) {
+    if (i == 0)
+      dma_x4(d.ra, d.lds, dma_lds_off(0), ln.a[0], d.k);
+    else
+      dma_x4(d.rb, d.lds, dma_lds_off(1), ln.b[0], d.k);
+  }
+
+  // Operands of one stage (16 k values): one 16-byte read per 32-row block of
+  // A and per 32-column block of Bt; lanes 0-31 take k 0-7 of their row,
+  // lanes 32-63 k 8-15.
+  struct Frag {
+    bf16x8 a[2], b[2];
+  };
+  static __device__ __forceinline__ void load_frag(const char* sbase, Frag& f) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w & 1, wn = w >> 1;
+    const int lr = l & 31, q = l >> 5;
+    const char* bbase = sbase + A_STAGE;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int row = wm * 64 + rb * 32 + lr;
+      f.a[rb] = *(const bf16x8*)(sbase + row * ROW_BYTES + ((q ^ swz(row)) << 4));
+    }
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+      const int col = wn * 64 + cb * 32 + lr;
+      f.b[cb] = *(const bf16x8*)(bbase + col * ROW_BYTES + ((q ^ swz(col)) << 4));
+    }
+  }
+
+  // One group: the two k-stages in ring slots slot and slot+1, 8 MFMAs per
+  // wave in ascending k, the second stage's operands read while the first
+  // stage's MFMAs run. `pre` runs first (false abandons the group before any
+  // accumulator changes); `mid(i)`, i = 0..GROUP*LOADS-1, runs after MFMA
+  // 2i+1: the stage loops issue the next group's load i there.
+  template <class Pre, class Mid>
+  static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
+                                                 Pre&& pre, Mid&& mid) {
+    const char* gbase = ring + slot * STAGE;
+    Frag f[2];
+    if (!pre()) return false;
+    load_frag(gbase, f[0]);
+#pragma unroll
+    for (int j = 0; j < GROUP; ++j) {
+      if (j + 1 < GROUP) load_frag(gbase + (j + 1) * STAGE, f[(j + 1) & 1]);
+      const Frag& c = f[j & 1];
+#pragma unroll
+      for (int m = 0; m < 4; ++m) {
+        const int rb = m >> 1, cb = m & 1;
+        acc.c[rb][cb] =
+            __builtin_amdgcn_mfma_f32_32x32x16_bf16(c.a[rb], c.b[cb], acc.c[rb][cb], 0, 0, 0);
+        if (m & 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          mid(j * 2 + (m >> 1));
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+    }
+    return true;
+  }
+  static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {
+    compute(ring, slot, acc, [] { return true; }, [](int) {});
+  }
+
+  // Output element (tile-relative row, col) of accumulator register e.
+  static __device__ __forceinline__ void coord(int e, int& r, int& c) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w & 1, wn = w >> 1, rb = e >> 5, cb = (e >> 4) & 1, i = e & 15;
+    r = wm * 64 + rb * 32 + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+    c = wn * 64 + cb * 32 + (l & 31);
+  }
+  static __device__ __forceinline__ float get(const Acc& a, int e) {
+    return a.c[e >> 5][(e >> 4) & 1][e & 15];
+  }
+  static __device__ __forceinline__ void set(Acc& a, int e, float v) {
+    a.c[e >> 5][(e >> 4) & 1][e & 15] = v;
+  }
+
+  // Epilogue pass p: accumulator row block rb = p of every wave into LDS as
+  // rows [wm*32, wm*32+32) of a 64 x TN tile; LDS row rr holds tile row
+  // pass_row(p, rr).
+  static __device__ __forceinline__ void stage_pass(const Acc& acc, char* lds, int p) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w & 1, wn = w >> 1;
+    float* t = (float*)lds;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int rr = wm * 32 + 8 * (i >> 2) + 4 * (l >> 5) + (i & 3);
+        t[rr * STAGE_LD + wn * 64 + cb * 32 + (l & 31)] = acc.c[p][cb][i];
+      }
+  }
+  static __device__ __forceinline__ int pass_row(int p, int rr) {
+    return (rr >> 5) * 64 + p * 32 + (rr & 31);
+  }
+};
+
+}  // namespace apk

@@ -52,6 +52,7 @@ struct EngBf16x256 {
   // Waves per SIMD at most (1 block of 8 waves per CU): the register budget the
   // compiler may schedule for.
   static constexpr int WAVES_PER_SIMD = 2;
+  static constexpr int MIN_WAVES_PER_SIMD = 1;  // occupancy the registers must allow
   static constexpr int ROW_BYTES = KS * 2;                  // 64 B
   static constexpr int A_STAGE = TM * ROW_BYTES;            // 16 KiB
   static constexpr int B_STAGE = TN * ROW_BYTES;            // 16 KiB

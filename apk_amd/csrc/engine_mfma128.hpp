@@ -35,6 +35,7 @@ struct EngMfma128 {
   // Waves per SIMD at most (1 block per CU (LDS-bound)): the register budget the
   // compiler may schedule for.
   static constexpr int WAVES_PER_SIMD = 1;
+  static constexpr int MIN_WAVES_PER_SIMD = 1;  // occupancy the registers must allow
   static constexpr int A_STAGE = TM * KS * 4;               // bytes
   static constexpr int B_STAGE = KS * TN * 4;               // bytes
   static constexpr int STAGE = A_STAGE + B_STAGE;           // 32 KiB

@@ -25,6 +25,7 @@ struct EngValu64 {
   // Waves per SIMD at most (3 blocks per CU (LDS-bound)): the register budget the
   // compiler may schedule for.
   static constexpr int WAVES_PER_SIMD = 3;
+  static constexpr int MIN_WAVES_PER_SIMD = 1;  // occupancy the registers must allow
   static constexpr int A_STAGE = TM * KS * 4;               // 8 KiB
   static constexpr int B_STAGE = KS * TN * 4;               // 8 KiB
   static constexpr int STAGE = A_STAGE + B_STAGE;           // 16 KiB

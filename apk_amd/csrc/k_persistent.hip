@@ -11,6 +11,7 @@
 #include <mutex>
 
 #include "capi.hpp"
+#include "engine_bf16x128.hpp"
 #include "engine_bf16x256.hpp"
 #include "engine_mfma128.hpp"
 #include "engine_valu64.hpp"
@@ -19,7 +20,7 @@
 namespace apk {
 
 template <class E>
-__global__ void __launch_bounds__(E::THREADS) __attribute__((amdgpu_waves_per_eu(1, E::WAVES_PER_SIMD)))
+__global__ void __launch_bounds__(E::THREADS) __attribute__((amdgpu_waves_per_eu(E::MIN_WAVES_PER_SIMD, E::WAVES_PER_SIMD)))
     k_persistent_gemm(const void* __restrict__ A, const void* __restrict__ B,
                       float* __restrict__ C, int M, int N, int K, int kChunk,
                       unsigned* next_task, apk_tile_record* log) {
@@ -179,6 +180,10 @@ extern "C" int apk_persistent_gemm(int engine, const void* A, const void* B,
       return launch_persistent_gemm<EngBf16x256>(A, B, C, M, N, K, k_chunk,
                                                  next_task, log, blocks,
                                                  as_stream(stream));
+    case APK_ENGINE_BF16X128:
+      return launch_persistent_gemm<EngBf16x128>(A, B, C, M, N, K, k_chunk,
+                                                 next_task, log, blocks,
+                                                 as_stream(stream));
     default:
       set_error("persistent_gemm: unknown engine %d", engine);
       return APK_EINVAL;
@@ -191,6 +196,7 @@ extern "C" int apk_persistent_gemm_occupancy(int engine, int* blocks_per_cu) {
     case APK_ENGINE_VALU64: return occupancy_of<EngValu64>(blocks_per_cu);
     case APK_ENGINE_MFMA128: return occupancy_of<EngMfma128>(blocks_per_cu);
     case APK_ENGINE_BF16X256: return occupancy_of<EngBf16x256>(blocks_per_cu);
+    case APK_ENGINE_BF16X128: return occupancy_of<EngBf16x128>(blocks_per_cu);
     default:
       set_error("occupancy: unknown engine %d", engine);
       return APK_EINVAL;
@@ -211,6 +217,9 @@ extern "C" int apk_persistent_gemm_noalloc(int engine, const void* A, const void
       break;
     case APK_ENGINE_BF16X256:
       rc = validate_persistent_gemm<EngBf16x256>(A, B, C, M, N, K, k_chunk, blocks);
+      break;
+    case APK_ENGINE_BF16X128:
+      rc = validate_persistent_gemm<EngBf16x128>(A, B, C, M, N, K, k_chunk, blocks);
       break;
     default:
       set_error("persistent_gemm_noalloc: unknown engine %d", engine);

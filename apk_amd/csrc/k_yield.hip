@@ -25,6 +25,7 @@
 // from LDS after a barrier (the snapshot discipline of src/midyield.cu:
 // 177-200), so a block never splits across barriers.
 #include "capi.hpp"
+#include "engine_bf16x128.hpp"
 #include "engine_bf16x256.hpp"
 #include "engine_mfma128.hpp"
 #include "engine_valu64.hpp"
@@ -36,7 +37,7 @@ namespace apk {
 // cooperative instantiations carry none of its code and the retreat ones
 // none of the in-kernel urgent path.
 template <class E, int POLL, bool ORACLE, bool SYS, bool RETREAT>
-__global__ void __launch_bounds__(E::THREADS) __attribute__((amdgpu_waves_per_eu(1, E::WAVES_PER_SIMD)))
+__global__ void __launch_bounds__(E::THREADS) __attribute__((amdgpu_waves_per_eu(E::MIN_WAVES_PER_SIMD, E::WAVES_PER_SIMD)))
 k_persistent_yield(const apk_yield_params) {
   // Every parameter is re-read from the kernel-argument segment where it is
   // used (P() is opaque to the optimiser), instead of being loaded once at
@@ -102,9 +103,8 @@ k_persistent_yield(const apk_yield_params) {
     __syncthreads();
     // A retreat-arm continuation starts from the generation it follows
     // (launch_epoch), so that one raised before it got its CUs still counts.
-    const int seen = P().launch_epoch > 0 ? P().launch_epoch : f0;
     if (f0 < 0) fLatest = f0;
-    else lastSeen = seen < P().num_events ? seen : P().num_events;
+    else lastSeen = proto::first_seen(f0, P().launch_epoch, P().num_events);
   }
   enum { ST_YIELDS = APK_ST_YIELDS, ST_SAVE = APK_ST_SAVE, ST_URGENT = APK_ST_URGENT,
          ST_RESTORE = APK_ST_RESTORE, ST_INFLIGHT = APK_ST_INFLIGHT,
@@ -539,9 +539,9 @@ k_persistent_yield(const apk_yield_params) {
         // (queued behind it) to start.
         const int quota = (P().retreat + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS;
         const int dom = (int)xcc_id() * APK_SES_PER_XCD + (int)se_id();
-        const bool cont = P().continuation != 0;
-        const bool newest = cont && P().launch_epoch > 0 && f > P().launch_epoch;
-        if (!newest && (cont || f != 1)) continue;  // not this block's turn: keep working
+        const int role = proto::retreat_role(P().continuation != 0, P().launch_epoch, f);
+        if (role == proto::RETREAT_NONE) continue;  // not this block's turn: keep working
+        const bool newest = role == proto::RETREAT_ALL;
         unsigned t = RQ_NONE;
         if (tid == 0) {
           int* rc = &P().retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + dom];
@@ -787,6 +787,8 @@ extern "C" int apk_persistent_yield(int engine, int poll, int oracle,
       return launch_e<EngMfma128>(poll, oracle, params, blocks, as_stream(stream));
     case APK_ENGINE_BF16X256:
       return launch_e<EngBf16x256>(poll, oracle, params, blocks, as_stream(stream));
+    case APK_ENGINE_BF16X128:
+      return launch_e<EngBf16x128>(poll, oracle, params, blocks, as_stream(stream));
     default:
       set_error("persistent_yield: unknown engine %d", engine);
       return APK_EINVAL;
@@ -799,6 +801,7 @@ extern "C" long long apk_yield_ckpt_floats(int engine) {
     case APK_ENGINE_VALU64: return Ckpt<EngValu64>::SLOT_FLOATS;
     case APK_ENGINE_MFMA128: return Ckpt<EngMfma128>::SLOT_FLOATS;
     case APK_ENGINE_BF16X256: return Ckpt<EngBf16x256>::SLOT_FLOATS;
+    case APK_ENGINE_BF16X128: return Ckpt<EngBf16x128>::SLOT_FLOATS;
     default: return -1;
   }
 }
@@ -839,6 +842,7 @@ extern "C" int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_
     case APK_ENGINE_VALU64: return yield_occupancy_of<EngValu64>(poll, blocks_per_cu);
     case APK_ENGINE_MFMA128: return yield_occupancy_of<EngMfma128>(poll, blocks_per_cu);
     case APK_ENGINE_BF16X256: return yield_occupancy_of<EngBf16x256>(poll, blocks_per_cu);
+    case APK_ENGINE_BF16X128: return yield_occupancy_of<EngBf16x128>(poll, blocks_per_cu);
     default:
       set_error("occupancy: engine %d", engine);
       return APK_EINVAL;

@@ -5,135 +5,58 @@
 #pragma once
 #include "device.hpp"
 
+#define APK_PROTO_FN __device__ __forceinline__
+#include "protocol.hpp"
+
 namespace apk {
 
 // ---------------------------------------------------------------------------
-// XCD-aware work queue. The tile grid (tilesM x tilesN) is walked in a
-// grouped order G: bands of GM tile rows, column by column inside a band, so
-// that consecutive positions form GM x n blocks of the grid. Positions
-// [q*T/8, (q+1)*T/8) of G are XCD q's list; pass p of the task space maps
-// position i of list q to task p*T + G(i). A worker pops its own XCD's list
-// (counter ctr[q]) and, once that is exhausted, the other lists in turn, so
-// every task id below num_tasks is handed out exactly once and task u always
-// computes tile u % T.
-struct TaskQueue {
-  static constexpr int GM = 4;
-  unsigned* ctr;
-  int tilesM, tilesN, T;
-  unsigned numTasks, passes;
-
-  __device__ __forceinline__ TaskQueue(unsigned* c, int tm, int tn, unsigned n)
-      : ctr(c), tilesM(tm), tilesN(tn), T(tm * tn), numTasks(n),
-        passes((n + (unsigned)(tm * tn) - 1) / (unsigned)(tm * tn)) {}
-
-  __device__ __forceinline__ int grouped(int i) const {
-    const int band = i / (GM * tilesN);
-    const int rows = min(GM, tilesM - band * GM);
-    const int r = i - band * GM * tilesN;
-    return (band * GM + r % rows) * tilesN + r / rows;
+// The scheduler protocol (work queue, resume ring, generations) lives in
+// protocol.hpp, shared with the CPU protocol simulator; here it runs on the
+// device's agent-scope atomics, fences, wall clock and s_sleep.
+struct DevPlat {
+  static __device__ __forceinline__ unsigned fetch_add(unsigned* p, unsigned v) {
+    return fetch_add_u32(p, v);
   }
-  __device__ __forceinline__ int list_begin(int q) const {
-    return (int)(((long long)q * T) / APK_QUEUE_XCDS);
+  static __device__ __forceinline__ unsigned cas(unsigned* p, unsigned e, unsigned d) {
+    return cas_u32(p, e, d);
   }
-  // Thread-0 only. Returns the next task id, or 0xffffffff when every list
-  // is exhausted.
-  __device__ __forceinline__ unsigned pop(int home) const {
-    for (int k = 0; k < APK_QUEUE_XCDS; ++k) {
-      const int q = (home + k) & (APK_QUEUE_XCDS - 1);
-      const int b = list_begin(q), n = list_begin(q + 1) - b;
-      if (n == 0) continue;
-      const unsigned total = (unsigned)n * passes;
-      for (;;) {
-        const unsigned j = fetch_add_u32(&ctr[q], 1u);
-        if (j >= total) break;
-        const unsigned u = (j / (unsigned)n) * (unsigned)T + (unsigned)grouped(b + (int)(j % (unsigned)n));
-        if (u < numTasks) return u;
-      }
-    }
-    return 0xffffffffu;
+  static __device__ __forceinline__ unsigned load(const unsigned* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
+  static __device__ __forceinline__ int load(const int* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  static __device__ __forceinline__ void store(int* p, int v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  static __device__ __forceinline__ void release() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  }
+  static __device__ __forceinline__ void acquire() {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+  }
+  static __device__ __forceinline__ int64_t ticks() { return wall_ticks(); }
+  static __device__ __forceinline__ void pause() { __builtin_amdgcn_s_sleep(8); }
 };
 
-// ---------------------------------------------------------------------------
-// Resume queue of the retreat arm: a bounded ring of `cap` entries, tickets
-// [head, tail) in rq_ctl[0..1]. Entry i = {task, stage, seq, kind << 8 |
-// domain} with its checkpoint slot i; ticket t uses entry t % cap. `seq`
-// orders the entry's rounds (bounded MPMC ring with per-slot sequence
-// numbers): seq == t means free for ticket t, t + 1 published by ticket t's
-// producer, and the consumer of ticket t sets it to t + cap once it has read
-// the checkpoint back. A producer reserves a ticket only when its entry is
-// free (otherwise the ring is full and it declines the retreat), so it never
-// waits; a consumer claims the oldest reserved ticket and waits for its
-// producer (a resident block on its exit path) with a bounded spin. The host
-// sets seq = i for every entry before a job.
-constexpr unsigned RQ_NONE = 0xffffffffu;
-// Longest wait for a claimed entry to be published: 20 ms at the 100 MHz
-// wall clock. A producer publishes within microseconds; running out means a
-// lost task, which the exactly-once counts then report.
-constexpr int64_t RQ_WAIT_TICKS = 2000000;
-
-__device__ __forceinline__ int rq_seq_load(const int* en) {
-  return __hip_atomic_load(&en[2], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+using TaskQueue = proto::TaskQueue<DevPlat>;
+using proto::RQ_FULL;
+using proto::RQ_NONE;
+// Thread-0 only, each of them.
+__device__ __forceinline__ unsigned rq_reserve(unsigned* ctl, unsigned cap, const int* en) {
+  return proto::rq_reserve<DevPlat>(ctl, cap, en);
 }
-// Thread-0 only. Takes the next ticket with one fetch-add (no CAS loop: the
-// producers of one generation arrive together, and a CAS loop would
-// serialise them round trip by round trip) and waits, bounded, for its entry
-// to be free. The ring holds several generations' retreats, so the entry is
-// free at once unless consumers have stalled; a ticket whose entry stays
-// taken for RQ_WAIT_TICKS is returned with RQ_FULL set: the caller does not
-// retreat and counts an error (that ticket's consumer then reports it lost
-// after its own bounded wait; no task is lost, the producer keeps its tile).
-constexpr unsigned RQ_FULL = 0x80000000u;
-__device__ __forceinline__ unsigned rq_reserve(unsigned* ctl, unsigned cap, const int* entries) {
-  const unsigned t = fetch_add_u32(&ctl[1], 1u);
-  const int* en = entries + (size_t)(t % cap) * 4;
-  if (rq_seq_load(en) == (int)t) return t;
-  const int64_t deadline = wall_ticks() + RQ_WAIT_TICKS;
-  while (rq_seq_load(en) != (int)t) {
-    if (wall_ticks() > deadline) return t | RQ_FULL;
-    __builtin_amdgcn_s_sleep(8);
-  }
-  return t;
-}
-// Thread-0 only. Claims the oldest reserved ticket, or RQ_NONE if none.
-__device__ __forceinline__ unsigned rq_pop(unsigned* ctl) {
-  for (;;) {
-    const unsigned h = __hip_atomic_load(&ctl[0], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const unsigned t = __hip_atomic_load(&ctl[1], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (h >= t) return RQ_NONE;
-    if (cas_u32(&ctl[0], h, h + 1) == h) return h;
-  }
-}
-// Thread-0 only, after every thread's checkpoint stores have completed and a
-// barrier: entry fields, an agent-scope release (it writes back this XCD's
-// L2, which holds every thread's checkpoint stores, so one release by one
-// thread covers the block), then seq = ticket + 1.
+__device__ __forceinline__ unsigned rq_pop(unsigned* ctl) { return proto::rq_pop<DevPlat>(ctl); }
 __device__ __forceinline__ void rq_publish(int* en, unsigned ticket, int task, int stage,
                                            int kind, int domain) {
-  en[0] = task;
-  en[1] = stage;
-  en[3] = (kind << 8) | domain;  // domain: where the retreat freed a CU (xcd * 4 + se)
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __hip_atomic_store(&en[2], (int)(ticket + 1), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  proto::rq_publish<DevPlat>(en, ticket, task, stage, kind, domain);
 }
-// Thread-0 only. Waits (bounded) for claimed ticket h to be published;
-// returns its kind + 1, or 0 if it was not published within RQ_WAIT_TICKS.
 __device__ __forceinline__ int rq_wait_ready(const int* en, unsigned h) {
-  const int64_t deadline = wall_ticks() + RQ_WAIT_TICKS;
-  for (;;) {
-    if (rq_seq_load(en) == (int)(h + 1)) {
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
-      return (en[3] >> 8) + 1;
-    }
-    if (wall_ticks() > deadline) return 0;
-    __builtin_amdgcn_s_sleep(8);
-  }
+  return proto::rq_wait_ready<DevPlat>(en, h);
 }
-// Thread-0 only, once every thread has read the entry's checkpoint back (a
-// barrier after the reads completed): frees the entry for ticket h + cap.
 __device__ __forceinline__ void rq_release(int* en, unsigned h, unsigned cap) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
-  __hip_atomic_store(&en[2], (int)(h + cap), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  proto::rq_release<DevPlat>(en, h, cap);
 }
 
 // ---------------------------------------------------------------------------

@@ -1,0 +1,193 @@
+// protocol.hpp -- the scheduler protocol of the persistent kernels, written
+// once for two executors: the gfx950 kernels (through DevPlat in
+// pipeline.hpp) and the CPU protocol simulator (apk_amd/sim/, through
+// std::atomic-style host primitives, one std::thread per block). It holds
+// only the parts whose correctness is a matter of ordering between blocks:
+//   - the XCD-aware work queue (exactly-once task hand-out with stealing);
+//   - the resume ring of the retreat arm (bounded MPMC ring with per-entry
+//     sequence numbers);
+//   - which generation a block acts on, and which blocks retreat at it.
+// The tile arithmetic, LDS rings and checkpoints stay in the kernels.
+//
+// The includer defines APK_PROTO_FN (the function qualifiers: device
+// inline for the kernels, plain inline for the simulator) and passes a
+// platform P with static members:
+//   unsigned fetch_add(unsigned*, unsigned)   relaxed, device-wide
+//   unsigned cas(unsigned*, unsigned e, unsigned d) -> previous value
+//   unsigned load(const unsigned*), int load(const int*)   relaxed
+//   void store(int*, int)                     relaxed
+//   void release(), acquire()                 device-wide fences
+//   int64_t ticks()                           constant-rate clock (100 MHz)
+//   void pause()                              back off while spinning
+#pragma once
+#include <stdint.h>
+
+#include "apk.h"
+
+#ifndef APK_PROTO_FN
+#error "APK_PROTO_FN must name the function qualifiers before protocol.hpp is included"
+#endif
+
+namespace apk {
+namespace proto {
+
+// ---------------------------------------------------------------------------
+// XCD-aware work queue. The tile grid (tilesM x tilesN) is walked in a
+// grouped order G: bands of GM tile rows, column by column inside a band, so
+// that consecutive positions form GM x n blocks of the grid. Positions
+// [q*T/8, (q+1)*T/8) of G are XCD q's list; pass p of the task space maps
+// position i of list q to task p*T + G(i). A worker pops its own XCD's list
+// (counter ctr[q]) and, once that is exhausted, the other lists in turn, so
+// every task id below num_tasks is handed out exactly once and task u always
+// computes tile u % T.
+template <class P>
+struct TaskQueue {
+  static constexpr int GM = 4;
+  unsigned* ctr;
+  int tilesM, tilesN, T;
+  unsigned numTasks, passes;
+
+  APK_PROTO_FN TaskQueue(unsigned* c, int tm, int tn, unsigned n)
+      : ctr(c), tilesM(tm), tilesN(tn), T(tm * tn), numTasks(n),
+        passes((n + (unsigned)(tm * tn) - 1) / (unsigned)(tm * tn)) {}
+
+  APK_PROTO_FN int grouped(int i) const {
+    const int band = i / (GM * tilesN);
+    const int left = tilesM - band * GM;
+    const int rows = left < GM ? left : GM;
+    const int r = i - band * GM * tilesN;
+    return (band * GM + r % rows) * tilesN + r / rows;
+  }
+  APK_PROTO_FN int list_begin(int q) const {
+    return (int)(((long long)q * T) / APK_QUEUE_XCDS);
+  }
+  // One caller per block. Returns the next task id, or 0xffffffff when every
+  // list is exhausted.
+  APK_PROTO_FN unsigned pop(int home) const {
+    for (int k = 0; k < APK_QUEUE_XCDS; ++k) {
+      const int q = (home + k) & (APK_QUEUE_XCDS - 1);
+      const int b = list_begin(q), n = list_begin(q + 1) - b;
+      if (n == 0) continue;
+      const unsigned total = (unsigned)n * passes;
+      for (;;) {
+        const unsigned j = P::fetch_add(&ctr[q], 1u);
+        if (j >= total) break;
+        const unsigned u =
+            (j / (unsigned)n) * (unsigned)T + (unsigned)grouped(b + (int)(j % (unsigned)n));
+        if (u < numTasks) return u;
+      }
+    }
+    return 0xffffffffu;
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Resume queue of the retreat arm: a bounded ring of `cap` entries, tickets
+// [head, tail) in ctl[0..1]. Entry i = {task, stage, seq, kind << 8 |
+// domain} with its checkpoint slot i; ticket t uses entry t % cap. `seq`
+// orders the entry's rounds (bounded MPMC ring with per-entry sequence
+// numbers): seq == t means free for ticket t, t + 1 published by ticket t's
+// producer, and the consumer of ticket t sets it to t + cap once it has read
+// the checkpoint back. A producer that finds its entry still taken after a
+// bounded wait declines the retreat (the ring is full); a consumer claims the
+// oldest reserved ticket and waits, bounded, for its producer (a resident
+// block on its exit path). The host sets seq = i for every entry before a job.
+constexpr unsigned RQ_NONE = 0xffffffffu;
+constexpr unsigned RQ_FULL = 0x80000000u;
+// Longest wait for an entry: 20 ms at the 100 MHz clock. A producer
+// publishes within microseconds; running out means a lost task, which the
+// exactly-once counts then report.
+constexpr int64_t RQ_WAIT_TICKS = 2000000;
+
+// Takes the next ticket with one fetch-add (no CAS loop: the producers of one
+// generation arrive together, and a CAS loop would serialise them round trip
+// by round trip) and waits, bounded, for its entry to be free. A ticket whose
+// entry stays taken for `wait` ticks is returned with RQ_FULL set: the caller
+// does not retreat and counts an error (that ticket's consumer then reports
+// it lost after its own bounded wait; no task is lost, the producer keeps its
+// tile).
+template <class P>
+APK_PROTO_FN unsigned rq_reserve(unsigned* ctl, unsigned cap, const int* entries,
+                                 int64_t wait = RQ_WAIT_TICKS) {
+  const unsigned t = P::fetch_add(&ctl[1], 1u);
+  const int* en = entries + (size_t)(t % cap) * 4;
+  if (P::load(&en[2]) == (int)t) return t;
+  const int64_t deadline = P::ticks() + wait;
+  while (P::load(&en[2]) != (int)t) {
+    if (P::ticks() > deadline) return t | RQ_FULL;
+    P::pause();
+  }
+  return t;
+}
+// Claims the oldest reserved ticket, or RQ_NONE if none.
+template <class P>
+APK_PROTO_FN unsigned rq_pop(unsigned* ctl) {
+  for (;;) {
+    const unsigned h = P::load(&ctl[0]);
+    const unsigned t = P::load(&ctl[1]);
+    if (h >= t) return RQ_NONE;
+    if (P::cas(&ctl[0], h, h + 1) == h) return h;
+  }
+}
+// Once the checkpoint stores of the whole block are complete: the entry's
+// fields, a device-wide release (on gfx950 it writes back this XCD's L2,
+// which holds every thread's checkpoint stores, so one release by one thread
+// covers the block), then seq = ticket + 1.
+template <class P>
+APK_PROTO_FN void rq_publish(int* en, unsigned ticket, int task, int stage, int kind,
+                             int domain) {
+  en[0] = task;
+  en[1] = stage;
+  en[3] = (kind << 8) | domain;  // domain: where the retreat freed a CU (xcd * 4 + se)
+  P::release();
+  P::store(&en[2], (int)(ticket + 1));
+}
+// Waits (bounded) for claimed ticket h to be published; returns its kind + 1,
+// or 0 if it was not published within `wait` ticks.
+template <class P>
+APK_PROTO_FN int rq_wait_ready(const int* en, unsigned h, int64_t wait = RQ_WAIT_TICKS) {
+  const int64_t deadline = P::ticks() + wait;
+  for (;;) {
+    if (P::load(&en[2]) == (int)(h + 1)) {
+      P::acquire();
+      return (en[3] >> 8) + 1;
+    }
+    if (P::ticks() > deadline) return 0;
+    P::pause();
+  }
+}
+// Once every reader of ticket h's checkpoint is done: frees the entry for
+// ticket h + cap.
+template <class P>
+APK_PROTO_FN void rq_release(int* en, unsigned h, unsigned cap) {
+  P::release();
+  P::store(&en[2], (int)(h + cap));
+}
+
+// ---------------------------------------------------------------------------
+// Generations. The flag carries a generation number g (event g - 1); a block
+// acts on the newest generation it has not seen. A relaunch (continuation)
+// joins a running job: generations raised before it started were handled by
+// the blocks that saw them, except that a retreat-arm continuation starts
+// from the generation it follows (launch_epoch), so that one raised before it
+// got its CUs still counts. Returns the block's initial last-seen generation,
+// clamped to the event arrays.
+APK_PROTO_FN int first_seen(int flag_at_start, int launch_epoch, int num_events) {
+  const int seen = launch_epoch > 0 ? launch_epoch : flag_at_start;
+  return seen < num_events ? seen : num_events;
+}
+
+// Which blocks of the retreat arm retreat at generation f: the first grid,
+// by quota, at f = 1; afterwards only the newest continuation (launched
+// after generation launch_epoch, so f > launch_epoch), all of it -- it holds
+// the CUs the previous generation freed, and it must complete for the next
+// continuation (queued behind it) to start. Every other block keeps working.
+enum RetreatRole { RETREAT_NONE = 0, RETREAT_BY_QUOTA = 1, RETREAT_ALL = 2 };
+APK_PROTO_FN int retreat_role(bool continuation, int launch_epoch, int f) {
+  if (continuation && launch_epoch > 0 && f > launch_epoch) return RETREAT_ALL;
+  if (continuation || f != 1) return RETREAT_NONE;
+  return RETREAT_BY_QUOTA;
+}
+
+}  // namespace proto
+}  // namespace apk

@@ -19,7 +19,7 @@
 //  * the background is the preemptible kernel with polling off (tasks cycle
 //    the tile grid, src/urgent_baseline.cu:78-80), the urgent job is
 //    apk_persistent_gemm with --urgent-blocks workers over its own tiles.
-// Additions: --engine valu64|mfma128|bf16x256, --gemm-k K (background depth, walked
+// Additions: --engine valu64|mfma128|bf16x256|bf16x128, --gemm-k K (background depth, walked
 // in --k chunks), --urgent-m/-n/-k (urgent GEMM shape; default
 // urgent-blocks tiles of depth --gemm-k, as the reference), --arrival
 // uniform|exp with --mean-gap-us (exponential delays, redrawn until they fall
@@ -98,9 +98,10 @@ int main(int argc, char** argv) {
   const int engine = engName == "mfma128"    ? APK_ENGINE_MFMA128
                      : engName == "valu64"   ? APK_ENGINE_VALU64
                      : engName == "bf16x256" ? APK_ENGINE_BF16X256
+                     : engName == "bf16x128" ? APK_ENGINE_BF16X128
                                              : -1;
   if (engine < 0) {
-    fprintf(stderr, "unknown --engine %s (valu64|mfma128|bf16x256)\n", engName.c_str());
+    fprintf(stderr, "unknown --engine %s (valu64|mfma128|bf16x256|bf16x128)\n", engName.c_str());
     return 1;
   }
   apk_engine_geometry geo;
@@ -154,7 +155,7 @@ int main(int argc, char** argv) {
 
   // hA/hB (hAu/hBu): the values the float64 reference multiplies, B as
   // K x N. dev*: the bytes the kernels read -- the same floats for the fp32
-  // engines; bf16 bit patterns with B transposed (Bt = N x K) for BF16X256.
+  // engines; bf16 bit patterns with B transposed (Bt = N x K) for the bf16 engines.
   const bool bf16 = geo.elem_bytes == 2;
   std::vector<float> hA((size_t)M * K), hB((size_t)K * N);
   std::vector<float> hAu((size_t)urgentM * urgentK), hBu((size_t)urgentK * urgentN);

@@ -95,6 +95,59 @@ Device device_query() {
   return d;
 }
 
+ClockProbe::ClockProbe(int probes) : probes_(probes) {
+  HIP_CHECK(hipMalloc(&d_, (size_t)probes_ * 4 * sizeof(long long)));
+  HIP_CHECK(hipMemset(d_, 0, (size_t)probes_ * 4 * sizeof(long long)));
+  HIP_CHECK(hipStreamCreateWithFlags(&s_, hipStreamNonBlocking));
+  APK_CHECK(apk_clock_probe(d_, probes_, 1, s_));  // creates the stream's queue
+  HIP_CHECK(hipStreamSynchronize(s_));
+  HIP_CHECK(hipMemset(d_, 0, (size_t)probes_ * 4 * sizeof(long long)));
+}
+
+ClockProbe::~ClockProbe() {
+  (void)hipStreamSynchronize(s_);
+  (void)hipStreamDestroy(s_);
+  (void)hipFree(d_);
+}
+
+void ClockProbe::launch(double window_us, double wall_mhz) {
+  const long long w = std::max(1LL, (long long)(window_us * wall_mhz));
+  APK_CHECK(apk_clock_probe(d_, probes_, std::min(w, 6000000000LL), s_));
+}
+
+bool ClockProbe::read(double wall_mhz, double* mean, double* mn, double* mx, int* count,
+                      long long lo_t, long long hi_t) const {
+  std::vector<long long> pr((size_t)probes_ * 4);
+  HIP_CHECK(hipMemcpy(pr.data(), d_, pr.size() * sizeof(long long), hipMemcpyDeviceToHost));
+  double sum = 0, lo = 0, hi = 0;
+  int n = 0;
+  for (int i = 0; i < probes_; ++i) {
+    if (pr[4 * i + 1] <= 0) continue;
+    if (hi_t > 0 && (pr[4 * i + 3] < lo_t || pr[4 * i + 3] + pr[4 * i + 1] > hi_t)) continue;
+    const double mhz = (double)pr[4 * i] / (double)pr[4 * i + 1] * wall_mhz;
+    lo = n ? std::min(lo, mhz) : mhz;
+    hi = n ? std::max(hi, mhz) : mhz;
+    sum += mhz;
+    ++n;
+  }
+  *count = n;
+  if (!n) return false;
+  *mean = sum / n;
+  *mn = lo;
+  *mx = hi;
+  return true;
+}
+
+void ClockProbe::print(const char* what, double wall_mhz, long long lo, long long hi) const {
+  double mean, mn, mx;
+  int n = 0;
+  if (read(wall_mhz, &mean, &mn, &mx, &n, lo, hi))
+    printf("engine clock during %s (%d probes): mean %.0f MHz | min %.0f | max %.0f\n", what,
+           n, mean, mn, mx);
+  else
+    printf("engine clock during %s: no probe ran inside it\n", what);
+}
+
 std::vector<long long> uniform_schedule(unsigned seed, double gmin_us,
                                         double gmax_us, int events) {
   std::mt19937 rng(seed);

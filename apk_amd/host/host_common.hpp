@@ -97,6 +97,29 @@ struct Device {
 };
 Device device_query();
 
+// Engine clock beside a throughput figure: one-wave apk_clock_probe blocks
+// on a stream of their own, launched right after the kernel they time and
+// counting shader cycles against the wall clock over `window_us`. The
+// stream is created and warmed by the constructor, so the first timed
+// launch does not wait for its queue. read() after the device has synced.
+class ClockProbe {
+ public:
+  explicit ClockProbe(int probes = 32);
+  ~ClockProbe();
+  void launch(double window_us, double wall_mhz);
+  // mean / min / max MHz over the probes that ran, and only those whose
+  // window lies inside [lo, hi] wall ticks when hi > 0; false when none did.
+  bool read(double wall_mhz, double* mean, double* mn, double* mx, int* n,
+            long long lo = 0, long long hi = 0) const;
+  // "engine clock during <what> (N probes): mean X MHz | min | max"
+  void print(const char* what, double wall_mhz, long long lo = 0, long long hi = 0) const;
+
+ private:
+  int probes_;
+  long long* d_ = nullptr;
+  hipStream_t s_ = nullptr;
+};
+
 // Event schedules (cumulative ns). uniform: mt19937(seed), U(gmin,gmax) us,
 // truncated per gap (src/yield.cu:824-830). exponential: mean_us.
 std::vector<long long> uniform_schedule(unsigned seed, double gmin_us,

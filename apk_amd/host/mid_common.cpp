@@ -46,6 +46,7 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
   const int engine = engName == "mfma128"    ? APK_ENGINE_MFMA128
                      : engName == "valu64"   ? APK_ENGINE_VALU64
                      : engName == "bf16x256" ? APK_ENGINE_BF16X256
+                     : engName == "bf16x128" ? APK_ENGINE_BF16X128
                                              : -1;
   const int naive = disc == "naive" ? 1 : 0;
   const int poison = disc == "poison" ? 1 : 0;
@@ -106,7 +107,7 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
 
   // hA/hB (and hAu/hBu): the values the float64 reference multiplies, B as
   // K x N. dev*: the bytes the kernels read -- the same floats for the fp32
-  // engines; bf16 bit patterns with B transposed (Bt = N x K) for BF16X256.
+  // engines; bf16 bit patterns with B transposed (Bt = N x K) for the bf16 engines.
   const bool bf16 = geo.elem_bytes == 2;
   std::vector<float> hA((size_t)M * K), hB((size_t)K * N);
   std::vector<float> hAu((size_t)Mu * Ku), hBu((size_t)Ku * Nu);
@@ -170,42 +171,27 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
     rig.reset(false);
     const double warmMs = timed_run(APK_POLL_OFF, (unsigned)blocks, false, 0, false);
     rig.reset(false);
-    // Engine clock during the timed run: one-wave probes on a side stream
-    // over 80% of the run's expected length (apk_clock_probe).
-    const int probes = 32;
-    long long* dProbe;
-    HIP_CHECK(hipMalloc(&dProbe, (size_t)probes * 4 * sizeof(long long)));
-    HIP_CHECK(hipMemset(dProbe, 0, (size_t)probes * 4 * sizeof(long long)));
-    hipStream_t side;
-    HIP_CHECK(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
-    const long long window = std::max(
-        1LL, (long long)(0.8 * warmMs * ((double)tasks / blocks) * 1e3 * dev.wall_mhz));
+    // Engine clock during the timed run: probes over 80% of its expected
+    // length (apk_clock_probe).
+    ClockProbe probe;
     hipEvent_t a, b;
     HIP_CHECK(hipEventCreate(&a));
     HIP_CHECK(hipEventCreate(&b));
     HIP_CHECK(hipEventRecord(a, kStream));
     rig.launch(APK_POLL_OFF, 1, resume, 0, tasks, false, 0, false, kStream, 0, 0);
     HIP_CHECK(hipEventRecord(b, kStream));
-    APK_CHECK(apk_clock_probe(dProbe, probes, window, side));
+    probe.launch(0.8 * warmMs * ((double)tasks / blocks) * 1e3, dev.wall_mhz);
     HIP_CHECK(hipDeviceSynchronize());
     HIP_CHECK(hipGetLastError());
     float fms = 0;
     HIP_CHECK(hipEventElapsedTime(&fms, a, b));
     const double ms = fms;
-    std::vector<long long> pr((size_t)probes * 4);
-    HIP_CHECK(hipMemcpy(pr.data(), dProbe, pr.size() * 8, hipMemcpyDeviceToHost));
-    std::vector<double> mhz;
-    for (int i = 0; i < probes; ++i)
-      if (pr[4 * i + 1] > 0) mhz.push_back((double)pr[4 * i] / pr[4 * i + 1] * dev.wall_mhz);
     const double flop = 2.0 * geo.tile_m * geo.tile_n * (double)K * tasks;
     const double peak = bf16 ? kPeakBf16TF : kPeakFp32TF;
     printf("calibrate K=%d: %u tasks on %d blocks in %.3f ms -> %.2f us/task/block | %.1f "
            "GFLOP/s (%.1f%% of %.1f TFLOP/s)\n", K, tasks, blocks, ms, ms * 1e3 * blocks / tasks,
            flop / (ms * 1e6), 100.0 * flop / (ms * 1e9) / peak, peak);
-    if (!mhz.empty())
-      printf("engine clock during the run (%zu probes): mean %.0f MHz | min %.0f | max %.0f\n",
-             mhz.size(), std::accumulate(mhz.begin(), mhz.end(), 0.0) / mhz.size(),
-             *std::min_element(mhz.begin(), mhz.end()), *std::max_element(mhz.begin(), mhz.end()));
+    probe.print("the run", dev.wall_mhz);
     return 0;
   }
 
@@ -364,10 +350,13 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
   const bool cOk = verify_C(cNow);
 
   unsigned long long yields = 0, inflight = 0, stale = 0, ckpts = 0, inflightAll = 0,
-                     staleAll = 0;
+                     staleAll = 0, tSave = 0, tUrg = 0, tRest = 0;
   for (int b = 0; b < blocks; ++b) {
     const unsigned long long* st = &r.stats[(size_t)b * APK_STATS_PER_BLOCK];
     yields += st[APK_ST_YIELDS];
+    tSave += st[APK_ST_SAVE];
+    tUrg += st[APK_ST_URGENT];
+    tRest += st[APK_ST_RESTORE];
     inflight += st[APK_ST_INFLIGHT];
     stale += st[APK_ST_STALE];
     ckpts += st[APK_ST_CHECKPOINTS];
@@ -438,6 +427,10 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
     printf("yields: %llu | a live stage was still in flight when the drain began: %llu "
            "(of all %llu checkpoints: %llu) | stale checkpoints: %llu\n", yields, inflight, ckpts,
            inflightAll, staleAll);
+  if (yields)  // block averages on the device wall clock
+    printf("per yield: save %.2f us, urgent %.2f us, restore %.2f us\n",
+           tSave / dev.wall_mhz / yields, tUrg / dev.wall_mhz / yields,
+           tRest / dev.wall_mhz / yields);
   printf("resumed background: %lld of %lld task fingerprints differ from the unpreempted "
          "tile%s | C bit-identical to the unpreempted run: %s\n", hashBad, hashed,
          hashAll ? "" : " (not hashed: too many tasks)", cBits ? "yes" : "NO");

@@ -38,13 +38,18 @@ enum {
  *             tile, src/tcyield.cu:91-356). Operands are bf16 (uint16 bit
  *             patterns): A is M x K row-major and B is passed TRANSPOSED, as
  *             Bt = N x K row-major (C = A . Bt^T); C is fp32 M x N.
+ *  BF16X128 : 128x128 tile of the same bf16 GEMM (same operand layout),
+ *             256 threads, 16-deep k-stages, 33 KiB of LDS: runs at 2 and
+ *             4 blocks per CU, where the 256x256 tile cannot (configs[4] of
+ *             the reference's study at 2 and 4 blocks/CU).
  * For the fp32 engines A is M x K and B is K x N, row-major fp32.
  */
 enum {
   APK_ENGINE_VALU64 = 0,
   APK_ENGINE_MFMA128 = 1,
   APK_ENGINE_BF16X256 = 2,
-  APK_ENGINE_COUNT = 3
+  APK_ENGINE_BF16X128 = 3,
+  APK_ENGINE_COUNT = 4
 };
 
 /* Per-step timing record; layout of TileRecord (src/tile.cuh:37-42). start

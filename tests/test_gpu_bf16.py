@@ -1,5 +1,7 @@
-"""GPU parity of the bf16 MFMA engine (APK_ENGINE_BF16X256: 256x256 tile,
-v_mfma_f32_32x32x16_bf16, fp32 accumulation) through the C ABI.
+"""GPU parity of the bf16 MFMA engines (v_mfma_f32_32x32x16_bf16, fp32
+accumulation) through the C ABI: APK_ENGINE_BF16X256 (256x256 tile, 1 block
+per CU) and APK_ENGINE_BF16X128 (128x128 tile, run here at 2 and 4 blocks
+per CU, the occupancies at which the 256x256 tile cannot run).
 
 What is pinned:
   * operand/accumulator lane layouts: small-integer bf16 inputs make every
@@ -22,6 +24,12 @@ from gpu_util import assert_queue_drained, dev, say
 
 pytestmark = pytest.mark.gpu
 
+ENGS = ["bf16x256", "bf16x128"]
+
+
+def tile_of(apk, eng):
+    return apk.geometry(eng).tile_m
+
 
 def bits_of_small_ints(rng, shape, lo=-3, hi=3):
     """bf16 bit patterns of small integers (exact in bf16) and their values."""
@@ -31,10 +39,10 @@ def bits_of_small_ints(rng, shape, lo=-3, hi=3):
     return bits, v
 
 
-def run_bf16(torch, apk, A_bits, Bt_bits, k_chunk, blocks=None):
+def run_bf16(torch, apk, A_bits, Bt_bits, k_chunk, blocks=None, eng=None):
     M, K = A_bits.shape
     N = Bt_bits.shape[0]
-    eng = apk.ENGINE_BF16X256
+    eng = apk.ENGINE_BF16X256 if eng is None else eng
     if blocks is None:
         blocks = apk.device_info().cu_count * apk.occupancy(eng)
     dA, dB = dev(torch, A_bits.view(np.int16)), dev(torch, Bt_bits.view(np.int16))
@@ -46,24 +54,29 @@ def run_bf16(torch, apk, A_bits, Bt_bits, k_chunk, blocks=None):
     return dC.cpu().numpy(), nxt.cpu().numpy()
 
 
-def test_bf16_layout_exact_small_integers(torch_gpu, apk):
-    say("bf16x256 layout: small integers, M=512 N=256 K=96")
+@pytest.mark.parametrize("name", ENGS)
+def test_bf16_layout_exact_small_integers(torch_gpu, apk, name):
+    eng = apk.ENGINES[name]
+    T = tile_of(apk, eng)
+    M, N, K = 2 * T, T, 96
+    say(f"{name} layout: small integers, M={M} N={N} K={K}")
     rng = np.random.default_rng(5)
-    M, N, K = 512, 256, 96
     A_bits, A = bits_of_small_ints(rng, (M, K))
     Bt_bits, Bt = bits_of_small_ints(rng, (N, K))
-    C, nxt = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=K, blocks=3)
+    C, nxt = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=K, blocks=3, eng=eng)
     ref = (A.astype(np.int64) @ Bt.astype(np.int64).T).astype(np.float32)
-    assert_queue_drained(nxt, (M // 256) * (N // 256), blocks=3)
+    assert_queue_drained(nxt, (M // T) * (N // T), blocks=3)
     assert np.array_equal(C, ref)
 
 
-def test_bf16_normal_inputs_vs_float64(torch_gpu, apk):
-    say("bf16x256 numerics: normal(0,1) bf16, M=N=512 K=1024")
+@pytest.mark.parametrize("name", ENGS)
+def test_bf16_normal_inputs_vs_float64(torch_gpu, apk, name):
+    say(f"{name} numerics: normal(0,1) bf16, M=N=512 K=1024")
+    eng = apk.ENGINES[name]
     M, N, K = 512, 512, 1024
     A_bits, A, B_bits, B = oracle.fill_normal_bf16(7, M, N, K)
     Bt_bits = np.ascontiguousarray(B_bits.T)
-    C, _ = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=256)
+    C, _ = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=256, eng=eng)
     ref = oracle.gemm_f64(A, B, threads=8)
     rf = oracle.rel_frobenius(C, ref)
     say(f"  rel-Frobenius {rf:.3e}")
@@ -71,28 +84,42 @@ def test_bf16_normal_inputs_vs_float64(torch_gpu, apk):
     assert rf <= 1e-5  # fp32 accumulation of exact bf16 products
 
 
-def test_bf16_bit_identical_across_chunks_and_workers(torch_gpu, apk):
-    say("bf16x256 determinism across k_chunk and worker counts")
+@pytest.mark.parametrize("name", ENGS)
+def test_bf16_bit_identical_across_chunks_and_workers(torch_gpu, apk, name):
+    say(f"{name} determinism across k_chunk and worker counts")
+    eng = apk.ENGINES[name]
     M, N, K = 512, 512, 512
     A_bits, _, B_bits, _ = oracle.fill_normal_bf16(11, M, N, K)
     Bt_bits = np.ascontiguousarray(B_bits.T)
-    C0, _ = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=32, blocks=1)
+    C0, _ = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=32, blocks=1, eng=eng)
     for kc, blocks in ((512, None), (64, 3), (128, 2)):
-        C1, _ = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=kc, blocks=blocks)
+        C1, _ = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=kc, blocks=blocks, eng=eng)
         assert np.array_equal(C0.view(np.uint32), C1.view(np.uint32)), (kc, blocks)
+
+
+def test_bf16x128_runs_at_4_blocks_per_cu(apk):
+    """The 128x128 tile's plain and yield kernels fit 4 blocks per CU (128
+    registers and 33 KiB of LDS per block); the 256x256 tile fits one."""
+    e128, e256 = apk.ENGINES["bf16x128"], apk.ENGINES["bf16x256"]
+    assert apk.occupancy(e128) >= 4
+    for poll in (apk.POLL_OFF, apk.POLL_CHUNK, apk.POLL_STAGE, apk.POLL_ISSUE):
+        assert apk.yield_occupancy(e128, poll) >= 4, poll
+    assert apk.occupancy(e256) == 1
 
 
 class Bf16Job:
     """Preemptible bf16 GEMM with an urgent bf16 job, all through the C ABI."""
 
-    def __init__(self, torch, apk, M, N, K, kc, Mu, Nu, Ku, events, blocks, passes, seed=3):
+    def __init__(self, torch, apk, M, N, K, kc, Mu, Nu, Ku, events, blocks, passes, seed=3,
+                 eng=None):
         T = torch
         self.t, self.apk = torch, apk
-        self.eng = apk.ENGINE_BF16X256
+        self.eng = apk.ENGINE_BF16X256 if eng is None else eng
+        self.tile = tile_of(apk, self.eng)
         self.M, self.N, self.K, self.kc = M, N, K, kc
         self.Mu, self.Nu, self.Ku = Mu, Nu, Ku
-        self.tiles = (M // 256) * (N // 256)
-        self.U = (Mu // 256) * (Nu // 256)
+        self.tiles = (M // self.tile) * (N // self.tile)
+        self.U = (Mu // self.tile) * (Nu // self.tile)
         self.num_tasks = self.tiles * passes
         self.events, self.blocks = events, blocks
         A_bits, self.A, B_bits, self.B = oracle.fill_normal_bf16(seed, M, N, K)
@@ -161,19 +188,33 @@ class Bf16Job:
         }
 
 
-@pytest.fixture(scope="module")
-def bf16_job(torch_gpu, apk):
-    say("building bf16x256 yield job M=N=512 K=1024 kc=64, urgent 256x512x256")
-    # 144 passes = 9 tiles per block: the job outlasts the 24 events the
-    # setter (block 0) raises 3 us apart at its own poll sites.
-    return Bf16Job(torch_gpu, apk, 512, 512, 1024, 64, 256, 512, 256, events=24, blocks=64,
-                   passes=144)
+# (engine, blocks per CU or a block count): the 256x256 tile on 64 workers,
+# the 128x128 tile at 2 and 4 blocks on every CU.
+JOBS = [("bf16x256", 64), ("bf16x128", "2/CU"), ("bf16x128", "4/CU")]
+
+
+@pytest.fixture(scope="module", params=JOBS, ids=lambda j: f"{j[0]}-{j[1]}".replace("/", "per"))
+def bf16_job(torch_gpu, apk, request):
+    name, b = request.param
+    eng = apk.ENGINES[name]
+    blocks = b if isinstance(b, int) else apk.device_info().cu_count * int(b.split("/")[0])
+    for poll in (apk.POLL_CHUNK, apk.POLL_STAGE):  # every worker resident
+        assert apk.yield_occupancy(eng, poll) * apk.device_info().cu_count >= blocks
+    T = tile_of(apk, eng)
+    # 9 tasks per block: the job outlasts the 24 events the setter (block 0)
+    # raises 3 us apart at its own poll sites.
+    tiles = (512 // T) ** 2
+    passes = -(-9 * blocks // tiles)
+    say(f"building {name} yield job M=N=512 K=1024 kc=64 on {blocks} blocks ({passes} passes), "
+        "urgent 256x512x256")
+    return Bf16Job(torch_gpu, apk, 512, 512, 1024, 64, 256, 512, 256, events=24, blocks=blocks,
+                   passes=passes, eng=eng)
 
 
 @pytest.mark.parametrize("poll,resume", [(2, 0), (2, 1), (2, 2), (1, 0)])
 def test_bf16_yield_bit_identical(bf16_job, apk, poll, resume):
     j = bf16_job
-    say(f"bf16x256 yield poll={poll} resume={resume}")
+    say(f"engine {j.eng} on {j.blocks} blocks: yield poll={poll} resume={resume}")
     ref = j.run(apk.POLL_OFF, events=0)
     r = j.run(poll, resume=resume)
     fired = int((r["set_gt"] != 0).sum())
@@ -181,8 +222,9 @@ def test_bf16_yield_bit_identical(bf16_job, apk, poll, resume):
     assert fired == j.events and yields >= fired
     assert np.array_equal(r["C"].view(np.uint32), ref["C"].view(np.uint32))
     # every task's fingerprint equals its tile's fingerprint in the unpreempted C
-    tn = j.N // 256
-    th = np.array([oracle.tile_hash(ref["C"], (t // tn) * 256, (t % tn) * 256, 256, 256)
+    T = j.tile
+    tn = j.N // T
+    th = np.array([oracle.tile_hash(ref["C"], (t // tn) * T, (t % tn) * T, T, T)
                    for t in range(j.tiles)], dtype=np.uint64)
     assert np.array_equal(r["task_hash"], th[np.arange(j.num_tasks) % j.tiles])
     # every claimed event's urgent output equals the non-preemptible urgent GEMM
@@ -194,13 +236,14 @@ def test_bf16_yield_bit_identical(bf16_job, apk, poll, resume):
 
 
 def run_bf16_urgent(j):
-    C, _ = run_bf16(j.t, j.apk, j.Aubits, j.Bubits, k_chunk=j.Ku, blocks=2)
+    C, _ = run_bf16(j.t, j.apk, j.Aubits, j.Bubits, k_chunk=j.Ku, blocks=2, eng=j.eng)
     return C
 
 
 def test_bf16_float64_and_oracle(bf16_job, apk):
     j = bf16_job
-    say("bf16x256 stage yields: float64 check and exactly-once oracle")
+    say(f"engine {j.eng} on {j.blocks} blocks: stage yields, float64 check and exactly-once "
+        "oracle")
     r = j.run(apk.POLL_STAGE, resume=0, use_oracle=True)
     ref = oracle.gemm_f64(j.A, j.B, threads=8)
     assert oracle.rel_frobenius(r["C"], ref) <= 1e-5
@@ -208,13 +251,20 @@ def test_bf16_float64_and_oracle(bf16_job, apk):
     assert (r["u_exec"] == j.U).all()
 
 
-@pytest.fixture(scope="module")
-def bf16_odd_job(torch_gpu, apk):
-    # K = 160 is 5 k-stages: the stage loop takes them in pairs (0,1), (2,3),
-    # (4, a stage of zeros); the urgent K = 96 (3 stages) ends the same way.
-    say("building bf16x256 odd-length yield job M=N=512 K=160 kc=32, urgent 256x256x96")
-    return Bf16Job(torch_gpu, apk, 512, 512, 160, 32, 256, 256, 96, events=24, blocks=64,
-                   passes=384)
+@pytest.fixture(scope="module", params=ENGS)
+def bf16_odd_job(torch_gpu, apk, request):
+    # 5 k-stages (K = 160 for the 32-deep stages of the 256x256 tile, 80 for
+    # the 16-deep stages of the 128x128 tile): the stage loop takes them in
+    # pairs (0,1), (2,3), (4, a stage of zeros); the urgent job's 3 stages end
+    # the same way.
+    eng = apk.ENGINES[request.param]
+    ks = apk.geometry(eng).k_stage
+    T = tile_of(apk, eng)
+    passes = 1536 // (512 // T) ** 2  # 24 tasks per block
+    say(f"building {request.param} odd-length yield job M=N=512 K={5 * ks} kc={ks}, urgent "
+        f"256x256x{3 * ks}")
+    return Bf16Job(torch_gpu, apk, 512, 512, 5 * ks, ks, 256, 256, 3 * ks, events=24, blocks=64,
+                   passes=passes, eng=eng)
 
 
 @pytest.mark.parametrize("resume", [0, 1, 2])
@@ -224,7 +274,7 @@ def test_bf16_odd_length_pairs_yield(bf16_odd_job, apk, resume):
     to the unpreempted run, within tolerance of float64, urgent outputs equal the
     non-preemptible urgent GEMM, every task and event counted once."""
     j = bf16_odd_job
-    say(f"bf16x256 odd-length pairs, stage yields, resume={resume}")
+    say(f"engine {j.eng} odd-length pairs, stage yields, resume={resume}")
     ref = j.run(apk.POLL_OFF, events=0)
     r = j.run(apk.POLL_STAGE, resume=resume, use_oracle=True)
     fired = int((r["set_gt"] != 0).sum())

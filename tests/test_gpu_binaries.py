@@ -14,12 +14,16 @@ Scaling: fewer events / trials / tasks and smaller tile grids than the
 drivers use, so that each binary runs for seconds.
 """
 import os
+import re
 import struct
 import subprocess
 
 import numpy as np
 import pytest
 
+from apk_amd.analysis import common as an_common
+from apk_amd.analysis import maxofn, visibility
+from apk_amd.analysis import spread as an_spread
 from gpu_util import say
 
 pytestmark = pytest.mark.gpu
@@ -92,6 +96,17 @@ def test_calibrate_sh(tmp_path):
         assert all(int(r["end_cyc"]) >= int(r["start_cyc"]) for r in rows)
 
 
+def test_persistent_prints_engine_clock(tmp_path):
+    """The final pass's TFLOP/s comes with the engine clock read on the device
+    during that pass (apk_clock_probe windows inside the pass's records)."""
+    out = run_bin("persistent", "--engine", "mfma128", "--tiles-m", 32, "--tiles-n", 32,
+                  "--gemm-k", 4096, "--k", 128, "--passes", 3, "--verify", 0,
+                  "--csv", tmp_path / "p.csv")
+    m = re.search(r"engine clock during the final pass \((\d+) probes\): mean (\d+) MHz", out)
+    assert m, out[-1500:]
+    assert int(m.group(1)) >= 1 and 500 <= int(m.group(2)) <= 3000, m.group(0)
+
+
 def test_phase2_sh(tmp_path):
     """scripts/phase2.sh: urgent_baseline --mode sat|sat-1|1persm --trials T."""
     for mode in ("sat", "sat-1", "1persm"):
@@ -143,6 +158,15 @@ def test_phase3_sh(tmp_path):
                 assert int(set_ns[e]) == int(r["set_ns"]) or abs(int(set_ns[e]) - int(r["set_ns"])) <= 20
         assert complete >= 250, complete
         assert "claim_site" in cols
+        # the analysis ports read the binary's own files: the identity
+        # lat == first + spread holds row by row, and the OBS1 matrix feeds
+        # the held-out max-of-N model
+        n = an_spread.analyse_rows(rows, 20, str(lat))[0]
+        assert n == sum(1 for r in rows if r["complete"] == "1" and int(r["event"]) >= 20)
+        d = an_common.delays_us(obs, 20)
+        assert d.shape[1] == blocks - 1 and d.shape[0] >= 200
+        for q, pred, meas in maxofn.heldout(d):
+            assert pred > 0 and meas > 0
 
 
 def test_phase5_sh(tmp_path):
@@ -206,6 +230,9 @@ def test_visibility(tmp_path, loaded, iters):
     assert (set_ns > 0).all()
     assert (o > 0).all(), f"{int((o == 0).sum())} (event, block) pairs never observed"
     assert (o >= set_ns[:, None] - 20).all()
+    p50, p99 = visibility.dmax_quantiles(obs, 20)
+    dmax = ((o - set_ns[:, None]).max(axis=1) / 1e3)[20:]
+    assert dmax.min() <= p50 <= p99 <= dmax.max()
 
 
 def test_pareto_sh(tmp_path):
