@@ -70,12 +70,18 @@ k_persistent_yield(const apk_yield_params) {
   auto copies = [&] { return P().flag_copies > 0 ? P().flag_copies : 1; };
   auto row = [&] { return P().block_base + bid; };  // this block's stats / obs column
   // Poll sites sit at barriers: every GROUP-th k-stage at the finest.
+  // Chunk polls (APK_POLL_CHUNK) are at every poll_every-th k-chunk boundary
+  // the block passes, counted across its tasks (src/yield.cu:124-134 polls
+  // at every PE-th tile boundary): chunksDone counts the chunks of the
+  // background tasks this block has completed.
+  const int chunkStages = P().k_chunk / E::KS;
+  const int pollEvery = POLL == APK_POLL_CHUNK && P().poll_every > 0 ? P().poll_every : 1;
   const int pollStride = [&] {
-    const int st = (POLL == APK_POLL_STAGE || POLL == APK_POLL_ISSUE)
-                       ? 1
-                       : (P().k_chunk / E::KS) * (P().poll_every > 0 ? P().poll_every : 1);
+    const int st = (POLL == APK_POLL_STAGE || POLL == APK_POLL_ISSUE) ? 1
+                                                                      : chunkStages * pollEvery;
     return (st + E::GROUP - 1) / E::GROUP * E::GROUP;
   }();
+  int chunksDone = 0;  // uniform
   const i32x4 flag_rsrc =
       make_rsrc((const char*)P().flag + (size_t)(bid % copies()) * APK_FLAG_STRIDE, 4);
   const bool isSetter = P().flag_set != nullptr && P().sched != nullptr && bid == 0;
@@ -297,7 +303,18 @@ k_persistent_yield(const apk_yield_params) {
     };
     for (;;) {  // (re)entries of the stage loop of this job
       if (srcKind != AS_IS) {
-        nextSite = !pollable ? S + 2 : (s + pollStride - 1) / pollStride * pollStride;
+        if (!pollable) {
+          nextSite = S + 2;
+        } else if (POLL == APK_POLL_CHUNK && pollEvery > 1) {
+          // the next chunk boundary c at or after s whose running count
+          // chunksDone + c is a multiple of poll_every
+          const int c0 = (s + chunkStages - 1) / chunkStages;
+          const int ph = (chunksDone + c0) % pollEvery;
+          const int st = (c0 + (ph ? pollEvery - ph : 0)) * chunkStages;
+          nextSite = (st + E::GROUP - 1) / E::GROUP * E::GROUP;
+        } else {
+          nextSite = (s + pollStride - 1) / pollStride * pollStride;
+        }
         const int64_t tIn = wall_ticks();
         ahead = POLL == APK_POLL_ISSUE && srcKind == FULL;
         if (srcKind == FRESH) {
@@ -657,6 +674,7 @@ k_persistent_yield(const apk_yield_params) {
     if (ORACLE && tid == 0)
       fetch_add_i32(urgent ? &P().u_exec_count[serving] : &P().exec_count[task], 1);
     if (urgent) uidx = pop_urgent(serving);
+    else chunksDone += S / chunkStages;
   }
 
   if (P().run_gt && tid == 0 && fetch_add_u32(P().exit_count, 1u) == gridDim.x - 1)

@@ -23,9 +23,12 @@
 // the same tile computed without preemption; and C against float64.
 // --discipline poison adds +1.0 to one staged B value of every urgent tile,
 // so every claimed event must be flagged corrupt (src/midyield.cu:146-147).
-// --poll issue is accepted as stage: the flag sample is issued together with
-// the stage loads here, so there is no separate issue site.
-// Additions: --engine valu64|mfma128 (default valu64), --gemm-k K (depth of
+// --poll issue is the window-forcing issue site (src/midyield.cu:246-258):
+// the next stages' loads go out, the flag is polled right behind them and a
+// yield checkpoints before any wait, so --discipline naive can save a stage
+// still in flight.
+// Additions: --engine valu64|mfma128|bf16x256|bf16x128 (default valu64),
+// --dump-obs PATH (the OBS1 observation matrix), --gemm-k K (depth of
 // the background GEMM, default --k), --resume ckpt|acc|restart, --urgent-m/
 // -n/-k (default one tile of depth --k), --arrival uniform|exp,
 // --mean-gap-us, --seed, --flag-copies, --verify-rows (float64 rows of C).

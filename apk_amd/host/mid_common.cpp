@@ -34,6 +34,7 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
   const int warmupEvents = (int)parse_arg(argc, argv, "--warmup-events", 100);
   const bool oracle = parse_arg(argc, argv, "--oracle", 0) != 0;
   const char* csvPath = parse_str(argc, argv, "--csv", "");
+  const char* dumpObsPath = parse_str(argc, argv, "--dump-obs", "");
   const std::string engName = parse_str(argc, argv, "--engine", v.engine);
   const int gemmK = (int)parse_arg(argc, argv, "--gemm-k", kChunk);
   const std::string resumeS = parse_str(argc, argv, "--resume", "ckpt");
@@ -307,15 +308,20 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
     printf("verify: %u tasks (~%.0f us), %d events %.1f us apart\n", tasks, runUs, nEv,
            gapNs / 1e3);
   } else if (mode == "events") {
-    // Size the background queue off a probe drain so the schedule fits with
-    // ~1.5x margin (src/midyield.cu:604-618).
+    // Size the background queue off a probe drain so the schedule fits
+    // (src/midyield.cu:604-618 sizes it with 1.5x margin). The probe runs
+    // twice and the second is timed: the first starts from an idle clock and
+    // overstates the task time. The margin is 2x: a probe of 8 tasks per
+    // block still runs slower per task than the full job does.
     rig.reset(false);
     const unsigned probe = (unsigned)blocks * 8;
+    timed_run(poll, probe, false, 0, false);
+    rig.reset(false);
     const double usPerTask = timed_run(poll, probe, false, 0, false) * 1e3 / probe;
     gaps = arrival == "exp" ? exp_schedule(seed, meanGapUs, nEv)
                             : uniform_schedule(seed, gapMinUs, gapMaxUs, nEv);
     const double schedUs = gaps.back() / 1e3;
-    tasks = (unsigned)std::min(1.5 * schedUs / usPerTask, 4.0e9);
+    tasks = (unsigned)std::min(2.0 * schedUs / usPerTask, 4.0e9);
     printf("probe: %.3f us/task -> %u bg tasks for a %.1f ms schedule\n", usPerTask, tasks,
            schedUs / 1e3);
   } else {
@@ -333,6 +339,7 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
   rig.setSchedule(gaps, dev.wall_mhz);
   const double runMs = timed_run(poll, tasks, true, nEv, oracle);
   const EventResult r = rig.readEvents(nEv);
+  dump_obs1(dumpObsPath, r, nEv, blocks, dev.wall_mhz);  // OBS1, as yield --dump-obs
   const std::vector<EventRow> rowsE = summarize_events(r, nEv, blocks, dev.wall_mhz);
 
   // Background: fingerprints of every task against the unpreempted tile.

@@ -159,7 +159,7 @@ struct Sim {
     const int home = bid & (APK_QUEUE_XCDS - 1);
     const int dom = bid % c.domains;
     const int quota = (c.retreatN + c.domains - 1) / c.domains;
-    int lastSeen = 0;
+    int lastSeen = 0, chunksDone = 0;  // chunksDone: stage boundaries of completed tasks
     if (cont) lastSeen = proto::first_seen(HostPlat::load(&flag), epoch, c.events);
     proto::TaskQueue<HostPlat> tq(ctr.data(), c.tilesM, c.tilesN, numTasks);
     const unsigned T = (unsigned)(c.tilesM * c.tilesN);
@@ -214,7 +214,7 @@ struct Sim {
       if (kind >= 0) enter(ck, kind);
       bool retreated = false;
       while (s < S) {
-        if (s % c.pollEvery == 0) {
+        if ((chunksDone + s) % c.pollEvery == 0) {  // every poll_every-th boundary passed
           int f = HostPlat::load(&flag);
           if (f > c.events) f = c.events;
           if (f > lastSeen) {
@@ -289,6 +289,7 @@ struct Sim {
         ++s;
       }
       if (retreated) break;  // the block exits: its CUs go to the urgent kernel
+      chunksDone += S;
       __atomic_fetch_add(&exec[task], 1, __ATOMIC_RELAXED);
       result[task] = acc;
     }
