@@ -8,7 +8,9 @@ the 1024 output tiles; inputs are resident in HBM before the timed region.
 
 Also reported (same line): the roofline of the GEMM kernel (fp32 MFMA dense
 peak 157.3 TFLOP/s; per-launch duration from HIP events on the launch stream),
-the engine clock the launches ran at (device-side probe), and the CPU
+the engine clock the launches ran at (device-side probe; the timed steps follow
+an untimed pre-warm of back-to-back launches, --prewarm-ms, because the clock
+climbs from its idle level over about a second of load), and the CPU
 baseline: the reference's float64 host GEMM (i-k-j, src/persistent.cu:221-227,
 restated in oracle/) timed on this host -- the whole GEMM with OpenMP on the
 host threads this process may use, and a 1024-row sample on one thread -- whose
@@ -228,6 +230,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--prewarm-ms", type=float, default=1500,
+                    help="back-to-back untimed launches before the warm-up steps, so that "
+                         "the engine clock has left its idle level (it takes ~1 s to climb)")
     ap.add_argument("--size", type=int, default=4096)
     ap.add_argument("--k-chunk", type=int, default=32)
     ap.add_argument("--cpu-rows", type=int, default=1024)
@@ -317,6 +322,21 @@ def main():
                                 stream.cuda_stream)
         ends[i].record(stream)
 
+    # Pre-warm: the engine clock climbs from its idle level over ~1 s of load
+    # (profiles/engine_clock_readback.md); a few warm-up launches leave it
+    # mid-climb. Untimed, on a counter set of its own.
+    pre_counters = torch.zeros(apk_amd.QUEUE_WORDS, dtype=torch.int32, device="cuda")
+    pre_launches = 0
+    t_pre = time.perf_counter()
+    while (time.perf_counter() - t_pre) * 1e3 < args.prewarm_ms:
+        for _ in range(20):
+            pre_counters.zero_()
+            apk_amd.persistent_gemm(eng, dA.data_ptr(), dB.data_ptr(), dC.data_ptr(),
+                                    M, N, K, kc, pre_counters.data_ptr(), None, blocks,
+                                    stream.cuda_stream)
+            pre_launches += 1
+        stream.synchronize()
+    pre_ms = (time.perf_counter() - t_pre) * 1e3
     for i in range(args.warmup):
         step(i)
     torch.cuda.synchronize()
@@ -383,6 +403,7 @@ def main():
             "frac_at_measured_clock": round(achieved / (PEAK_FP32_TF * clock["mean"] / 2400.0), 4),
             "traffic": measured_traffic() if (S, kc) == (4096, 32) else None,
         },
+        "prewarm": {"ms": round(pre_ms, 1), "launches": pre_launches},
     }
     if not args.no_preempt:
         out["preemption"] = preemption_metrics(args.events, args.trials)
