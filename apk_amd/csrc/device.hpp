@@ -117,11 +117,17 @@ __device__ __forceinline__ buf_rsrc make_buf_rsrc(const void* base, uint32_t byt
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                            0x00020000);
 }
+// CPOL: the store's cache policy; CPOL_SC1 (agent coherence) writes the line
+// through this XCD's L2, so the data is visible device-wide once the store
+// has completed (vmcnt), with no write-back of the whole L2 (a release fence
+// at agent scope is one: buffer_wbl2 sc1).
+constexpr int CPOL_SC1 = 16;
+template <int CPOL = 0>
 __device__ __forceinline__ void buf_store_f4(float4 v, buf_rsrc r, int voff, int soff) {
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
   const u32x4 u = {__float_as_uint(v.x), __float_as_uint(v.y), __float_as_uint(v.z),
                    __float_as_uint(v.w)};
-  __builtin_amdgcn_raw_buffer_store_b128(u, r, voff, soff, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(u, r, voff, soff, CPOL);
 }
 __device__ __forceinline__ float4 buf_load_f4(buf_rsrc r, int voff, int soff) {
   typedef unsigned u32x4 __attribute__((ext_vector_type(4)));

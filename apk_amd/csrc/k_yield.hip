@@ -508,7 +508,9 @@ k_persistent_yield(const apk_yield_params) {
       // `naive`, the saved stages are also compared with the landed ring: a
       // difference is a stale checkpoint, which the resumed tile inherits.
       int ckMoved = 0, ckStale = 0;  // uniform: what `observe` found
-      auto save_state = [&](float* dst, bool drain, bool observe) -> int64_t {
+      // `through`: the slot is read back on another XCD (retreat arm): stores
+      // written through (CPOL_SC1), published without an L2 write-back.
+      auto save_state = [&](float* dst, bool drain, bool observe, bool through) -> int64_t {
         // the slot of the most recently issued stage
         const int newest = POLL == APK_POLL_ISSUE ? (slot + E::NS - 1) % E::NS : next_slot<E>(slot);
         uint4 before = {0, 0, 0, 0};
@@ -521,8 +523,14 @@ k_persistent_yield(const apk_yield_params) {
           lds_sync();
         }
         const int64_t t0 = wall_ticks();
-        if (P().resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, dst, slot, live);
-        if (P().resume != APK_RESUME_RESTART) Ckpt<E>::save_acc(acc, dst);
+        if (through) {
+          if (P().resume == APK_RESUME_CKPT_FULL)
+            Ckpt<E>::template save_ring<CPOL_SC1>(ring, dst, slot, live);
+          if (P().resume != APK_RESUME_RESTART) Ckpt<E>::template save_acc<CPOL_SC1>(acc, dst);
+        } else {
+          if (P().resume == APK_RESUME_CKPT_FULL) Ckpt<E>::save_ring(ring, dst, slot, live);
+          if (P().resume != APK_RESUME_RESTART) Ckpt<E>::save_acc(acc, dst);
+        }
         if (observe) {
           wait_vmcnt<0>();  // every load landed, every checkpoint store done
           lds_sync();
@@ -579,7 +587,7 @@ k_persistent_yield(const apk_yield_params) {
         if (tk == RQ_NONE) continue;  // quota taken (or queue full): keep working
         float* dst = P().rq_slots + (size_t)(tk % P().rq_capacity) * Ckpt<E>::SLOT_FLOATS;
         // always drain: nothing may land in LDS after the block exits
-        const int64_t tSave = save_state(dst, true, false);
+        const int64_t tSave = save_state(dst, true, false, true);
         const int rkind = P().resume == APK_RESUME_RESTART ? 0
                           : P().resume == APK_RESUME_CKPT_FULL ? 2 : 1;
         // Every thread's checkpoint stores have completed at this XCD's L2;
@@ -610,7 +618,7 @@ k_persistent_yield(const apk_yield_params) {
           // Window-forcing order (src/midyield.cu:246-258): checkpoint right
           // after the flag read, before any further wait or atomic, then pop.
           // A block that gets no urgent tile goes on with its state intact.
-          tSave = save_state(ckslot(), drain, true);
+          tSave = save_state(ckslot(), drain, true, false);
           uidx = U > 0 ? pop_urgent(ev) : U;
           if (uidx >= U) {
             // No urgent tile: resume from the checkpoint just taken all the
@@ -629,7 +637,7 @@ k_persistent_yield(const apk_yield_params) {
         } else {
           uidx = U > 0 ? pop_urgent(ev) : U;
           if (uidx >= U) continue;
-          tSave = save_state(ckslot(), drain, true);
+          tSave = save_state(ckslot(), drain, true, false);
         }
         lds_sync();  // ring reads (checkpoint) done before the urgent tiles overwrite it
         if (tid == 0) {

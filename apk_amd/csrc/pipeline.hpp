@@ -33,6 +33,12 @@ struct DevPlat {
   static __device__ __forceinline__ void release() {
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   }
+  // The resume ring's payload (checkpoint slot, entry fields) is written
+  // through with agent-coherent stores (CPOL_SC1 / relaxed agent atomics),
+  // so publishing it needs only those stores to have completed: no L2
+  // write-back, which with every worker retreating at once serialised 32
+  // whole-L2 write-backs per XCD.
+  static __device__ __forceinline__ void publish_fence() { wait_vmcnt<0>(); }
   static __device__ __forceinline__ void acquire() {
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
   }
@@ -249,6 +255,9 @@ struct Ckpt {
   // accumulator read (or every load) to the top, which needs 4 VGPRs per
   // float4 at once -- all 256 VGPRs for the bf16 tile -- and spills.
   static constexpr int NJ = E::ACC_PER_THREAD / 4, GROUP = NJ < 8 ? NJ : 8;
+  // CPOL_SC1 for a checkpoint another XCD reads back (the retreat arm's
+  // resume slots): written through, published without an L2 write-back.
+  template <int CPOL = 0>
   static __device__ __forceinline__ void save_acc(const typename E::Acc& a, float* slot) {
     const buf_rsrc r = make_buf_rsrc(slot, ACC_FLOATS * 4);
     const int vo = (int)threadIdx.x * 16;
@@ -259,7 +268,7 @@ struct Ckpt {
       for (int j = j0; j < j0 + GROUP; ++j) {
         const float4 v = {E::get(a, 4 * j), E::get(a, 4 * j + 1), E::get(a, 4 * j + 2),
                           E::get(a, 4 * j + 3)};
-        buf_store_f4(v, r, vo, j * E::THREADS * 16);
+        buf_store_f4<CPOL>(v, r, vo, j * E::THREADS * 16);
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -291,13 +300,14 @@ struct Ckpt {
   // checkpoint positions 0, 1, ...
   // save_ring copies the newest stage (position n-1) first: without a drain
   // it is the one whose loads may still be landing.
+  template <int CPOL = 0>
   static __device__ __forceinline__ void save_ring(const char* ring, float* slot,
                                                    int first, int n) {
-    char* dst = (char*)(slot + ACC_FLOATS);
+    const buf_rsrc r = make_buf_rsrc(slot + ACC_FLOATS, RING_FLOATS * 4);
     for (int k = n - 1; k >= 0; --k) {
       const int b = (first + k) % E::NS;
       for (int i = threadIdx.x * 16; i < E::STAGE; i += E::THREADS * 16)
-        *(float4*)(dst + k * E::STAGE + i) = *(const float4*)(ring + b * E::STAGE + i);
+        buf_store_f4<CPOL>(*(const float4*)(ring + b * E::STAGE + i), r, i, k * E::STAGE);
     }
   }
   static __device__ __forceinline__ void load_ring(char* ring, const float* slot,

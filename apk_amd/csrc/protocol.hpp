@@ -17,6 +17,10 @@
 //   unsigned load(const unsigned*), int load(const int*)   relaxed
 //   void store(int*, int)                     relaxed
 //   void release(), acquire()                 device-wide fences
+//   void publish_fence()                      orders the caller's earlier
+//                                             payload stores (written by the
+//                                             platform's publishing stores)
+//                                             before its next store
 //   int64_t ticks()                           constant-rate clock (100 MHz)
 //   void pause()                              back off while spinning
 #pragma once
@@ -130,16 +134,17 @@ APK_PROTO_FN unsigned rq_pop(unsigned* ctl) {
   }
 }
 // Once the checkpoint stores of the whole block are complete: the entry's
-// fields, a device-wide release (on gfx950 it writes back this XCD's L2,
-// which holds every thread's checkpoint stores, so one release by one thread
-// covers the block), then seq = ticket + 1.
+// fields, the publish fence, then seq = ticket + 1. On gfx950 the slot is
+// written through with agent-coherent stores by every thread, each of which
+// waits for its stores before the barrier that precedes this call, so the
+// fence only orders this thread's field stores before the seq store.
 template <class P>
 APK_PROTO_FN void rq_publish(int* en, unsigned ticket, int task, int stage, int kind,
                              int domain) {
-  en[0] = task;
-  en[1] = stage;
-  en[3] = (kind << 8) | domain;  // domain: where the retreat freed a CU (xcd * 4 + se)
-  P::release();
+  P::store(&en[0], task);
+  P::store(&en[1], stage);
+  P::store(&en[3], (kind << 8) | domain);  // domain: where the retreat freed a CU
+  P::publish_fence();
   P::store(&en[2], (int)(ticket + 1));
 }
 // Waits (bounded) for claimed ticket h to be published; returns its kind + 1,
@@ -156,11 +161,11 @@ APK_PROTO_FN int rq_wait_ready(const int* en, unsigned h, int64_t wait = RQ_WAIT
     P::pause();
   }
 }
-// Once every reader of ticket h's checkpoint is done: frees the entry for
-// ticket h + cap.
+// Once every reader of ticket h's checkpoint is done (their loads complete):
+// frees the entry for ticket h + cap.
 template <class P>
 APK_PROTO_FN void rq_release(int* en, unsigned h, unsigned cap) {
-  P::release();
+  P::publish_fence();
   P::store(&en[2], (int)(h + cap));
 }
 

@@ -474,11 +474,22 @@ int main(int argc, char** argv) {
       errors += st[APK_ST_ERRORS];
       saveTicks += st[APK_ST_SAVE];
     }
+    // The background alone again, now that the engine clock has settled
+    // under the job (the drain estimate before it started from a cold clock
+    // and overstates the task time): the reference for the overhead and the
+    // tile time.
+    rig.reset(false);
+    rig.resetRetreat();
+    launch_bg();
+    HIP_CHECK(hipStreamSynchronize(bgStream));
+    HIP_CHECK(hipGetLastError());
+    const auto [as0, ae0] = rig.readRunGT();
+    const double usPerTaskWarm = (ae0 - as0) * tickUs / bgTasks;
     const double jobUs = (jobEnd - jobStart) * tickUs;
     const double flopTask = 2.0 * geo.tile_m * geo.tile_n * (double)K;
     const double tfJob = flopTask * jobTasks / (jobUs * 1e-6) / 1e12;
-    const double tfAlone = flopTask / (usPerTask * 1e-6) / 1e12;
-    const double tileUs = usPerTask * blocks / (K / kChunk);
+    const double tfAlone = flopTask / (usPerTaskWarm * 1e-6) / 1e12;
+    const double tileUs = usPerTaskWarm * blocks / (K / kChunk);
     printf("\n--- continuous retreat arm: %zu arrivals within the job (%d after it ended, %d "
            "not run), poll %s every %d, %d retreats per arrival, resume %s ---\n",
            raise.size(), afterJob, notRun, pollS.c_str(), pollEvery, retreatBlocks,
@@ -499,7 +510,7 @@ int main(int argc, char** argv) {
              percentile(cont, 0.5), percentile(cont, 0.99));
     printf("tile (k-chunk) time at full residency: %.2f us -> p50 latency = %.3f tiles\n",
            tileUs, raise.empty() ? -1.0 : percentile(raise, 0.5) / tileUs);
-    printf("background: %.2f TFLOP/s over the job with arrivals vs %.2f alone -> retreat "
+    printf("background: %.2f TFLOP/s over the job with arrivals vs %.2f alone (after it) -> retreat "
            "overhead %.2f%%\n", tfJob, tfAlone, (tfAlone / tfJob - 1.0) * 100.0);
     printf("retreats %llu | resumed %llu | save %.2f us per retreat | arrivals without a "
            "retreat %d | late drains %d | resume errors %llu | lost %u\n", retreats, resumed,

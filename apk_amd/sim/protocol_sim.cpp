@@ -61,6 +61,8 @@ struct HostPlat {
   static void store(int* p, int v) { __atomic_store_n(p, v, __ATOMIC_RELAXED); }
   static void release() { __atomic_thread_fence(__ATOMIC_RELEASE); }
   static void acquire() { __atomic_thread_fence(__ATOMIC_ACQUIRE); }
+  // host payload stores are plain: publishing them takes a release fence
+  static void publish_fence() { __atomic_thread_fence(__ATOMIC_RELEASE); }
   static int64_t ticks() {  // 100 MHz, as the device wall clock
     return std::chrono::duration_cast<std::chrono::nanoseconds>(
                std::chrono::steady_clock::now().time_since_epoch()).count() / 10;
