@@ -55,6 +55,7 @@ k_persistent_yield(const apk_yield_params) {
   __shared__ unsigned long long s_stats[APK_STATS_PER_BLOCK];
   __shared__ long long s_setter[2];  // next event, time base
   __shared__ long long s_serve_t1;   // start of the current service's urgent work
+  __shared__ int s_fsync;            // synchronous flag read (syncPoll)
 
   const int tid = threadIdx.x, bid = blockIdx.x;
   // Values the stage loop does not need are recomputed from the parameters
@@ -86,6 +87,12 @@ k_persistent_yield(const apk_yield_params) {
       make_rsrc((const char*)P().flag + (size_t)(bid % copies()) * APK_FLAG_STRIDE, 4);
   const bool isSetter = P().flag_set != nullptr && P().sched != nullptr && bid == 0;
   constexpr bool retreatArm = RETREAT && POLL != APK_POLL_OFF;
+  // A retreat-arm continuation is the set of blocks that retreats, all of
+  // it, at the next generation: it polls the flag synchronously (stage polls
+  // of one-barrier-per-stage engines), to act a stage sooner.
+  const bool syncPoll = retreatArm && !SYS && E::GROUP == 1 && POLL == APK_POLL_STAGE &&
+                        P().continuation != 0 && P().launch_epoch > 0;
+  const int* myFlag = (const int*)((const char*)P().flag + (size_t)(bid % copies()) * APK_FLAG_STRIDE);
 
   const uint32_t wl = wave_lds(ring);
   const uint32_t flag_lds = lds_addr_of(flagring);
@@ -394,7 +401,15 @@ k_persistent_yield(const apk_yield_params) {
           }
           if (POLL != APK_POLL_OFF && s == nextSite) {
             if (s != siteDone) {
-              const int f = uniform(flagring[site_flag(slot)]);
+              int f = uniform(flagring[site_flag(slot)]);
+              if (syncPoll) {
+                // The blocks that retreat at the next generation read the
+                // flag itself at the site (one load and one barrier) instead
+                // of the sample issued a stage earlier.
+                if (tid == 0) s_fsync = flag_load(myFlag);
+                lds_sync();
+                f = uniform(s_fsync);
+              }
               fLatest = f;
               if (f != lastSeen || isSetter) {
                 fSeen = f;

@@ -478,13 +478,17 @@ int main(int argc, char** argv) {
     // under the job (the drain estimate before it started from a cold clock
     // and overstates the task time): the reference for the overhead and the
     // tile time.
+    // 64 tasks per worker, so that the drain's tail (the last tasks run on
+    // fewer workers) weighs as little as it does in the job.
+    const unsigned aloneTasks = std::min(jobTasks, (unsigned)std::max(bgTasks, 64 * blocks));
     rig.reset(false);
     rig.resetRetreat();
-    launch_bg();
+    rig.launchRetreat(poll, pollEvery, resume, aloneTasks, retreatN, 1, false, blocks, 0, false,
+                      rig.dRunGT(), rig.dExitCount(), bgStream);
     HIP_CHECK(hipStreamSynchronize(bgStream));
     HIP_CHECK(hipGetLastError());
     const auto [as0, ae0] = rig.readRunGT();
-    const double usPerTaskWarm = (ae0 - as0) * tickUs / bgTasks;
+    const double usPerTaskWarm = (ae0 - as0) * tickUs / aloneTasks;
     const double jobUs = (jobEnd - jobStart) * tickUs;
     const double flopTask = 2.0 * geo.tile_m * geo.tile_n * (double)K;
     const double tfJob = flopTask * jobTasks / (jobUs * 1e-6) / 1e12;
