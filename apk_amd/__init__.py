@@ -108,6 +108,7 @@ _SIGNATURES = {
     "apk_persistent_gemm_occupancy": (_I, [_I, ctypes.POINTER(_I)]),
     "apk_persistent_gemm": (_I, [_I, _P, _P, _P, _I, _I, _I, _I, _P, _P, _I, _P]),
     "apk_persistent_gemm_noalloc": (_I, [_I, _P, _P, _P, _I, _I, _I, _I, _P, _I, _P]),
+    "apk_urgent_gemm": (_I, [_I, _P, _P, _P, _I, _I, _I, _P, _P, _P]),
     "apk_persistent_yield": (_I, [_I, _I, _I, ctypes.POINTER(YieldParams), _I, _P]),
     "apk_yield_ckpt_floats": (ctypes.c_longlong, [_I]),
     "apk_persistent_yield_occupancy": (_I, [_I, _I, ctypes.POINTER(_I)]),
@@ -180,6 +181,13 @@ def persistent_gemm_noalloc(engine, A, B, C, M, N, K, k_chunk, log, blocks, stre
     device array; no allocation). Asynchronous."""
     check(load().apk_persistent_gemm_noalloc(engine, A, B, C, M, N, K, k_chunk, log,
                                              blocks, stream))
+
+
+def urgent_gemm(engine, A, B, C, M, N, K, start_gt=None, end_gt=None, stream=0):
+    """Launch apk_urgent_gemm: one block per tile, no queue; optional device
+    pointers receive the start (block 0's first instruction) and end ticks.
+    Asynchronous."""
+    check(load().apk_urgent_gemm(engine, A, B, C, M, N, K, start_gt, end_gt, stream))
 
 
 def yield_occupancy(engine, poll):

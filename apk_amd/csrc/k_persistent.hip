@@ -83,6 +83,33 @@ __global__ void __launch_bounds__(E::THREADS) __attribute__((amdgpu_waves_per_eu
   }
 }
 
+// The urgent job as the reference runs it (urgent_tile, src/urgent_baseline.cu:
+// 100-112): one block per output tile, block b computing tile b over the
+// whole K, no queue; block 0 stamps the job's start at its first
+// instruction and every block raises the job's end once its tile is stored.
+template <class E>
+__global__ void __launch_bounds__(E::THREADS) __attribute__((amdgpu_waves_per_eu(E::MIN_WAVES_PER_SIMD, E::WAVES_PER_SIMD)))
+    k_urgent_tiles(const void* __restrict__ A, const void* __restrict__ B,
+                   float* __restrict__ C, int M, int N, int K, long long* start_gt,
+                   unsigned long long* end_gt) {
+  if (start_gt && blockIdx.x == 0 && threadIdx.x == 0) *start_gt = (long long)wall_ticks();
+  __shared__ __attribute__((aligned(16))) char ring[E::LDS_BYTES];
+  const int tilesN = N / E::TN;
+  const int row0 = (int)(blockIdx.x / (unsigned)tilesN) * E::TM;
+  const int col0 = (int)(blockIdx.x % (unsigned)tilesN) * E::TN;
+  const typename E::Ctx ctx = E::make_ctx(A, B, M, N, K);
+  typename E::Acc acc;
+  E::zero(acc);
+  run_stages<E>(ring, wave_lds(ring), ctx, acc, row0, col0, K / E::KS, [](int) {});
+  store_tile<E>(acc, ring, C, N, row0, col0, false);
+  if (end_gt) {
+    wait_vmcnt<0>();  // this thread's C stores have completed
+    lds_sync();       // ... and every other thread's
+    if (threadIdx.x == 0)
+      atomic_max_u64(end_gt, (unsigned long long)wall_ticks());
+  }
+}
+
 template <class E>
 static int validate_persistent_gemm(const void* A, const void* B, float* C, int M, int N, int K,
                                     int kChunk, int blocks) {
@@ -147,6 +174,19 @@ static int scratch_of_current_device(unsigned** out) {
     g_scratch[dev] = (unsigned*)p;
   }
   *out = g_scratch[dev];
+  return APK_OK;
+}
+
+template <class E>
+static int launch_urgent_tiles(const void* A, const void* B, float* C, int M, int N, int K,
+                               long long* start_gt, unsigned long long* end_gt,
+                               hipStream_t st) {
+  const int rc = validate_persistent_gemm<E>(A, B, C, M, N, K, K, 1);
+  if (rc != APK_OK) return rc;
+  const int tiles = (M / E::TM) * (N / E::TN);
+  hipLaunchKernelGGL(k_urgent_tiles<E>, dim3(tiles), dim3(E::THREADS), 0, st, A, B, C, M, N, K,
+                     start_gt, end_gt);
+  APK_LAUNCHED();
   return APK_OK;
 }
 
@@ -233,4 +273,23 @@ extern "C" int apk_persistent_gemm_noalloc(int engine, const void* A, const void
                      (int)APK_QUEUE_WORDS);
   APK_LAUNCHED();
   return apk_persistent_gemm(engine, A, B, C, M, N, K, k_chunk, q, log, blocks, stream);
+}
+
+extern "C" int apk_urgent_gemm(int engine, const void* A, const void* B, float* C, int M, int N,
+                               int K, long long* start_gt, unsigned long long* end_gt,
+                               void* stream) {
+  using namespace apk;
+  switch (engine) {
+    case APK_ENGINE_VALU64:
+      return launch_urgent_tiles<EngValu64>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));
+    case APK_ENGINE_MFMA128:
+      return launch_urgent_tiles<EngMfma128>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));
+    case APK_ENGINE_BF16X256:
+      return launch_urgent_tiles<EngBf16x256>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));
+    case APK_ENGINE_BF16X128:
+      return launch_urgent_tiles<EngBf16x128>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));
+    default:
+      set_error("urgent_gemm: unknown engine %d", engine);
+      return APK_EINVAL;
+  }
 }

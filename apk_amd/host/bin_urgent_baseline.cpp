@@ -313,8 +313,10 @@ int main(int argc, char** argv) {
     // host raises each of `events` arrivals (exponential gaps, --mean-gap-us)
     // as it falls due: [raise flag -> urgent GEMM] on the urgent stream, then
     // the continuation that brings the retreated workers back on a third
-    // stream ordered after the urgent GEMM. The urgent GEMM is launched with
-    // apk_persistent_gemm_noalloc (no per-arrival counter buffer or memset).
+    // stream ordered after the urgent GEMM. The urgent GEMM is the reference's
+    // urgent_tile (apk_urgent_gemm: one block per tile, no queue to clear),
+    // whose start is stamped at block 0's first instruction as the
+    // reference stamps it (src/urgent_baseline.cu:104).
     const int T = tilesM * tilesN;
     const std::vector<unsigned long long> tileHash = [&] {
       rig.reserveTasks((unsigned)T, 0);
@@ -346,15 +348,18 @@ int main(int argc, char** argv) {
     float* dCuAll;
     long long* dRunC;
     unsigned* dExitC;
-    apk_tile_record* dULogAll;
+    long long* dUStartAll;           // per arrival: urgent block 0's first instruction
+    unsigned long long* dUEndAll;    // per arrival: the last urgent tile stored
     HIP_CHECK(hipMalloc(&dCuAll, (size_t)(keepCu + 1) * urgentM * urgentN * 4));
     HIP_CHECK(hipMalloc(&dRunC, 2 * (size_t)events * sizeof(long long)));
     HIP_CHECK(hipMalloc(&dExitC, (size_t)events * sizeof(unsigned)));
-    HIP_CHECK(hipMalloc(&dULogAll, (size_t)events * uTiles * sizeof(apk_tile_record)));
+    HIP_CHECK(hipMalloc(&dUStartAll, (size_t)events * sizeof(long long)));
+    HIP_CHECK(hipMalloc(&dUEndAll, (size_t)events * sizeof(unsigned long long)));
     HIP_CHECK(hipMemset(dCuAll, 0xFF, (size_t)(keepCu + 1) * urgentM * urgentN * 4));
     HIP_CHECK(hipMemset(dRunC, 0, 2 * (size_t)events * sizeof(long long)));
     HIP_CHECK(hipMemset(dExitC, 0, (size_t)events * sizeof(unsigned)));
-    HIP_CHECK(hipMemset(dULogAll, 0, (size_t)events * uTiles * sizeof(apk_tile_record)));
+    HIP_CHECK(hipMemset(dUStartAll, 0, (size_t)events * sizeof(long long)));
+    HIP_CHECK(hipMemset(dUEndAll, 0, (size_t)events * sizeof(unsigned long long)));
     hipStream_t cStream;
     HIP_CHECK(hipStreamCreateWithFlags(&cStream, hipStreamNonBlocking));
     hipEvent_t evU;
@@ -373,9 +378,10 @@ int main(int argc, char** argv) {
       spin_until_ns(t0 + gaps[e]);
       float* cu = dCuAll + (size_t)std::min(e, keepCu) * urgentM * urgentN;
       APK_CHECK(apk_raise_flag(rig.dFlag(), 1, e + 1, rig.dSetGT() + e, uStream));
-      APK_CHECK(apk_persistent_gemm_noalloc(engine, dAu, dBu, cu, urgentM, urgentN, urgentK,
-                                            urgentK, dULogAll + (size_t)e * uTiles,
-                                            urgentBlocks, uStream));
+      // the reference's urgent_tile: one block per tile, start stamped at
+      // block 0's first instruction (src/urgent_baseline.cu:100-112)
+      APK_CHECK(apk_urgent_gemm(engine, dAu, dBu, cu, urgentM, urgentN, urgentK,
+                                dUStartAll + e, dUEndAll + e, uStream));
       HIP_CHECK(hipEventRecord(evU, uStream));
       HIP_CHECK(hipStreamWaitEvent(cStream, evU, 0));
       rig.launchRetreat(poll, pollEvery, resume, jobTasks, retreatN, events, oracle,
@@ -402,8 +408,11 @@ int main(int argc, char** argv) {
     HIP_CHECK(hipMemcpy(runC.data(), dRunC, runC.size() * 8, hipMemcpyDeviceToHost));
     long long jobEnd = bgEnd;
     for (int e = 0; e < events; ++e) jobEnd = std::max(jobEnd, runC[2 * (size_t)e + 1]);
-    std::vector<apk_tile_record> ulog((size_t)events * uTiles);
-    HIP_CHECK(hipMemcpy(ulog.data(), dULogAll, ulog.size() * sizeof(apk_tile_record),
+    std::vector<long long> uStart(events);
+    std::vector<unsigned long long> uEnd(events);
+    HIP_CHECK(hipMemcpy(uStart.data(), dUStartAll, events * sizeof(long long),
+                        hipMemcpyDeviceToHost));
+    HIP_CHECK(hipMemcpy(uEnd.data(), dUEndAll, events * sizeof(unsigned long long),
                         hipMemcpyDeviceToHost));
     std::vector<double> raise, uend, rfirst, rlast, cont;
     int afterJob = 0, noRetreat = 0, notRun = 0;
@@ -413,11 +422,7 @@ int main(int argc, char** argv) {
                    "retreat_last_us,retreats,cont_start_us,in_job\n");
     for (int e = 0; e < events; ++e) {
       const long long set = rr.setGT[e];
-      long long us = INT64_MAX, ue = 0;
-      for (int u = 0; u < uTiles; ++u) {
-        us = std::min<long long>(us, ulog[(size_t)e * uTiles + u].start);
-        ue = std::max<long long>(ue, ulog[(size_t)e * uTiles + u].end);
-      }
+      const long long us = uStart[e], ue = (long long)uEnd[e];
       if (set == 0 || ue == 0) {
         ++notRun;
         continue;
@@ -478,9 +483,10 @@ int main(int argc, char** argv) {
     // under the job (the drain estimate before it started from a cold clock
     // and overstates the task time): the reference for the overhead and the
     // tile time.
-    // 64 tasks per worker, so that the drain's tail (the last tasks run on
-    // fewer workers) weighs as little as it does in the job.
-    const unsigned aloneTasks = std::min(jobTasks, (unsigned)std::max(bgTasks, 64 * blocks));
+    // A sixteenth of the job (over a second of work), so that the launch and
+    // the drain's tail (the last tasks run on fewer workers) weigh as little
+    // as they do in the job.
+    const unsigned aloneTasks = std::min(jobTasks, std::max((unsigned)bgTasks, jobTasks / 16));
     rig.reset(false);
     rig.resetRetreat();
     rig.launchRetreat(poll, pollEvery, resume, aloneTasks, retreatN, 1, false, blocks, 0, false,

@@ -112,6 +112,18 @@ int apk_persistent_gemm(int engine, const void* A, const void* B, float* C,
                         unsigned int* next_task, apk_tile_record* log,
                         int blocks, void* stream);
 
+/* urgent_tile (src/urgent_baseline.cu:100-112): the urgent job as one block
+ * per output tile, block b computing tile b (row-major tile order) over the
+ * whole K, with no work queue (nothing to clear, nothing allocated). Same
+ * operands, layouts and per-element k order as apk_persistent_gemm, so C is
+ * bit-identical to it. Optional outputs (device memory, may be NULL):
+ * *start_gt = wall-clock ticks at block 0's first instruction (the
+ * reference's uStartGT); *end_gt raised (atomic max, unsigned) to the time
+ * each block's tile is stored (the reference's uEndGT; the caller zeroes
+ * it). Requires M % tile_m == 0, N % tile_n == 0, K % k_stage == 0. */
+int apk_urgent_gemm(int engine, const void* A, const void* B, float* C, int M, int N, int K,
+                    long long* start_gt, unsigned long long* end_gt, void* stream);
+
 /* Allocation-free variant of apk_persistent_gemm. No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops). Same arguments and results as
