@@ -8,9 +8,11 @@ mode, which needs root; without it the engine clock follows power from one
 dispatch to the next. This script does not change any GPU setting: it runs
 a load (by default the persistent fp32 MFMA GEMM at 8192^3 for a few
 seconds, whose last pass also prints the clock read on the device by
-apk_clock_probe) and samples `rocm-smi --showclocks` every --interval
-seconds meanwhile, then prints each sample and the min / median / max of
-the engine clock (sclk) seen while the load ran.
+apk_clock_probe) and samples `rocm-smi --showclocks --showpower` every
+--interval seconds meanwhile, then prints each sample and the min / median
+/ max of the engine clock (sclk) and of the package power seen while the
+load ran, beside the power cap (`--showmaxpower`): a clock that sags while
+the power sits at the cap is power-bound.
 
     python -m apk_amd.analysis.clock_readback --seconds 10 --csv clock.csv
     python -m apk_amd.analysis.clock_readback -- apk_amd/bin/tcyield --mode calibrate ...
@@ -35,10 +37,23 @@ BIN_DIR = os.path.join(os.path.dirname(_HERE), "bin")
 _CLOCK_LINE = re.compile(r"GPU\[(\d+)\][^:]*:\s*(\w+)\b.*?\(?\s*(\d+(?:\.\d+)?)\s*M[Hh]z\)?")
 
 
+# "GPU[0]          : Current Socket Graphics Package Power (W): 845.0",
+# "... Average Graphics Package Power (W): 845.0", "... Max Graphics Package
+# Power (W): 1400.0".
+_POWER_LINE = re.compile(r"GPU\[(\d+)\][^:]*:\s*(.*?Power)\s*\(W\):\s*(\d+(?:\.\d+)?)")
+
+
 def parse_rocm_smi(text):
-    """{(gpu, clock name): MHz} from `rocm-smi --showclocks` text."""
+    """{(gpu, clock name): MHz} from `rocm-smi --showclocks` text, plus
+    {(gpu, "power_w"): W} for a current or average package power line and
+    {(gpu, "power_cap_w"): W} for a maximum one."""
     out = {}
     for line in text.splitlines():
+        m = _POWER_LINE.search(line)
+        if m:
+            key = "power_cap_w" if "max" in m.group(2).lower() else "power_w"
+            out[(int(m.group(1)), key)] = float(m.group(3))
+            continue
         m = _CLOCK_LINE.search(line)
         if m:
             out[(int(m.group(1)), m.group(2).lower())] = float(m.group(3))
@@ -54,8 +69,8 @@ def default_load(seconds):
             "--verify", "0", "--csv", "/dev/null"]
 
 
-def sample(smi):
-    r = subprocess.run([smi, "--showclocks"], capture_output=True, text=True, timeout=30)
+def sample(smi, what=("--showclocks", "--showpower")):
+    r = subprocess.run([smi, *what], capture_output=True, text=True, timeout=30)
     return r.returncode, parse_rocm_smi(r.stdout), r.stdout + r.stderr
 
 
@@ -81,6 +96,8 @@ def main(argv=None):
     if rc != 0:
         print(f"rocm-smi exited {rc}: read-back denied on this host", file=sys.stderr)
         return 2
+    _, cap, _ = sample(smi, ("--showmaxpower",))
+    cap_w = cap.get((a.gpu, "power_cap_w"))
 
     cmd = a.load or default_load(a.seconds)
     limit = a.max_seconds if a.max_seconds > 0 else 3 * a.seconds + 30
@@ -102,7 +119,7 @@ def main(argv=None):
             if rc == 0 and clocks:
                 rows.append((t, clocks))
                 print(f"t={t:6.2f} s  " + "  ".join(
-                    f"{name}={mhz:.0f}" for (g, name), mhz in sorted(clocks.items())
+                    f"{name}={v:.0f}" for (g, name), v in sorted(clocks.items())
                     if g == a.gpu), flush=True)
             if t > limit:
                 stopped = True
@@ -132,7 +149,8 @@ def main(argv=None):
     if a.csv:
         names = sorted({k[1] for _, c in rows for k in c if k[0] == a.gpu})
         with open(a.csv, "w") as f:
-            f.write("t_s," + ",".join(f"{n}_mhz" for n in names) + "\n")
+            f.write("t_s," + ",".join(n if n.startswith("power") else f"{n}_mhz"
+                                      for n in names) + "\n")
             for t, c in rows:
                 f.write(f"{t:.3f}," + ",".join(
                     f"{c[(a.gpu, n)]:.0f}" if (a.gpu, n) in c else "" for n in names) + "\n")
@@ -142,6 +160,11 @@ def main(argv=None):
     print(f"sclk under load ({len(sclk)} samples): min {min(sclk):.0f} | median "
           f"{pct(sclk, 0.5):.0f} | max {max(sclk):.0f} MHz (not locked: determinism "
           f"mode needs root)")
+    watts = [c[(a.gpu, "power_w")] for _, c in rows if (a.gpu, "power_w") in c]
+    if watts:
+        print(f"package power under load ({len(watts)} samples): min {min(watts):.0f} | "
+              f"median {pct(watts, 0.5):.0f} | max {max(watts):.0f} W | cap "
+              + (f"{cap_w:.0f} W" if cap_w else "not reported"))
     return 0
 
 

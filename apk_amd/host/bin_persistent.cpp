@@ -1,4 +1,4 @@
-// persistent -- tile calibration of the persistent fp32 GEMM on MI355X.
+// persistent -- tile calibration of the persistent GEMM on MI355X.
 //
 // Measurement surface of the reference's bin/persistent (src/persistent.cu:
 // 96-264): same flags and defaults (--k 128 --tiles-m 48 --tiles-n 48
@@ -6,8 +6,12 @@
 // results/raw/phase1_tiles.csv), same stdout lines and the same per-task CSV
 // schema "task,block,smid,start_cyc,end_cyc,dur_cyc,dur_us" (extra columns
 // tile,chunk appended). Additions:
-//   --engine valu64|mfma128   tile engine (valu64 = the reference's 64x64
-//                             fmaf tile; mfma128 = 128x128 on fp32 MFMA)
+//   --engine valu64|mfma128|bf16x256|bf16x128
+//                             tile engine (valu64 = the reference's 64x64
+//                             fmaf tile; mfma128 = 128x128 on fp32 MFMA;
+//                             bf16x256 / bf16x128 = bf16 MFMA tiles on the
+//                             reference's tcyield data, normal(0,1) rounded
+//                             to bf16, B passed transposed)
 //   --gemm-k K                full GEMM depth, walked in --k wide chunks
 //                             (default = --k: one chunk per tile, as the
 //                             reference); records are per (tile, chunk)
@@ -47,8 +51,11 @@ int main(int argc, char** argv) {
   int engine = -1;
   if (engName == "valu64") engine = APK_ENGINE_VALU64;
   else if (engName == "mfma128") engine = APK_ENGINE_MFMA128;
+  else if (engName == "bf16x256") engine = APK_ENGINE_BF16X256;
+  else if (engName == "bf16x128") engine = APK_ENGINE_BF16X128;
   if (engine < 0) {
-    fprintf(stderr, "unknown --engine %s (valu64|mfma128)\n", engName.c_str());
+    fprintf(stderr, "unknown --engine %s (valu64|mfma128|bf16x256|bf16x128)\n",
+            engName.c_str());
     return 1;
   }
   apk_engine_geometry geo;
@@ -84,19 +91,35 @@ int main(int argc, char** argv) {
          seed == 0 ? " (glibc: srand(0) == srand(1))" : "");
   printf("clock for us conversion: %.0f MHz (device wall clock ticks)\n", clkMHz);
 
+  // hA/hB: the values the float64 check multiplies (B as K x N); devA/devB:
+  // the bytes the kernel reads (bf16 bit patterns, B transposed to N x K,
+  // for the bf16 engines).
+  const bool bf16 = geo.elem_bytes == 2;
+  const double peakTF = bf16 ? kPeakBf16TF : kPeakFp32TF;
   std::vector<float> hA((size_t)M * K), hB((size_t)K * N);
-  fill_uniform_pm1(seed, hA, hB);
+  std::vector<uint8_t> devA, devB;
+  if (bf16) {
+    std::vector<uint16_t> a, b;
+    fill_normal_bf16(seed, hA, a, hB, b);
+    devA = as_bytes(a);
+    devB = as_bytes(transpose_u16(b, K, N));
+  } else {
+    fill_uniform_pm1(seed, hA, hB);
+    devA = as_bytes(hA);
+    devB = as_bytes(hB);
+  }
 
-  float *dA, *dB, *dC;
+  void *dA, *dB;
+  float* dC;
   unsigned* dNext;
   apk_tile_record* dLog;
-  HIP_CHECK(hipMalloc(&dA, hA.size() * sizeof(float)));
-  HIP_CHECK(hipMalloc(&dB, hB.size() * sizeof(float)));
+  HIP_CHECK(hipMalloc(&dA, devA.size()));
+  HIP_CHECK(hipMalloc(&dB, devB.size()));
   HIP_CHECK(hipMalloc(&dC, (size_t)M * N * sizeof(float)));
   HIP_CHECK(hipMalloc(&dNext, APK_QUEUE_WORDS * sizeof(unsigned)));
   HIP_CHECK(hipMalloc(&dLog, (size_t)numRecs * sizeof(apk_tile_record)));
-  HIP_CHECK(hipMemcpy(dA, hA.data(), hA.size() * sizeof(float), hipMemcpyHostToDevice));
-  HIP_CHECK(hipMemcpy(dB, hB.data(), hB.size() * sizeof(float), hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemcpy(dA, devA.data(), devA.size(), hipMemcpyHostToDevice));
+  HIP_CHECK(hipMemcpy(dB, devB.data(), devB.size(), hipMemcpyHostToDevice));
 
   hipEvent_t e0, e1;
   HIP_CHECK(hipEventCreate(&e0));
@@ -120,10 +143,10 @@ int main(int argc, char** argv) {
     HIP_CHECK(hipDeviceSynchronize());
     HIP_CHECK(hipGetLastError());
     HIP_CHECK(hipEventElapsedTime(&lastMs, e0, e1));
-    printf("pass %d: %.3f ms wall | %.1f GFLOP/s | %.2f TFLOP/s (%.1f%% of %.1f fp32 peak) "
+    printf("pass %d: %.3f ms wall | %.1f GFLOP/s | %.2f TFLOP/s (%.1f%% of %.1f %s peak) "
            "| %.0f tasks/s%s\n",
            p, lastMs, flopTotal / (lastMs * 1e6), tflops(flopTotal, lastMs * 1e-3),
-           100.0 * tflops(flopTotal, lastMs * 1e-3) / kPeakFp32TF, kPeakFp32TF,
+           100.0 * tflops(flopTotal, lastMs * 1e-3) / peakTF, peakTF, bf16 ? "bf16" : "fp32",
            numTasks / (lastMs * 1e-3), p + 1 < passes ? " (warmup)" : "");
   }
 

@@ -226,6 +226,16 @@ GPU[1]          : sclk clock level: 0: (132Mhz)
     assert clock_readback.parse_rocm_smi("no clocks here") == {}
 
 
+def test_parse_rocm_smi_power():
+    text = ("GPU[0]\t\t: Current Socket Graphics Package Power (W): 1198.0\n"
+            "GPU[1]\t\t: Average Graphics Package Power (W): 301.5\n"
+            "GPU[0]\t\t: Max Graphics Package Power (W): 1400.0\n"
+            "GPU[0]\t\t: sclk clock level: 1: (1905Mhz)\n")
+    c = clock_readback.parse_rocm_smi(text)
+    assert c[(0, "power_w")] == 1198.0 and c[(1, "power_w")] == 301.5
+    assert c[(0, "power_cap_w")] == 1400.0 and c[(0, "sclk")] == 1905
+
+
 def test_default_load_is_a_built_binary_path():
     cmd = clock_readback.default_load(10.0)
     assert os.path.basename(cmd[0]) == "persistent"
@@ -238,7 +248,8 @@ def test_clock_readback_stops_its_load(tmp_path, capsys):
     terminated, and the samples taken meanwhile are still reported."""
     smi = tmp_path / "fake-smi"
     smi.write_text("#!/bin/sh\necho 'GPU[0]\t\t: sclk clock level: 1: (1405Mhz)'\n"
-                   "echo 'GPU[0]\t\t: mclk clock level: 0: (2000Mhz)'\n")
+                   "echo 'GPU[0]\t\t: mclk clock level: 0: (2000Mhz)'\n"
+                   "echo 'GPU[0]\t\t: Current Socket Graphics Package Power (W): 990.0'\n")
     smi.chmod(0o755)
     pidfile = tmp_path / "pid"
     load = [sys.executable, "-c",
@@ -258,6 +269,7 @@ def test_clock_readback_stops_its_load(tmp_path, capsys):
     out = capsys.readouterr()
     assert "load up" in out.out
     assert "sclk under load" in out.out and "median 1405" in out.out
+    assert "package power under load" in out.out and "median 990" in out.out
     assert "stopped at the 2 s limit" in out.err
     rows = csv.read_text().splitlines()
-    assert rows[0] == "t_s,mclk_mhz,sclk_mhz" and len(rows) > 3
+    assert rows[0] == "t_s,mclk_mhz,power_w,sclk_mhz" and len(rows) > 3

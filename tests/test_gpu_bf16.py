@@ -276,18 +276,29 @@ def test_bf16_odd_length_pairs_yield(bf16_odd_job, apk, resume):
     j = bf16_odd_job
     say(f"engine {j.eng} odd-length pairs, stage yields, resume={resume}")
     ref = j.run(apk.POLL_OFF, events=0)
-    r = j.run(apk.POLL_STAGE, resume=resume, use_oracle=True)
-    fired = int((r["set_gt"] != 0).sum())
-    assert fired == j.events and int(r["stats"][:, 0].sum()) >= fired
-    assert np.array_equal(r["C"].view(np.uint32), ref["C"].view(np.uint32))
-    assert oracle.rel_frobenius(r["C"], oracle.gemm_f64(j.A, j.B, threads=8)) <= 1e-5
     uref = run_bf16_urgent(j)
     assert oracle.rel_frobenius(uref, oracle.gemm_f64(j.Au, j.Bu, threads=8)) <= 1e-5
-    for e in range(j.events):
-        assert np.array_equal(r["Cu"][e].view(np.uint32), uref.view(np.uint32)), e
-    assert (r["exec"] == 1).all() and (r["u_exec"] == j.U).all()
-    # sites are the pair boundaries 0, 2, 4; site 4 is the pair with the zero stage
-    assert set(np.unique(r["site"]).tolist()) <= {0, 2, 4}
-    assert (r["site"] == 4).any()
-    say(f"  fired {fired} events at sites {np.bincount(r['site'], minlength=5).tolist()}, "
+    c64 = oracle.gemm_f64(j.A, j.B, threads=8)
+    # The setter (block 0) raises each event at its first poll site past the
+    # event's time, so the site an event lands on depends on how long the
+    # setter spends before each site; with the short 16-deep stages of the
+    # 128x128 tile, a job of 24 events can land none at site 4. Jobs are
+    # repeated, each checked in full, until an event has.
+    sites = np.zeros(5, dtype=np.int64)
+    for attempt in range(16):
+        r = j.run(apk.POLL_STAGE, resume=resume, use_oracle=True)
+        fired = int((r["set_gt"] != 0).sum())
+        assert fired == j.events and int(r["stats"][:, 0].sum()) >= fired
+        assert np.array_equal(r["C"].view(np.uint32), ref["C"].view(np.uint32))
+        assert oracle.rel_frobenius(r["C"], c64) <= 1e-5
+        for e in range(j.events):
+            assert np.array_equal(r["Cu"][e].view(np.uint32), uref.view(np.uint32)), e
+        assert (r["exec"] == 1).all() and (r["u_exec"] == j.U).all()
+        # sites are the pair boundaries 0, 2, 4; site 4 is the pair with the zero stage
+        assert set(np.unique(r["site"]).tolist()) <= {0, 2, 4}
+        sites += np.bincount(r["site"], minlength=5)
+        if sites[4] > 0:
+            break
+    assert sites[4] > 0
+    say(f"  {attempt + 1} job(s), {j.events} events each, at sites {sites.tolist()}, "
         "bit-identical, float64 within 1e-5")
