@@ -25,7 +25,12 @@ the reference's latency), the retreat arm (one background job; flag raised ->
 urgent GEMM starts on its own stream), the no-preemption baseline, the polling
 overhead (ABAB drains) and the tile time at full residency they are measured
 against -- and `bf16`: the cfg5 bf16 MFMA GEMM throughput (M=N=K=8192,
-256x256 tiles, no yields) with its engine clock.
+256x256 tiles, no yields) with its engine clock: right after the preemption
+runs (`tflops`, the poll-off preemptible kernel over two GEMMs), and
+sustained (one GEMM per launch after a pre-warm of the same launches), beside
+torch.matmul (hipBLASLt) on the same operands under the same conditions. The
+sustained bf16 clock is set by the load on the whole chip (`--bf16-sweep`
+times the GEMM on 64-256 workers).
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-preempt]
 """
@@ -225,6 +230,111 @@ def bf16_metrics():
             "us_per_tile": us}
 
 
+def timed_sustained(launch, flop, steps, prewarm_ms, wall_mhz, torch, apk_amd, stream):
+    """Per-launch time (HIP events on the launch stream) of `steps` launches
+    that follow `prewarm_ms` of untimed back-to-back launches, with the
+    engine clock read by apk_clock_probe on a side stream meanwhile. Returns
+    (TFLOP/s from the mean launch time, clock summary)."""
+    import numpy as np
+    t0 = time.perf_counter()
+    n = 0
+    while (time.perf_counter() - t0) * 1e3 < prewarm_ms:
+        for _ in range(20):
+            launch(n)
+            n += 1
+        stream.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    launch(n)
+    ev[0][0].record(stream)
+    launch(n + 1)
+    ev[0][1].record(stream)
+    stream.synchronize()
+    est_ms = ev[0][0].elapsed_time(ev[0][1])
+    probes = torch.zeros(32 * 4, dtype=torch.int64, device="cuda")
+    side = torch.cuda.Stream()
+    apk_amd.clock_probe(probes.data_ptr(), 32, 1, side.cuda_stream)
+    torch.cuda.synchronize()
+    window = max(1, int(0.6 * steps * est_ms * 1e3 * wall_mhz))
+    for i in range(steps):
+        ev[i][0].record(stream)
+        launch(n + 2 + i)
+        ev[i][1].record(stream)
+        if i == 0:
+            apk_amd.clock_probe(probes.data_ptr(), 32, window, side.cuda_stream)
+    stream.synchronize()
+    side.synchronize()
+    ms = float(np.mean([a.elapsed_time(b) for a, b in ev]))
+    return flop / (ms * 1e-3) / 1e12, clock_summary(probes.cpu().numpy(), wall_mhz)
+
+
+def bf16_sustained(workers_list, steps, prewarm_ms, vendor):
+    """The bf16x256 persistent GEMM (8192^3, one GEMM per launch, bf16
+    operands, fp32 accumulate) on each worker count of `workers_list`, and
+    with `vendor` torch.matmul (hipBLASLt) on the same operands, each timed
+    after a sustained pre-warm of the same launches with the engine clock
+    read beside it. Returns one dict per case."""
+    import torch
+    import apk_amd
+    apk_amd.load()
+    info = apk_amd.device_info()
+    wall_mhz = info.wall_clock_khz / 1e3
+    S = 8192
+    flop = 2.0 * S ** 3
+    gen = torch.Generator(device="cuda")
+    gen.manual_seed(5)
+    A = torch.randn((S, S), generator=gen, device="cuda").to(torch.bfloat16)
+    Bt = torch.randn((S, S), generator=gen, device="cuda").to(torch.bfloat16)
+    C = torch.empty((S, S), device="cuda", dtype=torch.float32)
+    stream = torch.cuda.current_stream()
+    eng = apk_amd.ENGINE_BF16X256
+    ring = 8192  # queue counters per launch; zeroed again only when the ring wraps
+    counters = torch.zeros((ring, apk_amd.QUEUE_WORDS), dtype=torch.int32, device="cuda")
+    out = []
+    for blocks in workers_list:
+        counters.zero_()
+
+        def launch(i, blocks=blocks):
+            if i % ring == 0 and i > 0:
+                counters.zero_()  # stream-ordered after every earlier launch
+            apk_amd.persistent_gemm(eng, A.data_ptr(), Bt.data_ptr(), C.data_ptr(), S, S, S, S,
+                                    counters[i % ring].data_ptr(), None, blocks,
+                                    stream.cuda_stream)
+        tf, clk = timed_sustained(launch, flop, steps, prewarm_ms, wall_mhz, torch, apk_amd,
+                                  stream)
+        out.append({"kernel": "bf16x256 persistent GEMM", "workers": blocks,
+                    "tflops": round(tf, 1), "frac": round(tf / 2516.6, 4),
+                    "tflops_per_worker": round(tf / blocks, 3), "engine_clock_mhz": clk,
+                    "frac_at_measured_clock": round(tf / (2516.6 * clk["mean"] / 2400.0), 4)})
+    if vendor:
+        B = Bt.t().contiguous()
+        Cv = torch.matmul(A, B)
+        ours = C if workers_list else None
+        tf, clk = timed_sustained(lambda i: torch.matmul(A, B, out=Cv), flop, steps,
+                                  prewarm_ms, wall_mhz, torch, apk_amd, stream)
+        case = {"kernel": "torch.matmul bf16 (hipBLASLt)", "tflops": round(tf, 1),
+                "frac": round(tf / 2516.6, 4), "engine_clock_mhz": clk,
+                "frac_at_measured_clock": round(tf / (2516.6 * clk["mean"] / 2400.0), 4)}
+        if ours is not None:
+            # both products of the same bf16 operands (fp32 accumulate, the
+            # vendor's output rounded to bf16): agreement to bf16 rounding
+            d = (ours - Cv.float()).norm() / Cv.float().norm()
+            case["rel_frobenius_vs_ours"] = float(d)
+        out.append(case)
+    del A, Bt, C
+    torch.cuda.empty_cache()
+    return out
+
+
+def bf16_power_sweep(steps, prewarm_ms):
+    """Diagnostic (--bf16-sweep): is the bf16 GEMM's clock set by the load
+    on the whole chip? The bf16x256 persistent GEMM on 256, 192, 128 and 64
+    workers (one per CU), and torch.matmul on the same shape, each after a
+    sustained pre-warm with the engine clock. One JSON line per case."""
+    for case in bf16_sustained((256, 192, 128, 64), steps, prewarm_ms, vendor=True):
+        print(json.dumps(case), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -246,6 +356,10 @@ def main():
     ap.add_argument("--vendor-gemm", action="store_true",
                     help="only time torch.matmul (rocBLAS/hipBLASLt) on the same shapes: bf16 "
                          "8192^3 and fp32 4096^3, for comparison")
+    ap.add_argument("--bf16-sweep", action="store_true",
+                    help="only run the bf16 clock-versus-load diagnostic (bf16x256 GEMM on "
+                         "256/192/128/64 workers and torch.matmul, each after a sustained "
+                         "pre-warm, with the engine clock)")
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="only run a plain device-to-device copy of MIB MiB (the "
                          "known-size kernel that scales rocprofv3 FETCH_SIZE/WRITE_SIZE)")
@@ -281,6 +395,9 @@ def main():
             res[str(dt).split(".")[1]] = {"n": n, "ms": round(ms, 4),
                                           "tflops": round(2 * n ** 3 / ms / 1e9, 1)}
         print(json.dumps({"vendor_gemm": res}), flush=True)
+        return
+    if args.bf16_sweep:
+        bf16_power_sweep(max(args.steps, 20), args.prewarm_ms)
         return
     if args.calibrate_copy:
         n = args.calibrate_copy * (1 << 20) // 4
@@ -408,6 +525,15 @@ def main():
     if not args.no_preempt:
         out["preemption"] = preemption_metrics(args.events, args.trials)
         out["bf16"] = bf16_metrics()
+        blocks_bf16 = info.cu_count * apk_amd.occupancy(apk_amd.ENGINE_BF16X256)
+        ours, vendor = bf16_sustained((blocks_bf16,), 20, args.prewarm_ms, vendor=True)
+        out["bf16"]["sustained"] = {k: ours[k] for k in ("tflops", "frac", "engine_clock_mhz",
+                                                         "frac_at_measured_clock")}
+        out["bf16"]["sustained"]["workload"] = (
+            "one 8192^3 GEMM per launch (apk_persistent_gemm, bf16x256), 20 launches timed "
+            f"after {args.prewarm_ms:.0f} ms of the same launches")
+        out["bf16"]["vendor_sustained"] = {k: vendor[k] for k in (
+            "kernel", "tflops", "frac", "engine_clock_mhz", "frac_at_measured_clock")}
         log("preemption: " + json.dumps(out["preemption"]))
         log("bf16: " + json.dumps(out["bf16"]))
     if not args.no_cpu:
