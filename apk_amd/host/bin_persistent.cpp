@@ -11,7 +11,8 @@
 //                             fmaf tile; mfma128 = 128x128 on fp32 MFMA;
 //                             bf16x256 / bf16x128 = bf16 MFMA tiles on the
 //                             reference's tcyield data, normal(0,1) rounded
-//                             to bf16, B passed transposed)
+//                             to bf16, B passed transposed); --dtype
+//                             fp32|bf16 picks valu64 or bf16x256
 //   --gemm-k K                full GEMM depth, walked in --k wide chunks
 //                             (default = --k: one chunk per tile, as the
 //                             reference); records are per (tile, chunk)
@@ -42,7 +43,7 @@ int main(int argc, char** argv) {
   int blocks = (int)parse_arg(argc, argv, "--blocks", 0);
   double clkMHz = parse_arg(argc, argv, "--sm-clock-mhz", 0.0);
   const char* csvPath = parse_str(argc, argv, "--csv", "results/raw/phase1_tiles.csv");
-  const std::string engName = parse_str(argc, argv, "--engine", "valu64");
+  const std::string engName = engine_arg(argc, argv, "valu64");
   const int gemmK = (int)parse_arg(argc, argv, "--gemm-k", kChunk);
   const int bpc = (int)parse_arg(argc, argv, "--blocks-per-cu", 1);
   const unsigned seed = (unsigned)parse_arg(argc, argv, "--seed", 21);

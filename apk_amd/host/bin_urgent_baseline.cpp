@@ -19,7 +19,8 @@
 //  * the background is the preemptible kernel with polling off (tasks cycle
 //    the tile grid, src/urgent_baseline.cu:78-80), the urgent job is
 //    apk_persistent_gemm with --urgent-blocks workers over its own tiles.
-// Additions: --engine valu64|mfma128|bf16x256|bf16x128, --gemm-k K (background depth, walked
+// Additions: --engine valu64|mfma128|bf16x256|bf16x128 (or --dtype fp32|bf16),
+// --gemm-k K (background depth, walked
 // in --k chunks), --urgent-m/-n/-k (urgent GEMM shape; default
 // urgent-blocks tiles of depth --gemm-k, as the reference), --arrival
 // uniform|exp with --mean-gap-us (exponential delays, redrawn until they fall
@@ -69,7 +70,7 @@ int main(int argc, char** argv) {
   const int reserve = (int)parse_arg(argc, argv, "--reserve", -1);
   const int urgentBlocks = (int)parse_arg(argc, argv, "--urgent-blocks", 1);
   const char* csvPath = parse_str(argc, argv, "--csv", "");
-  const std::string engName = parse_str(argc, argv, "--engine", "valu64");
+  const std::string engName = engine_arg(argc, argv, "valu64");
   const int gemmK = (int)parse_arg(argc, argv, "--gemm-k", kChunk);
   const std::string arrival = parse_str(argc, argv, "--arrival", "uniform");
   const double meanGapUs = parse_arg(argc, argv, "--mean-gap-us", 2000);

@@ -10,7 +10,8 @@
 // complete,last_block,block0_delay_us,lat_excl_setter_us" (extra columns
 // appended), the overhead CSV "rep,poll,wall_ms" and the OBS1 matrix.
 // Additions:
-//   --engine valu64|mfma128   tile engine (default valu64, the reference tile)
+//   --engine valu64|mfma128   tile engine (default valu64, the reference tile;
+//                             --dtype fp32 names the same default)
 //   --gemm-k K                GEMM depth walked in --k chunks (default --k)
 //   --poll chunk|stage        poll at chunk boundaries (default) or every stage
 //   --resume ckpt|acc|restart what a yielding block does with its tile
@@ -72,7 +73,7 @@ int main(int argc, char** argv) {
   const char* csvPath = parse_str(argc, argv, "--csv", "");
   const char* dumpObsPath = parse_str(argc, argv, "--dump-obs", "");
   const int urgentTiles = (int)parse_arg(argc, argv, "--urgent-tiles", 1);
-  const std::string engName = parse_str(argc, argv, "--engine", "valu64");
+  const std::string engName = engine_arg(argc, argv, "valu64");
   const int gemmK = (int)parse_arg(argc, argv, "--gemm-k", kChunk);
   const int poll = poll_mode(parse_str(argc, argv, "--poll", "chunk"));
   const int resume = resume_mode(parse_str(argc, argv, "--resume", "ckpt"));

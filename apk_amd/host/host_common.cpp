@@ -23,6 +23,19 @@ const char* parse_str(int argc, char** argv, const char* name, const char* dflt)
   return dflt;
 }
 
+std::string engine_arg(int argc, char** argv, const char* fp32Default) {
+  const std::string eng = parse_str(argc, argv, "--engine", "");
+  const std::string dt = parse_str(argc, argv, "--dtype", "");
+  const bool engBf16 = eng.rfind("bf16", 0) == 0;
+  if (dt.empty()) return eng.empty() ? std::string(fp32Default) : eng;
+  if (dt == "bf16" && (eng.empty() || engBf16)) return eng.empty() ? "bf16x256" : eng;
+  if ((dt == "fp32" || dt == "f32") && (eng.empty() || !engBf16))
+    return eng.empty() ? std::string(fp32Default) : eng;
+  fprintf(stderr, "--dtype %s does not name the operand type of --engine %s (fp32|bf16)\n",
+          dt.c_str(), eng.empty() ? "(none)" : eng.c_str());
+  return "";
+}
+
 int64_t now_ns() {
   using namespace std::chrono;
   return duration_cast<nanoseconds>(steady_clock::now().time_since_epoch()).count();

@@ -41,6 +41,11 @@ namespace host {
 // atof (src/persistent.cu:83-94).
 double parse_arg(int argc, char** argv, const char* name, double dflt);
 const char* parse_str(int argc, char** argv, const char* name, const char* dflt);
+// The tile engine named by --engine, or chosen by --dtype fp32|bf16 when
+// --engine is absent (fp32: `fp32Default`; bf16: bf16x256). Returns "" when
+// the two flags disagree or --dtype is neither, which the caller reports as a
+// bad flag.
+std::string engine_arg(int argc, char** argv, const char* fp32Default);
 
 int64_t now_ns();
 void spin_for_ns(int64_t ns);

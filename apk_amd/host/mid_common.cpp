@@ -35,7 +35,7 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
   const bool oracle = parse_arg(argc, argv, "--oracle", 0) != 0;
   const char* csvPath = parse_str(argc, argv, "--csv", "");
   const char* dumpObsPath = parse_str(argc, argv, "--dump-obs", "");
-  const std::string engName = parse_str(argc, argv, "--engine", v.engine);
+  const std::string engName = engine_arg(argc, argv, v.engine);
   const int gemmK = (int)parse_arg(argc, argv, "--gemm-k", kChunk);
   const std::string resumeS = parse_str(argc, argv, "--resume", "ckpt");
   const std::string arrival = parse_str(argc, argv, "--arrival", "uniform");
@@ -43,6 +43,9 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
   const unsigned seed = (unsigned)parse_arg(argc, argv, "--seed", 21);
   const int flagCopies = (int)parse_arg(argc, argv, "--flag-copies", 1);
   const int verifyRowsArg = (int)parse_arg(argc, argv, "--verify-rows", -1);
+  // --poll boundary only: a site at every poll_every-th k-chunk boundary
+  // (counted across tasks, as yield --poll-every does)
+  const int pollEvery = (int)parse_arg(argc, argv, "--poll-every", 1);
 
   const int engine = engName == "mfma128"    ? APK_ENGINE_MFMA128
                      : engName == "valu64"   ? APK_ENGINE_VALU64
@@ -62,6 +65,10 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
                      : resumeS == "acc"                           ? APK_RESUME_CKPT_ACC
                      : resumeS == "restart"                       ? APK_RESUME_RESTART
                                                                   : -1;
+  if (pollEvery < 1) {
+    fprintf(stderr, "--poll-every must be >= 1\n");
+    return 1;
+  }
   if (engine < 0 || poll < 0 || resume < 0 ||
       (disc != "drain" && disc != "naive" && disc != "poison")) {
     fprintf(stderr, "bad --engine, --discipline, --poll or --resume\n");
@@ -155,7 +162,8 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
     HIP_CHECK(hipEventCreate(&a));
     HIP_CHECK(hipEventCreate(&b));
     HIP_CHECK(hipEventRecord(a, kStream));
-    rig.launch(pm, 1, resume, poison, nTasks, setter, nEv, orc, kStream, 0, naive);
+    rig.launch(pm, pm == APK_POLL_CHUNK ? pollEvery : 1, resume, poison, nTasks, setter, nEv,
+               orc, kStream, 0, naive);
     HIP_CHECK(hipEventRecord(b, kStream));
     HIP_CHECK(hipStreamSynchronize(kStream));
     HIP_CHECK(hipGetLastError());

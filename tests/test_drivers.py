@@ -49,3 +49,26 @@ def test_driver_binaries_and_flags(path):
     assert used <= known, sorted(used - known)
     for csv in re.findall(r'--csv "([^"]+)"', text):
         assert csv.startswith("$RAW/") and csv.endswith(".csv"), csv
+
+
+BIN = os.path.join(ROOT, "apk_amd", "bin")
+
+
+@pytest.mark.parametrize("binary,args,needle", [
+    ("persistent", ["--dtype", "bf16", "--engine", "mfma128"], "--dtype bf16 does not name"),
+    ("tcyield", ["--dtype", "fp16"], "--dtype fp16 does not name"),
+    ("midyield", ["--dtype", "bf16", "--engine", "valu64"], "--dtype bf16 does not name"),
+    ("urgent_baseline", ["--dtype", "fp32", "--engine", "bf16x256"], "--dtype fp32 does not name"),
+    ("persistent", ["--engine", "fp64"], "unknown --engine"),
+])
+def test_binaries_reject_bad_engine_flags(binary, args, needle):
+    """--dtype picks the engine when --engine is absent (fp32: the binary's
+    default, bf16: bf16x256); a --dtype that contradicts --engine, an
+    unknown --dtype or engine is a bad flag: exit 1 before any GPU call (the
+    reference returns 1 on bad flags, src/midyield.cu:378-381)."""
+    path = os.path.join(BIN, binary)
+    if not os.access(path, os.X_OK):
+        pytest.skip("binaries not built (python -c 'import __graft_entry__ as g; g.build()')")
+    r = subprocess.run([path] + args, capture_output=True, text=True, timeout=60)
+    assert r.returncode == 1, (r.returncode, r.stdout[-500:], r.stderr[-500:])
+    assert needle in r.stderr, r.stderr[-500:]

@@ -107,17 +107,21 @@ def test_persistent_prints_engine_clock(tmp_path):
     assert int(m.group(1)) >= 1 and 500 <= int(m.group(2)) <= 3000, m.group(0)
 
 
-@pytest.mark.parametrize("engine,tiles,bpc", [("bf16x256", 4, 1), ("bf16x128", 8, 2),
-                                              ("bf16x128", 8, 4)])
-def test_persistent_bf16_engines(tmp_path, engine, tiles, bpc):
-    """persistent --engine bf16x256|bf16x128: the bf16 tiles on the reference's
-    tcyield data (normal(0,1) rounded to bf16), float64 check passes, one
-    record per (tile, chunk) in the reference's CSV schema."""
+@pytest.mark.parametrize("sel,tiles,bpc", [(("--engine", "bf16x256"), 4, 1),
+                                            (("--dtype", "bf16"), 4, 1),
+                                            (("--engine", "bf16x128"), 8, 2),
+                                            (("--engine", "bf16x128"), 8, 4)])
+def test_persistent_bf16_engines(tmp_path, sel, tiles, bpc):
+    """persistent --engine bf16x256|bf16x128 (--dtype bf16 = bf16x256): the
+    bf16 tiles on the reference's tcyield data (normal(0,1) rounded to bf16),
+    float64 check passes, one record per (tile, chunk) in the reference's CSV
+    schema."""
     csv = tmp_path / "bf16.csv"
-    out = run_bin("persistent", "--engine", engine, "--tiles-m", tiles, "--tiles-n", tiles,
+    out = run_bin("persistent", *sel, "--tiles-m", tiles, "--tiles-n", tiles,
                   "--gemm-k", 1024, "--k", 256, "--passes", 2, "--blocks-per-cu", bpc,
                   "--verify", 1, "--csv", csv)
     assert "PASS:" in out and "bf16 peak" in out, out[-1500:]
+    assert ("bf16x256" if sel[1] == "bf16" else sel[1]) in out
     assert_header(csv, HDR_PERSISTENT)
     assert len(read_csv(csv)) == tiles * tiles * 4
 
