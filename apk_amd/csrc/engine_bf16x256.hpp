@@ -131,6 +131,11 @@ struct EngBf16x256 {
     uint32_t lds, k;
     i32x4 ra, rb;
   };
+  // Materialises a stage's load descriptors in scalar registers at this
+  // point of the program (nothing moves their computation later).
+  static __device__ __forceinline__ void pin(Dst& d) {
+    asm volatile("" : "+s"(d.lds), "+s"(d.k), "+s"(d.ra), "+s"(d.rb));
+  }
   static __device__ __forceinline__ Dst stage_dst(uint32_t wave_lds, const Ctx& c, int slot,
                                                   int t, int S) {
     const bool real = t < S;

@@ -379,8 +379,10 @@ k_persistent_yield(const apk_yield_params) {
       bool atSite = false;
       int fSeen = 0;
       while (s < S) {
-        wait_landed<E>();
-        lds_sync();
+        if constexpr (E::GROUP == 1) {
+          wait_landed<E>();
+          lds_sync();
+        }
         // Poll site: the flag sample for site s has landed with stage s (it
         // was issued in front of the loads of stage s+1, or of the pair s).
         // A new generation (or the setter's turn) ends the loop here, before
@@ -435,6 +437,13 @@ k_persistent_yield(const apk_yield_params) {
           slot = next_slot<E>(slot);
           ++s;
         } else {
+          // Everything scalar about this pair -- the site bookkeeping and the
+          // next pair's load descriptors -- is formed before the wait, while
+          // the pair's loads land, and the descriptors are pinned there:
+          // formed after the barrier (where the compiler sinks them in the
+          // polled kernels, next to their use) they held back the next
+          // pair's loads and cost the chunk-poll kernel 5-6% with no site
+          // polled at all.
           const bool site = POLL != APK_POLL_OFF && s == nextSite;
           const bool check = site && s != siteDone;
           if (site) nextSite += pollStride;
@@ -454,8 +463,12 @@ k_persistent_yield(const apk_yield_params) {
           // the other half of the ring, which held the previous pair.
           const int other = slot ^ 2;
           const bool carry = s + 2 == nextSite;
-          const typename E::Dst d0 = E::stage_dst(wl, ctx, other, s + 2, S);
-          const typename E::Dst d1 = E::stage_dst(wl, ctx, other + 1, s + 3, S);
+          typename E::Dst d0 = E::stage_dst(wl, ctx, other, s + 2, S);
+          typename E::Dst d1 = E::stage_dst(wl, ctx, other + 1, s + 3, S);
+          E::pin(d0);
+          E::pin(d1);
+          wait_landed<E>();
+          lds_sync();
           if constexpr (POLL == APK_POLL_ISSUE) {
             // Issue sites: the next pair goes out at once, then the poll.
             if (!ahead) {

@@ -134,17 +134,24 @@ __device__ __forceinline__ void run_stages(char* ring, uint32_t wl, const typena
   int slot = 0;
   for (int s = 0; s < S; s += E::GROUP) {
     hook(s);
-    wait_landed<E>();
-    lds_sync();
     if constexpr (E::GROUP == 1) {
+      wait_landed<E>();
+      lds_sync();
       const typename E::Dst d = E::stage_dst(wl, c, slot_after_next(slot), s + 2, S);
       E::compute(ring, slot, acc, [] { return true; },
                  [&](int i) { E::issue_one(c, ln, d, i); });
       slot = next_slot<E>(slot);
     } else {
+      // The next pair's load descriptors are formed and pinned before the
+      // wait, so that nothing scalar stands between the barrier and the
+      // next pair's loads (as in the preemptible kernel's pair loop).
       const int other = slot ^ 2;
-      const typename E::Dst d0 = E::stage_dst(wl, c, other, s + 2, S);
-      const typename E::Dst d1 = E::stage_dst(wl, c, other + 1, s + 3, S);
+      typename E::Dst d0 = E::stage_dst(wl, c, other, s + 2, S);
+      typename E::Dst d1 = E::stage_dst(wl, c, other + 1, s + 3, S);
+      E::pin(d0);
+      E::pin(d1);
+      wait_landed<E>();
+      lds_sync();
       if (s + 1 < S) hook(s + 1);
       E::compute(ring, slot, acc, [] { return true; },
                  [&](int i) { issue_group_one<E>(c, ln, d0, d1, i); });
