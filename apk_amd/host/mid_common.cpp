@@ -46,6 +46,8 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
   // --poll boundary only: a site at every poll_every-th k-chunk boundary
   // (counted across tasks, as yield --poll-every does)
   const int pollEvery = (int)parse_arg(argc, argv, "--poll-every", 1);
+  // --mode calibrate: untimed launches before the timed one (default none)
+  const double prewarmMs = parse_arg(argc, argv, "--prewarm-ms", 0);
 
   const int engine = engName == "mfma128"    ? APK_ENGINE_MFMA128
                      : engName == "valu64"   ? APK_ENGINE_VALU64
@@ -177,12 +179,23 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
   // ------------------------------------------------------------ calibrate
   // Tile throughput with polling off (src/tcyield.cu:637-651).
   if (mode == "calibrate") {
+    // Engine clock during the timed run: probes over 80% of its expected
+    // length (apk_clock_probe). The probe stream's hardware queue is set up
+    // first: set up beside a running GEMM it slows the GEMM for a while.
+    ClockProbe probe;
     rig.reset(false);
     const double warmMs = timed_run(APK_POLL_OFF, (unsigned)blocks, false, 0, false);
+    // --prewarm-ms: untimed launches of the timed run's size first, so that
+    // the engine clock has left its idle level (it climbs over ~1 s of load).
+    const int64_t preEnd = now_ns() + (int64_t)(prewarmMs * 1e6);
+    int preRuns = 0;
+    while (now_ns() < preEnd) {
+      rig.reset(false);
+      timed_run(APK_POLL_OFF, tasks, false, 0, false);
+      ++preRuns;
+    }
+    if (preRuns) printf("pre-warm: %d untimed runs of %u tasks\n", preRuns, tasks);
     rig.reset(false);
-    // Engine clock during the timed run: probes over 80% of its expected
-    // length (apk_clock_probe).
-    ClockProbe probe;
     hipEvent_t a, b;
     HIP_CHECK(hipEventCreate(&a));
     HIP_CHECK(hipEventCreate(&b));

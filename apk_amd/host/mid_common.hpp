@@ -35,7 +35,8 @@
 // -n/-k (default one tile of depth --k), --arrival uniform|exp,
 // --mean-gap-us, --seed, --flag-copies, --verify-rows (float64 rows of C),
 // --poll-every N (--poll boundary: a site at every N-th k-chunk boundary,
-// counted across tasks).
+// counted across tasks), --prewarm-ms T (--mode calibrate: T ms of untimed
+// runs before the timed one).
 #pragma once
 
 namespace host {
