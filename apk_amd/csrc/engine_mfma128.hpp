@@ -2,10 +2,22 @@
 // cores (v_mfma_f32_32x32x2_f32), fed by a 3-stage LDS ring of
 // buffer_load_dwordx4 ... lds (direct-to-LDS, no VGPR staging).
 //
+// Two ring shapes of the same tile (template parameter G):
+//  G = 1 (EngMfma128): 3 slots, one barrier per k-stage -- the preemptible
+//        kernels, which poll at every k-stage;
+//  G = 2 (EngMfma128Pairs): 4 slots (128 KiB) taken in pairs of k-stages,
+//        one barrier per pair -- the non-preemptible persistent GEMM and the
+//        urgent-job kernel, for tiles of an even number of k-stages. With
+//        one wave per SIMD nothing covers a barrier's wait and first operand
+//        reads, so halving the barriers gains 1.5-2% (4096^3 and 8192^3,
+//        ABAB).
+// Both walk every output's k in the same order, so their C is bit-identical.
+//
 // Block: 256 threads = 4 wave64s in a 2x2 arrangement; each wave owns a
 // 64x64 sub-tile held as 2x2 32x32 accumulators (64 VGPRs per lane).
 // Stage: k depth KS=32 -> A stage 128x32 fp32 (16 KiB) + B stage 32x128 fp32
-// (16 KiB); 3 stages = 96 KiB of the 160 KiB LDS (1 block per CU).
+// (16 KiB); 3 stages = 96 KiB (pairs: 4 = 128 KiB) of the 160 KiB LDS (1 block
+// per CU).
 //
 // LDS layouts (bank-conflict-free for the MFMA operand reads):
 //  A stage: 128 rows x 128 B. 16-byte quad q of row r is stored at slot
@@ -30,8 +42,14 @@
 
 namespace apk {
 
-struct EngMfma128 {
-  static constexpr int TM = 128, TN = 128, KS = 32, NS = 3, GROUP = 1, THREADS = 256;
+template <int G>
+struct EngMfma128T {
+  static_assert(G == 1 || G == 2, "stage groups of 1 or 2");
+  static constexpr int TM = 128, TN = 128, KS = 32, NS = G == 2 ? 4 : 3, GROUP = G,
+                       THREADS = 256;
+  // Pairs take tiles of an even number of k-stages only (a stage past the
+  // tile's end refetches the last one, which a pair would compute): the
+  // launches pick the one-stage ring for the others.
   // Waves per SIMD at most (1 block per CU (LDS-bound)): the register budget the
   // compiler may schedule for.
   static constexpr int WAVES_PER_SIMD = 1;
@@ -39,7 +57,7 @@ struct EngMfma128 {
   static constexpr int A_STAGE = TM * KS * 4;               // bytes
   static constexpr int B_STAGE = KS * TN * 4;               // bytes
   static constexpr int STAGE = A_STAGE + B_STAGE;           // 32 KiB
-  static constexpr int LDS_BYTES = NS * STAGE;              // 96 KiB
+  static constexpr int LDS_BYTES = NS * STAGE;              // 96 / 128 KiB
   static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 4 per thread
   static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 4 per thread
   static constexpr int LOADS = LOADS_A + LOADS_B;           // per stage
@@ -110,6 +128,15 @@ struct EngMfma128 {
   struct Dst {
     uint32_t lds, ka, kb;
   };
+  // Materialises a stage's load descriptors in scalar registers at this
+  // point of the program (nothing moves their computation later). They are
+  // uniform by construction; readfirstlane only tells the compiler so.
+  static __device__ __forceinline__ void pin(Dst& d) {
+    d.lds = __builtin_amdgcn_readfirstlane(d.lds);
+    d.ka = __builtin_amdgcn_readfirstlane(d.ka);
+    d.kb = __builtin_amdgcn_readfirstlane(d.kb);
+    asm volatile("" : "+s"(d.lds), "+s"(d.ka), "+s"(d.kb));
+  }
   // A stage past the tile's end (t >= S) fetches stage S-1 again: nothing
   // reads that slot before it is refilled.
   static __device__ __forceinline__ Dst stage_dst(uint32_t wave_lds, const Ctx& c, int slot,
@@ -158,27 +185,30 @@ struct EngMfma128 {
     }
   }
 
-  // One k-stage of MFMAs out of ring slot `slot`. The operands of group g+1
-  // are read from LDS while group g's 16 MFMAs run. `pre` runs after the
-  // first group's operand reads are issued (the preempt-flag check: its LDS
-  // read overlaps theirs); if it returns false the stage is abandoned before
-  // any accumulator changes and compute returns false. `mid(i)`, i = 0..
-  // LOADS-1, runs after MFMA 2i+1 of the first group: the stage loops issue
-  // the next stage's direct-to-LDS load i there, under the matrix work.
-  template <class Pre, class Mid>
-  static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
-                                                 Pre&& pre, Mid&& mid) {
+  // NST consecutive k-stages of MFMAs out of ring slots slot .. slot+NST-1
+  // (contiguous in LDS), as one sequence of k-groups in ascending k. The
+  // operands of group g+1 are read from LDS while group g's 16 MFMAs run.
+  // `pre` runs after the first group's operand reads are issued (the
+  // preempt-flag check: its LDS read overlaps theirs); if it returns false
+  // the stages are abandoned before any accumulator changes and the call
+  // returns false. `mid(i)`, i = 0..NST*LOADS-1, runs after MFMA 2i+1 of the
+  // first groups (8 per group): the stage loops issue the next stages'
+  // direct-to-LDS load i there, under the matrix work.
+  template <int NST, class Pre, class Mid>
+  static __device__ __forceinline__ bool compute_n(const char* ring, int slot, Acc& acc,
+                                                   Pre&& pre, Mid&& mid) {
     const char* abase = ring + slot * STAGE;
-    constexpr int G = KS / 8;
+    constexpr int GS = KS / 8;    // k-groups per stage
+    constexpr int GG = GS * NST;  // k-groups in all
     Frag f[2];
     load_frag(abase, 0, f[0]);
     if (!pre()) return false;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
+    for (int g = 0; g < GG; ++g) {
       // The reads of group g+1 are issued ahead of group g's 16 MFMAs (the
       // scheduling barrier keeps the compiler from sinking each read next to
       // its first use, where the LDS latency would stall the matrix pipe).
-      if (g + 1 < G) load_frag(abase, g + 1, f[(g + 1) & 1]);
+      if (g + 1 < GG) load_frag(abase + ((g + 1) / GS) * STAGE, (g + 1) % GS, f[(g + 1) & 1]);
       __builtin_amdgcn_sched_barrier(0);
       const Frag& c = f[g & 1];
 #pragma unroll
@@ -186,14 +216,20 @@ struct EngMfma128 {
         const int s = m >> 2, rb = (m >> 1) & 1, cb = m & 1;
         acc.c[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x2f32(c.a4[rb][s], c.bv[cb][s],
                                                              acc.c[rb][cb], 0, 0, 0);
-        if (g == 0 && (m & 1) && (m >> 1) < LOADS) {
+        if ((m & 1) && g * 8 + (m >> 1) < NST * LOADS) {
           __builtin_amdgcn_sched_barrier(0);
-          mid(m >> 1);
+          mid(g * 8 + (m >> 1));
           __builtin_amdgcn_sched_barrier(0);
         }
       }
     }
     return true;
+  }
+  // The ring's stage group (GROUP stages).
+  template <class Pre, class Mid>
+  static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
+                                                 Pre&& pre, Mid&& mid) {
+    return compute_n<GROUP>(ring, slot, acc, static_cast<Pre&&>(pre), static_cast<Mid&&>(mid));
   }
   static __device__ __forceinline__ void compute(const char* ring, int slot, Acc& acc) {
     compute(ring, slot, acc, [] { return true; }, [](int) {});
@@ -249,5 +285,8 @@ struct EngMfma128 {
         }
   }
 };
+
+using EngMfma128 = EngMfma128T<1>;
+using EngMfma128Pairs = EngMfma128T<2>;
 
 }  // namespace apk

@@ -213,6 +213,13 @@ extern "C" int apk_persistent_gemm(int engine, const void* A, const void* B,
                                                next_task, log, blocks,
                                                as_stream(stream));
     case APK_ENGINE_MFMA128:
+      // Stage pairs (one barrier per 64 k) for tiles of whole pairs, except
+      // where per-chunk records are asked for at chunks that end inside a pair.
+      if (K % (2 * EngMfma128Pairs::KS) == 0 &&
+          (log == nullptr || k_chunk % (2 * EngMfma128Pairs::KS) == 0))
+        return launch_persistent_gemm<EngMfma128Pairs>(A, B, C, M, N, K, k_chunk,
+                                                       next_task, log, blocks,
+                                                       as_stream(stream));
       return launch_persistent_gemm<EngMfma128>(A, B, C, M, N, K, k_chunk,
                                                 next_task, log, blocks,
                                                 as_stream(stream));
@@ -234,7 +241,16 @@ extern "C" int apk_persistent_gemm_occupancy(int engine, int* blocks_per_cu) {
   using namespace apk;
   switch (engine) {
     case APK_ENGINE_VALU64: return occupancy_of<EngValu64>(blocks_per_cu);
-    case APK_ENGINE_MFMA128: return occupancy_of<EngMfma128>(blocks_per_cu);
+    case APK_ENGINE_MFMA128: {
+      // the smaller of the two ring shapes' occupancies (both 1 per CU)
+      int a = 0, b = 0;
+      const int rc = occupancy_of<EngMfma128>(&a);
+      if (rc != APK_OK) return rc;
+      const int rc2 = occupancy_of<EngMfma128Pairs>(&b);
+      if (rc2 != APK_OK) return rc2;
+      *blocks_per_cu = a < b ? a : b;
+      return APK_OK;
+    }
     case APK_ENGINE_BF16X256: return occupancy_of<EngBf16x256>(blocks_per_cu);
     case APK_ENGINE_BF16X128: return occupancy_of<EngBf16x128>(blocks_per_cu);
     default:
@@ -283,6 +299,9 @@ extern "C" int apk_urgent_gemm(int engine, const void* A, const void* B, float* 
     case APK_ENGINE_VALU64:
       return launch_urgent_tiles<EngValu64>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));
     case APK_ENGINE_MFMA128:
+      if (K % (2 * EngMfma128Pairs::KS) == 0)
+        return launch_urgent_tiles<EngMfma128Pairs>(A, B, C, M, N, K, start_gt, end_gt,
+                                                    as_stream(stream));
       return launch_urgent_tiles<EngMfma128>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));
     case APK_ENGINE_BF16X256:
       return launch_urgent_tiles<EngBf16x256>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));

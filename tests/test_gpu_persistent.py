@@ -64,6 +64,23 @@ def test_mfma128_parity_and_order_independence(torch_gpu, apk, kc):
     assert (recs["block"] >= 0).all()
 
 
+@pytest.mark.parametrize("K", [96, 128, 32, 192])
+def test_mfma128_stage_pairs_odd_stage_counts(torch_gpu, apk, K):
+    """Without per-chunk records the fp32 MFMA tile runs its k-stages in
+    pairs (one barrier per 64 k) when a tile has an even number of 32-deep
+    stages, and one stage per barrier otherwise. C is bit-identical to the
+    one-stage-per-barrier loop (records at every 32-k chunk) and within
+    tolerance of float64."""
+    say(f"mfma128 stage pairs vs single stages, M=256 N=384 K={K} ({K // 32} stages)")
+    A, B = oracle.fill_uniform_pm1(8, 256, 384, K)
+    Cp, _, _ = run_persistent(torch_gpu, apk, apk.ENGINE_MFMA128, A, B, K, blocks=5,
+                              with_log=False)
+    Cs, recs, _ = run_persistent(torch_gpu, apk, apk.ENGINE_MFMA128, A, B, 32, blocks=5)
+    assert (_bits(Cp) == _bits(Cs)).all()
+    assert (recs["block"] >= 0).all()
+    assert oracle.rel_frobenius(Cp, oracle.gemm_f64(A, B)) <= FROB_F32
+
+
 def test_mfma128_single_tile_and_idle_workers(torch_gpu, apk):
     say("mfma128 single tile, 64 workers")
     A, B = oracle.fill_uniform_pm1(4, 128, 128, 64)

@@ -33,7 +33,9 @@ def test_urgent_fp32_matches_persistent(torch_gpu, apk, name):
     say(f"urgent_gemm {name} {M}x{N}x{K} vs persistent_gemm")
     A, B = oracle.fill_uniform_pm1(21, M, N, K)
     C, start, end = run_urgent(torch_gpu, apk, eng, A, B)
-    Cp, _, _ = run_persistent(torch_gpu, apk, eng, A, B, K, blocks=3, with_log=False)
+    # records at every k-stage: the persistent GEMM's one-stage-per-barrier
+    # loop, against the urgent kernel's (stage pairs for the fp32 MFMA tile)
+    Cp, _, _ = run_persistent(torch_gpu, apk, eng, A, B, g.k_stage, blocks=3)
     assert np.array_equal(C.view(np.uint32), Cp.view(np.uint32))
     if name == "valu64":
         assert np.array_equal(C.view(np.uint32), oracle.gemm_f32_chain(A, B).view(np.uint32))
