@@ -88,9 +88,10 @@ k_persistent_yield(const apk_yield_params) {
   const bool isSetter = P().flag_set != nullptr && P().sched != nullptr && bid == 0;
   constexpr bool retreatArm = RETREAT && POLL != APK_POLL_OFF;
   // A retreat-arm continuation is the set of blocks that retreats, all of
-  // it, at the next generation: it polls the flag synchronously (stage polls
-  // of one-barrier-per-stage engines), to act a stage sooner.
-  const bool syncPoll = retreatArm && !SYS && E::GROUP == 1 && POLL == APK_POLL_STAGE &&
+  // it, at the next generation: at its stage sites it reads the flag itself
+  // (one load, one barrier) rather than the sample issued a stage (or a pair
+  // of stages) earlier, to act that much sooner.
+  const bool syncPoll = retreatArm && !SYS && POLL == APK_POLL_STAGE &&
                         P().continuation != 0 && P().launch_epoch > 0;
   const int* myFlag = (const int*)((const char*)P().flag + (size_t)(bid % copies()) * APK_FLAG_STRIDE);
 
@@ -449,7 +450,12 @@ k_persistent_yield(const apk_yield_params) {
           if (site) nextSite += pollStride;
           auto poll = [&]() -> bool {
             if (!check) return true;
-            const int f = uniform(flagring[site_flag(slot)]);
+            int f = uniform(flagring[site_flag(slot)]);
+            if (syncPoll) {  // as in the one-stage loop above
+              if (tid == 0) s_fsync = flag_load(myFlag);
+              lds_sync();
+              f = uniform(s_fsync);
+            }
             fLatest = f;
             if (f != lastSeen || isSetter) {
               fSeen = f;

@@ -28,9 +28,10 @@ against -- and `bf16`: the cfg5 bf16 MFMA GEMM throughput (M=N=K=8192,
 256x256 tiles, no yields) with its engine clock: right after the preemption
 runs (`tflops`, the poll-off preemptible kernel over two GEMMs), and
 sustained (one GEMM per launch after a pre-warm of the same launches), beside
-torch.matmul (hipBLASLt) on the same operands under the same conditions. The
-sustained bf16 clock is set by the load on the whole chip (`--bf16-sweep`
-times the GEMM on 64-256 workers).
+torch.matmul (hipBLASLt) on the same operands under the same conditions (the
+sustained bf16 clock is set by the load on the whole chip; `--bf16-sweep`
+times the GEMM on 64-256 workers), and the retreat arm on the bf16 background
+(10,000 arrivals; retreating tiles re-queued from k = 0).
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-preempt]
 """
@@ -216,19 +217,44 @@ def preemption_metrics(events, trials):
 
 
 def bf16_metrics():
-    """cfg5 bf16 MFMA GEMM throughput (tcyield calibrate, no yields)."""
+    """cfg5 bf16 MFMA GEMM throughput (tcyield calibrate, no yields), and the
+    retreat arm's latency on the bf16 background (urgent_baseline)."""
     t = run_bin("tcyield", ["--mode", "calibrate", "--tiles-m", 32, "--tiles-n", 32,
                             "--gemm-k", 8192, "--k", 256, "--tasks", 2048,
                             "--prewarm-ms", 1500])
     us, gf = grab(t, r"-> ([\d.]+) us/task/block \| ([\d.]+) GFLOP/s")
     mhz, = grab(t, r"engine clock during the run \(\d+ probes\): mean ([\d.]+) MHz")
     tf = gf / 1e3
+    # Retreat arm on the bf16 background: one job, 10,000 exponential
+    # arrivals (mean 2 ms), urgent bf16 GEMM 256^3 on its own stream; the
+    # retreating blocks re-queue their tiles from k = 0 (no checkpoint of the
+    # 256 KiB accumulators).
+    rt = run_bin("urgent_baseline", ["--engine", "bf16x256", "--tiles-m", 32, "--tiles-n", 32,
+                                     "--gemm-k", 8192, "--k", 256, "--urgent-m", 256,
+                                     "--urgent-n", 256, "--urgent-k", 256, "--bg-tasks", 1024,
+                                     "--urgent-blocks", 1, "--arrival", "exp", "--mean-gap-us",
+                                     2000, "--verify-rows", 32, "--yield", 1, "--retreat", 1,
+                                     "--oracle", 1, "--continuous", 1, "--events", 10000,
+                                     "--resume", "restart"], timeout=600)
+    r50, r99 = grab(rt, r"flag raised -> urgent GEMM starts \(us\): p50 ([\d.]+) \| "
+                        r"p90 [\d.]+ \| p99 ([\d.]+)")
+    n_in, = grab(rt, r"continuous retreat arm: (\d+) arrivals within the job", int)
+    tile_us, = grab(rt, r"tile \(k-chunk\) time at full residency: ([\d.]+) us")
+    bad, total = grab(rt, r"SAFETY: (\d+) of (\d+) task fingerprints", int)
+    ovh, = grab(rt, r"retreat overhead ([-\d.]+)%")
     return {"workload": "cfg5: bf16 GEMM M=N=K=8192 (2 passes of 1024 256x256 tiles), fp32 "
                         "accumulate, 256 workers, no yields, after 1.5 s of the same runs",
             "tflops": round(tf, 2), "peak": 2516.6, "frac": round(tf / 2516.6, 4),
             "engine_clock_mhz": mhz,
             "frac_at_measured_clock": round(tf / (2516.6 * mhz / 2400.0), 4),
-            "us_per_tile": us}
+            "us_per_tile": us,
+            "retreat_latency_us": {"p50": r50, "p99": r99, "events": n_in,
+                                   "tile_us": tile_us, "p50_over_tile": round(r50 / tile_us, 3),
+                                   "mode": "continuous job, tiles re-queued from k = 0",
+                                   "background_overhead_pct": ovh, "corrupt_tasks": bad,
+                                   "tasks_checked": total,
+                                   "oracle": "PASS" if ("ORACLE: PASS" in rt and
+                                                        "yield: PASS" in rt) else "FAIL"}}
 
 
 def timed_sustained(launch, flop, steps, prewarm_ms, wall_mhz, torch, apk_amd, stream):
