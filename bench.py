@@ -560,18 +560,37 @@ def main():
         },
         "prewarm": {"ms": round(pre_ms, 1), "launches": pre_launches},
     }
+    failed = []
+
+    def section(name, fn):
+        """A section's figures, or {"error": ...} in their place (and a
+        non-zero exit status after the line is printed) if it fails: the
+        GEMM line above is never lost to a later section."""
+        try:
+            return fn()
+        except Exception as e:  # a binary's exit status, a missing pattern
+            import traceback
+            traceback.print_exc()
+            failed.append(name)
+            return {"error": f"{type(e).__name__}: {str(e)[:800]}"}
+
     if not args.no_preempt:
-        out["preemption"] = preemption_metrics(args.events, args.trials)
-        out["bf16"] = bf16_metrics()
-        blocks_bf16 = info.cu_count * apk_amd.occupancy(apk_amd.ENGINE_BF16X256)
-        ours, vendor = bf16_sustained((blocks_bf16,), 20, args.prewarm_ms, vendor=True)
-        out["bf16"]["sustained"] = {k: ours[k] for k in ("tflops", "frac", "engine_clock_mhz",
-                                                         "frac_at_measured_clock")}
-        out["bf16"]["sustained"]["workload"] = (
-            "one 8192^3 GEMM per launch (apk_persistent_gemm, bf16x256), 20 launches timed "
-            f"after {args.prewarm_ms:.0f} ms of the same launches")
-        out["bf16"]["vendor_sustained"] = {k: vendor[k] for k in (
-            "kernel", "tflops", "frac", "engine_clock_mhz", "frac_at_measured_clock")}
+        out["preemption"] = section("preemption",
+                                    lambda: preemption_metrics(args.events, args.trials))
+
+        def bf16_all():
+            b = bf16_metrics()
+            blocks_bf16 = info.cu_count * apk_amd.occupancy(apk_amd.ENGINE_BF16X256)
+            ours, vendor = bf16_sustained((blocks_bf16,), 20, args.prewarm_ms, vendor=True)
+            b["sustained"] = {k: ours[k] for k in ("tflops", "frac", "engine_clock_mhz",
+                                                   "frac_at_measured_clock")}
+            b["sustained"]["workload"] = (
+                "one 8192^3 GEMM per launch (apk_persistent_gemm, bf16x256), 20 launches timed "
+                f"after {args.prewarm_ms:.0f} ms of the same launches")
+            b["vendor_sustained"] = {k: vendor[k] for k in (
+                "kernel", "tflops", "frac", "engine_clock_mhz", "frac_at_measured_clock")}
+            return b
+        out["bf16"] = section("bf16", bf16_all)
         log("preemption: " + json.dumps(out["preemption"]))
         log("bf16: " + json.dumps(out["bf16"]))
     if not args.no_cpu:
@@ -584,7 +603,12 @@ def main():
                         "pass": bool(frob <= 1e-5)}
         log(f"cpu baseline {cb['value'] * 1e3:.1f} GFLOP/s on {cb['cores']} threads "
             f"({cb['single_thread']['value'] * 1e3:.2f} on 1); whole C rel-Frobenius {frob:.2e}")
+        if not out["check"]["pass"]:
+            failed.append("check")
     print(json.dumps(out), flush=True)
+    if failed:
+        log("bench.py: failed: " + ", ".join(failed))
+        sys.exit(1)
 
 
 if __name__ == "__main__":
