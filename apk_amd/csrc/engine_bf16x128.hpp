@@ -9,24 +9,30 @@
 // memory, LDS and operand registers. C is M x N row-major fp32.
 //
 // Block: 256 threads = 4 wave64s in a 2x2 arrangement; each wave owns a
-// 64x64 sub-tile held as 2x2 32x32 accumulators (64 fp32 per lane). At 4
-// blocks per CU a SIMD holds 4 waves, so a wave has 128 registers per lane:
-// 64 accumulators, two operand fragments of 16 and the addresses.
-// Stage: k depth KS=16 (one MFMA k-step) -> A stage 128 rows x 32 B (4 KiB)
-// + Bt stage 128 rows x 32 B (4 KiB); 4 slots = 32 KiB, synchronised once
-// per pair of stages (GROUP = 2) as in the 256x256 engine. The LDS block is
-// 33 KiB (the epilogue's staging of 64 padded rows), so 4 blocks take 132
-// KiB of the CU's 160 KiB.
+// 64x64 sub-tile held as 2x2 32x32 accumulators (64 fp32 per lane). Two
+// stage depths (template parameter KS), both with a 4-slot ring taken in
+// pairs of stages (GROUP = 2, one barrier per pair, as in the 256x256
+// engine):
+//  KS = 16 (EngBf16x128, engine bf16x128): one MFMA k-step per stage; A and
+//     Bt stages of 128 rows x 32 B, 32 KiB of ring; the LDS block is 33 KiB
+//     (the epilogue's staging of 64 padded rows), so 4 blocks take 132 KiB
+//     of the CU's 160 KiB, and a wave has 128 registers per lane (4 waves
+//     per SIMD).
+//  KS = 32 (EngBf16x128K32, engine bf16x128k32): two k-steps per stage, rows
+//     of 64 B, 64 KiB of ring: 2 blocks per CU, 256 registers per lane. Twice
+//     the MFMAs per barrier: 37-39% faster than KS = 16 at 1 and 2 blocks per
+//     CU (8192^3, ABAB), with C bit-identical.
 //
-// LDS layout (both operands): row r of a stage is 32 B = two 16-byte chunks;
-// chunk q is stored at slot q ^ swz(r), swz(r) = (r >> 3) & 1. A ds_read_b128
-// is served 16 lanes per cycle (256 B); 16 consecutive rows reading chunk q
-// then fall on 16 different 16-byte bank groups, where the unswizzled layout
-// puts rows r and r+8 on the same group.
+// LDS layout (both operands): row r of a stage is KS * 2 bytes = 2 or 4
+// 16-byte chunks; chunk q is stored at slot q ^ swz(r), swz(r) = (r >> 3) & 1
+// for 32-byte rows and (r >> 2) & 3 for 64-byte rows. A ds_read_b128 is
+// served 16 lanes per cycle (256 B); 16 consecutive rows reading one chunk
+// then fall on 16 different 16-byte bank groups (the 64-byte layout is the
+// 256x256 engine's, measured conflict-free there).
 //
-// k order: one MFMA k-step of 16 per stage, in ascending k; every output's
-// sum is formed in the same order whatever worker computes it and however
-// often it is checkpointed and resumed.
+// k order: the MFMA k-steps of 16 in ascending k; every output's sum is
+// formed in the same order whatever worker computes it, whatever the stage
+// depth, and however often it is checkpointed and resumed.
 //
 // Epilogue: the fp32 tile (64 KiB) is staged in 2 passes of 64 rows (32 rows
 // of each wave row), row stride TN + 4 floats.
@@ -37,24 +43,28 @@ namespace apk {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-struct EngBf16x128 {
-  static constexpr int TM = 128, TN = 128, KS = 16, NS = 4, GROUP = 2, THREADS = 256;
-  // 4 blocks of 4 waves per CU: every instantiation must fit 128 registers
-  // per lane (accumulators included), so the compiler is held to 4 waves.
-  static constexpr int WAVES_PER_SIMD = 4;
-  static constexpr int MIN_WAVES_PER_SIMD = 4;
-  static constexpr int ROW_BYTES = KS * 2;                  // 32 B
-  static constexpr int A_STAGE = TM * ROW_BYTES;            // 4 KiB
-  static constexpr int B_STAGE = TN * ROW_BYTES;            // 4 KiB
-  static constexpr int STAGE = A_STAGE + B_STAGE;           // 8 KiB
-  static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 1 per thread
-  static constexpr int LOADS_B = B_STAGE / (THREADS * 16);  // 1 per thread
+template <int KS_>
+struct EngBf16x128T {
+  static_assert(KS_ == 16 || KS_ == 32, "16- or 32-deep k-stages");
+  static constexpr int TM = 128, TN = 128, KS = KS_, NS = 4, GROUP = 2, THREADS = 256;
+  // KS 16: 4 blocks of 4 waves per CU, so every instantiation must fit 128
+  // registers per lane; KS 32: 2 blocks (64 KiB ring each), 256 registers.
+  static constexpr int WAVES_PER_SIMD = KS == 16 ? 4 : 2;
+  static constexpr int MIN_WAVES_PER_SIMD = WAVES_PER_SIMD;
+  static constexpr int CHUNKS = KS * 2 / 16;                // 16-byte chunks per row
+  static constexpr int ROW_BYTES = KS * 2;                  // 32 / 64 B
+  static constexpr int A_STAGE = TM * ROW_BYTES;            // 4 / 8 KiB
+  static constexpr int B_STAGE = TN * ROW_BYTES;
+  static constexpr int STAGE = A_STAGE + B_STAGE;           // 8 / 16 KiB
+  static constexpr int LOADS_A = A_STAGE / (THREADS * 16);  // 1 / 2 per thread
+  static constexpr int LOADS_B = B_STAGE / (THREADS * 16);
   static constexpr int LOADS = LOADS_A + LOADS_B;
   static constexpr int WAVES = THREADS / 64;
+  static constexpr int ROWS_PER_WAVE = 64 / CHUNKS;         // rows of one wave's load
   static constexpr int ACC_PER_THREAD = 64;                 // floats
   static constexpr int ELEM_BYTES = 2;                      // bf16 operands
   static constexpr int STORE_PASSES = 2, PASS_ROWS = 64, STAGE_LD = TN + 4;
-  static constexpr int RING_BYTES = NS * STAGE;             // 32 KiB
+  static constexpr int RING_BYTES = NS * STAGE;             // 32 / 64 KiB
   static constexpr int EPI_BYTES = PASS_ROWS * STAGE_LD * 4;
   static constexpr int LDS_BYTES = RING_BYTES > EPI_BYTES ? RING_BYTES : EPI_BYTES;
 
@@ -85,23 +95,35 @@ struct EngBf16x128 {
         for (int r = 0; r < 16; ++r) a.c[i][j][r] = 0.0f;
   }
 
-  static __device__ __forceinline__ int swz(int r) { return (r >> 3) & 1; }
+  // 32-byte rows: (r >> 3) & 1; 64-byte rows: (r >> 2) & 3 (the 256x256
+  // engine's layout).
+  static __device__ __forceinline__ int swz(int r) {
+    return KS == 16 ? (r >> 3) & 1 : (r >> 2) & 3;
+  }
 
-  // Direct-to-LDS loads of one k-stage: load 0 fills rows 32*wave + lane/2
-  // of the A stage (this wave's 1 KiB piece), load 1 the same rows of the Bt
-  // stage; lane l writes slot l & 1 of its row, so it reads the row's chunk
-  // (l & 1) ^ swz(row) from memory. Fixed per tile (one register per load);
-  // stage t only adds the scalar k offset.
+  // Direct-to-LDS loads of one k-stage: load i fills rows
+  // ROWS_PER_WAVE * (WAVES * i + wave) + lane / CHUNKS of the A stage (i <
+  // LOADS_A) or of the Bt stage; lane l writes slot l % CHUNKS of its row,
+  // so it reads the row's chunk (l % CHUNKS) ^ swz(row) from memory. The
+  // swizzle uses only row bits that i does not change, so each lane's offset
+  // of load i is fixed per tile (one register per load); stage t only adds
+  // the scalar k offset.
   struct Lane {
     uint32_t a[LOADS_A], b[LOADS_B];
   };
   static __device__ __forceinline__ Lane lane_offsets(const Ctx& c, int row0, int col0) {
     const int w = wave_id(), l = lane_id();
-    const int r = w * 32 + (l >> 1);
-    const int q = (l & 1) ^ swz(r);
+    const int r = w * ROWS_PER_WAVE + l / CHUNKS;
+    const int q = (l % CHUNKS) ^ swz(r);
+    const uint32_t a0 = (uint32_t)(((row0 + r) * c.K + 8 * q) * 2);
+    const uint32_t b0 = (uint32_t)(((col0 + r) * c.K + 8 * q) * 2);
     Lane ln;
-    ln.a[0] = (uint32_t)(((row0 + r) * c.K + 8 * q) * 2);
-    ln.b[0] = (uint32_t)(((col0 + r) * c.K + 8 * q) * 2);
+#pragma unroll
+    for (int i = 0; i < LOADS_A; ++i)
+      ln.a[i] = a0 + (uint32_t)(i * WAVES * ROWS_PER_WAVE) * (uint32_t)c.K * 2u;
+#pragma unroll
+    for (int i = 0; i < LOADS_B; ++i)
+      ln.b[i] = b0 + (uint32_t)(i * WAVES * ROWS_PER_WAVE) * (uint32_t)c.K * 2u;
     return ln;
   }
   // Scalar parts of stage t's loads into ring slot `slot` (as in the 256x256
@@ -126,25 +148,27 @@ struct EngBf16x128 {
   }
   // Byte offset inside a ring slot of load i's piece (thread t's 16 bytes of
   // load i land at slot + dma_lds_off(i) + 16 t).
-  static constexpr uint32_t dma_lds_off(int i) { return i == 0 ? 0u : (uint32_t)A_STAGE; }
+  static constexpr uint32_t dma_lds_off(int i) {
+    return (uint32_t)(i < LOADS_A ? i * WAVES * 1024 : A_STAGE + (i - LOADS_A) * WAVES * 1024);
+  }
   static __device__ __forceinline__ void issue_one(const Ctx&, const Lane& ln, const Dst& d,
                                                    int i) {
-    if (i == 0)
-      dma_x4(d.ra, d.lds, dma_lds_off(0), ln.a[0], d.k);
+    if (i < LOADS_A)
+      dma_x4(d.ra, d.lds, dma_lds_off(i), ln.a[i], d.k);
     else
-      dma_x4(d.rb, d.lds, dma_lds_off(1), ln.b[0], d.k);
+      dma_x4(d.rb, d.lds, dma_lds_off(i), ln.b[i - LOADS_A], d.k);
   }
 
-  // Operands of one stage (16 k values): one 16-byte read per 32-row block of
-  // A and per 32-column block of Bt; lanes 0-31 take k 0-7 of their row,
-  // lanes 32-63 k 8-15.
+  // Operands of k-step j (16 k values) of a stage: one 16-byte read per
+  // 32-row block of A and per 32-column block of Bt; lanes 0-31 take k 0-7
+  // of the step, lanes 32-63 k 8-15.
   struct Frag {
     bf16x8 a[2], b[2];
   };
-  static __device__ __forceinline__ void load_frag(const char* sbase, Frag& f) {
+  static __device__ __forceinline__ void load_frag(const char* sbase, int j, Frag& f) {
     const int w = threadIdx.x >> 6, l = lane_id();
     const int wm = w & 1, wn = w >> 1;
-    const int lr = l & 31, q = l >> 5;
+    const int lr = l & 31, q = 2 * j + (l >> 5);
     const char* bbase = sbase + A_STAGE;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
@@ -158,28 +182,31 @@ struct EngBf16x128 {
     }
   }
 
-  // One group: the two k-stages in ring slots slot and slot+1, 8 MFMAs per
-  // wave in ascending k, the second stage's operands read while the first
-  // stage's MFMAs run. `pre` runs first (false abandons the group before any
-  // accumulator changes); `mid(i)`, i = 0..GROUP*LOADS-1, runs after MFMA
-  // 2i+1: the stage loops issue the next group's load i there.
+  static constexpr int J = KS / 16;  // MFMA k-steps per stage
+
+  // One group: the two k-stages in ring slots slot and slot+1, 4 MFMAs per
+  // k-step per wave in ascending k, the operands of k-step j+1 read while
+  // k-step j's MFMAs run. `pre` runs first (false abandons the group before
+  // any accumulator changes); `mid(i)`, i = 0..GROUP*LOADS-1, runs after
+  // MFMA 2i+1: the stage loops issue the next group's load i there.
   template <class Pre, class Mid>
   static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
                                                  Pre&& pre, Mid&& mid) {
     const char* gbase = ring + slot * STAGE;
+    constexpr int JG = J * GROUP;
     Frag f[2];
     if (!pre()) return false;
-    load_frag(gbase, f[0]);
+    load_frag(gbase, 0, f[0]);
 #pragma unroll
-    for (int j = 0; j < GROUP; ++j) {
-      if (j + 1 < GROUP) load_frag(gbase + (j + 1) * STAGE, f[(j + 1) & 1]);
+    for (int j = 0; j < JG; ++j) {
+      if (j + 1 < JG) load_frag(gbase + ((j + 1) / J) * STAGE, (j + 1) % J, f[(j + 1) & 1]);
       const Frag& c = f[j & 1];
 #pragma unroll
       for (int m = 0; m < 4; ++m) {
         const int rb = m >> 1, cb = m & 1;
         acc.c[rb][cb] =
             __builtin_amdgcn_mfma_f32_32x32x16_bf16(c.a[rb], c.b[cb], acc.c[rb][cb], 0, 0, 0);
-        if (m & 1) {
+        if ((m & 1) && j * 2 + (m >> 1) < GROUP * LOADS) {
           __builtin_amdgcn_sched_barrier(0);
           mid(j * 2 + (m >> 1));
           __builtin_amdgcn_sched_barrier(0);
@@ -225,5 +252,8 @@ struct EngBf16x128 {
     return (rr >> 5) * 64 + p * 32 + (rr & 31);
   }
 };
+
+using EngBf16x128 = EngBf16x128T<16>;     // 16-deep stages: up to 4 blocks per CU
+using EngBf16x128K32 = EngBf16x128T<32>;  // 32-deep stages: up to 2 blocks per CU
 
 }  // namespace apk

@@ -231,6 +231,10 @@ extern "C" int apk_persistent_gemm(int engine, const void* A, const void* B,
       return launch_persistent_gemm<EngBf16x128>(A, B, C, M, N, K, k_chunk,
                                                  next_task, log, blocks,
                                                  as_stream(stream));
+    case APK_ENGINE_BF16X128K32:
+      return launch_persistent_gemm<EngBf16x128K32>(A, B, C, M, N, K, k_chunk,
+                                                    next_task, log, blocks,
+                                                    as_stream(stream));
     default:
       set_error("persistent_gemm: unknown engine %d", engine);
       return APK_EINVAL;
@@ -253,6 +257,7 @@ extern "C" int apk_persistent_gemm_occupancy(int engine, int* blocks_per_cu) {
     }
     case APK_ENGINE_BF16X256: return occupancy_of<EngBf16x256>(blocks_per_cu);
     case APK_ENGINE_BF16X128: return occupancy_of<EngBf16x128>(blocks_per_cu);
+    case APK_ENGINE_BF16X128K32: return occupancy_of<EngBf16x128K32>(blocks_per_cu);
     default:
       set_error("occupancy: unknown engine %d", engine);
       return APK_EINVAL;
@@ -276,6 +281,9 @@ extern "C" int apk_persistent_gemm_noalloc(int engine, const void* A, const void
       break;
     case APK_ENGINE_BF16X128:
       rc = validate_persistent_gemm<EngBf16x128>(A, B, C, M, N, K, k_chunk, blocks);
+      break;
+    case APK_ENGINE_BF16X128K32:
+      rc = validate_persistent_gemm<EngBf16x128K32>(A, B, C, M, N, K, k_chunk, blocks);
       break;
     default:
       set_error("persistent_gemm_noalloc: unknown engine %d", engine);
@@ -307,6 +315,9 @@ extern "C" int apk_urgent_gemm(int engine, const void* A, const void* B, float* 
       return launch_urgent_tiles<EngBf16x256>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));
     case APK_ENGINE_BF16X128:
       return launch_urgent_tiles<EngBf16x128>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));
+    case APK_ENGINE_BF16X128K32:
+      return launch_urgent_tiles<EngBf16x128K32>(A, B, C, M, N, K, start_gt, end_gt,
+                                                 as_stream(stream));
     default:
       set_error("urgent_gemm: unknown engine %d", engine);
       return APK_EINVAL;

@@ -849,6 +849,8 @@ extern "C" int apk_persistent_yield(int engine, int poll, int oracle,
       return launch_e<EngBf16x256>(poll, oracle, params, blocks, as_stream(stream));
     case APK_ENGINE_BF16X128:
       return launch_e<EngBf16x128>(poll, oracle, params, blocks, as_stream(stream));
+    case APK_ENGINE_BF16X128K32:
+      return launch_e<EngBf16x128K32>(poll, oracle, params, blocks, as_stream(stream));
     default:
       set_error("persistent_yield: unknown engine %d", engine);
       return APK_EINVAL;
@@ -862,6 +864,7 @@ extern "C" long long apk_yield_ckpt_floats(int engine) {
     case APK_ENGINE_MFMA128: return Ckpt<EngMfma128>::SLOT_FLOATS;
     case APK_ENGINE_BF16X256: return Ckpt<EngBf16x256>::SLOT_FLOATS;
     case APK_ENGINE_BF16X128: return Ckpt<EngBf16x128>::SLOT_FLOATS;
+    case APK_ENGINE_BF16X128K32: return Ckpt<EngBf16x128K32>::SLOT_FLOATS;
     default: return -1;
   }
 }
@@ -903,6 +906,8 @@ extern "C" int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_
     case APK_ENGINE_MFMA128: return yield_occupancy_of<EngMfma128>(poll, blocks_per_cu);
     case APK_ENGINE_BF16X256: return yield_occupancy_of<EngBf16x256>(poll, blocks_per_cu);
     case APK_ENGINE_BF16X128: return yield_occupancy_of<EngBf16x128>(poll, blocks_per_cu);
+    case APK_ENGINE_BF16X128K32:
+      return yield_occupancy_of<EngBf16x128K32>(poll, blocks_per_cu);
     default:
       set_error("occupancy: engine %d", engine);
       return APK_EINVAL;

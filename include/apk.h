@@ -42,6 +42,9 @@ enum {
  *             256 threads, 16-deep k-stages, 33 KiB of LDS: runs at 2 and
  *             4 blocks per CU, where the 256x256 tile cannot (configs[4] of
  *             the reference's study at 2 and 4 blocks/CU).
+ *  BF16X128K32 : the same 128x128 bf16 tile with 32-deep k-stages (64 KiB
+ *             of LDS): up to 2 blocks per CU, and faster than BF16X128 at
+ *             1 and 2 blocks per CU; C is bit-identical to BF16X128's.
  * For the fp32 engines A is M x K and B is K x N, row-major fp32.
  */
 enum {
@@ -49,7 +52,8 @@ enum {
   APK_ENGINE_MFMA128 = 1,
   APK_ENGINE_BF16X256 = 2,
   APK_ENGINE_BF16X128 = 3,
-  APK_ENGINE_COUNT = 4
+  APK_ENGINE_BF16X128K32 = 4,
+  APK_ENGINE_COUNT = 5
 };
 
 /* Per-step timing record; layout of TileRecord (src/tile.cuh:37-42). start

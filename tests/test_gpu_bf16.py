@@ -24,7 +24,7 @@ from gpu_util import assert_queue_drained, dev, say
 
 pytestmark = pytest.mark.gpu
 
-ENGS = ["bf16x256", "bf16x128"]
+ENGS = ["bf16x256", "bf16x128", "bf16x128k32"]
 
 
 def tile_of(apk, eng):
@@ -97,13 +97,32 @@ def test_bf16_bit_identical_across_chunks_and_workers(torch_gpu, apk, name):
         assert np.array_equal(C0.view(np.uint32), C1.view(np.uint32)), (kc, blocks)
 
 
+@pytest.mark.parametrize("K", [512, 160])
+def test_bf16x128_stage_depths_bit_identical(torch_gpu, apk, K):
+    """The 128x128 bf16 tile with 16-deep and with 32-deep k-stages forms
+    every output's sum in the same k order, so C is bit-identical; K = 160
+    is 10 stages of 16 but 5 of 32 (the last pair's second stage zeros)."""
+    say(f"bf16x128 vs bf16x128k32, M=N=256 K={K}")
+    A_bits, A, B_bits, B = oracle.fill_normal_bf16(13, 256, 256, K)
+    Bt_bits = np.ascontiguousarray(B_bits.T)
+    C16, _ = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=K, blocks=3,
+                      eng=apk.ENGINES["bf16x128"])
+    C32, _ = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=K, blocks=3,
+                      eng=apk.ENGINES["bf16x128k32"])
+    assert np.array_equal(C16.view(np.uint32), C32.view(np.uint32))
+    assert oracle.rel_frobenius(C32, oracle.gemm_f64(A, B, threads=8)) <= 1e-5
+
+
 def test_bf16x128_runs_at_4_blocks_per_cu(apk):
     """The 128x128 tile's plain and yield kernels fit 4 blocks per CU (128
-    registers and 33 KiB of LDS per block); the 256x256 tile fits one."""
+    registers and 33 KiB of LDS per block) with 16-deep k-stages and 2 with
+    32-deep ones (64 KiB); the 256x256 tile fits one."""
     e128, e256 = apk.ENGINES["bf16x128"], apk.ENGINES["bf16x256"]
-    assert apk.occupancy(e128) >= 4
+    e128d = apk.ENGINES["bf16x128k32"]
+    assert apk.occupancy(e128) >= 4 and apk.occupancy(e128d) >= 2
     for poll in (apk.POLL_OFF, apk.POLL_CHUNK, apk.POLL_STAGE, apk.POLL_ISSUE):
         assert apk.yield_occupancy(e128, poll) >= 4, poll
+        assert apk.yield_occupancy(e128d, poll) >= 2, poll
     assert apk.occupancy(e256) == 1
 
 
@@ -190,7 +209,7 @@ class Bf16Job:
 
 # (engine, blocks per CU or a block count): the 256x256 tile on 64 workers,
 # the 128x128 tile at 2 and 4 blocks on every CU.
-JOBS = [("bf16x256", 64), ("bf16x128", "2/CU"), ("bf16x128", "4/CU")]
+JOBS = [("bf16x256", 64), ("bf16x128", "2/CU"), ("bf16x128", "4/CU"), ("bf16x128k32", "2/CU")]
 
 
 @pytest.fixture(scope="module", params=JOBS, ids=lambda j: f"{j[0]}-{j[1]}".replace("/", "per"))

@@ -43,7 +43,7 @@ def test_urgent_fp32_matches_persistent(torch_gpu, apk, name):
     assert 0 < start <= end
 
 
-@pytest.mark.parametrize("name", ["bf16x256", "bf16x128"])
+@pytest.mark.parametrize("name", ["bf16x256", "bf16x128", "bf16x128k32"])
 def test_urgent_bf16_matches_persistent(torch_gpu, apk, name):
     eng = apk.ENGINES[name]
     T = apk.geometry(eng).tile_m
