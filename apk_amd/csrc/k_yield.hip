@@ -624,10 +624,9 @@ k_persistent_yield(const apk_yield_params) {
         const int64_t tSave = save_state(dst, true, false, true);
         const int rkind = P().resume == APK_RESUME_RESTART ? 0
                           : P().resume == APK_RESUME_CKPT_FULL ? 2 : 1;
-        // Every thread's checkpoint stores have completed at this XCD's L2;
-        // after the barrier, the agent-scope release in rq_publish (one L2
-        // write-back, by thread 0 alone) makes all of them visible device-wide
-        // before the entry is published.
+        // Every thread's checkpoint stores, written through the L2, have
+        // completed: after the barrier, thread 0 publishes the entry (its
+        // fields, then their completion, then the sequence number).
         wait_vmcnt<0>();
         lds_sync();
         if (tid == 0) {
