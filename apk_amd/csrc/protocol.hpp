@@ -123,14 +123,24 @@ APK_PROTO_FN unsigned rq_reserve(unsigned* ctl, unsigned cap, const int* entries
   }
   return t;
 }
-// Claims the oldest reserved ticket, or RQ_NONE if none.
+// Claims the oldest reserved ticket, or RQ_NONE if none. A try is one
+// compare-and-swap, retried from the head it returns; the tail (which only
+// grows) is read again only when the head has caught up with the copy in
+// hand. With a whole XCD's blocks, or a whole continuation grid, claiming at
+// once, tries that re-read both counters took three device-wide round trips
+// each, and the claims went out one per three round trips.
 template <class P>
 APK_PROTO_FN unsigned rq_pop(unsigned* ctl) {
+  unsigned h = P::load(&ctl[0]);
+  unsigned t = P::load(&ctl[1]);
   for (;;) {
-    const unsigned h = P::load(&ctl[0]);
-    const unsigned t = P::load(&ctl[1]);
-    if (h >= t) return RQ_NONE;
-    if (P::cas(&ctl[0], h, h + 1) == h) return h;
+    if (h >= t) {
+      t = P::load(&ctl[1]);
+      if (h >= t) return RQ_NONE;
+    }
+    const unsigned seen = P::cas(&ctl[0], h, h + 1);
+    if (seen == h) return h;
+    h = seen;
   }
 }
 // Once the checkpoint stores of the whole block are complete: the entry's
