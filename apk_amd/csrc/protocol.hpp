@@ -87,7 +87,8 @@ struct TaskQueue {
 
 // ---------------------------------------------------------------------------
 // Resume queue of the retreat arm: a bounded ring of `cap` entries, tickets
-// [head, tail) in ctl[0..1]. Entry i = {task, stage, seq, kind << 8 |
+// [head, tail) in ctl[0..1], and in ctl[2] the count of reserved tickets not
+// yet claimed. Entry i = {task, stage, seq, kind << 8 |
 // domain} with its checkpoint slot i; ticket t uses entry t % cap. `seq`
 // orders the entry's rounds (bounded MPMC ring with per-entry sequence
 // numbers): seq == t means free for ticket t, t + 1 published by ticket t's
@@ -115,33 +116,34 @@ APK_PROTO_FN unsigned rq_reserve(unsigned* ctl, unsigned cap, const int* entries
                                  int64_t wait = RQ_WAIT_TICKS) {
   const unsigned t = P::fetch_add(&ctl[1], 1u);
   const int* en = entries + (size_t)(t % cap) * 4;
-  if (P::load(&en[2]) == (int)t) return t;
-  const int64_t deadline = P::ticks() + wait;
-  while (P::load(&en[2]) != (int)t) {
-    if (P::ticks() > deadline) return t | RQ_FULL;
-    P::pause();
+  if (P::load(&en[2]) != (int)t) {
+    const int64_t deadline = P::ticks() + wait;
+    while (P::load(&en[2]) != (int)t) {
+      if (P::ticks() > deadline) return t | RQ_FULL;
+      P::pause();
+    }
   }
+  P::fetch_add(&ctl[2], 1u);  // one more ticket to claim
   return t;
 }
-// Claims the oldest reserved ticket, or RQ_NONE if none. A try is one
-// compare-and-swap, retried from the head it returns; the tail (which only
-// grows) is read again only when the head has caught up with the copy in
-// hand. With a whole XCD's blocks, or a whole continuation grid, claiming at
-// once, tries that re-read both counters took three device-wide round trips
-// each, and the claims went out one per three round trips.
+// Claims the oldest reserved ticket, or RQ_NONE if none is waiting. A claim
+// takes one from ctl[2] with a fetch-and-add (and gives it back if there was
+// none), then its ticket from the head with another: it never fails and
+// retries, however many blocks claim at once. (A compare-and-swap loop on the
+// head let one claim through per round trip; with a whole XCD at a tile
+// boundary, then a whole continuation grid, claiming at once, it kept them
+// from their polls for up to 0.5 ms.) ctl[2] dips below zero while claims
+// that found none give theirs back, and no claim takes a ticket that was not
+// reserved: a decrement succeeds only from 1 or more, which with the
+// give-backs still outstanding means more reservations than claims.
 template <class P>
 APK_PROTO_FN unsigned rq_pop(unsigned* ctl) {
-  unsigned h = P::load(&ctl[0]);
-  unsigned t = P::load(&ctl[1]);
-  for (;;) {
-    if (h >= t) {
-      t = P::load(&ctl[1]);
-      if (h >= t) return RQ_NONE;
-    }
-    const unsigned seen = P::cas(&ctl[0], h, h + 1);
-    if (seen == h) return h;
-    h = seen;
+  if ((int)P::load(&ctl[2]) <= 0) return RQ_NONE;
+  if ((int)P::fetch_add(&ctl[2], ~0u) <= 0) {
+    P::fetch_add(&ctl[2], 1u);
+    return RQ_NONE;
   }
+  return P::fetch_add(&ctl[0], 1u);
 }
 // Once the checkpoint stores of the whole block are complete: the entry's
 // fields, the publish fence, then seq = ticket + 1. On gfx950 the slot is

@@ -63,7 +63,7 @@ YieldRig::YieldRig(const RigShape& s, const std::vector<uint8_t>& A,
   if (s.retreatCap) {
     dRetreatCount_ = dalloc<int>((size_t)E * APK_RETREAT_DOMAINS);
     dRetreatGT_ = dalloc<long long>(2 * (size_t)E);
-    dRqCtl_ = dalloc<unsigned>(2);
+    dRqCtl_ = dalloc<unsigned>(3);
     dRqEntry_ = dalloc<int>((size_t)s.retreatCap * 4);
     dRqSlots_ = dalloc<float>((size_t)s.retreatCap * apk_yield_ckpt_floats(s.engine));
   }
@@ -205,7 +205,7 @@ void YieldRig::resetRetreat() {
   std::vector<long long> gt(2 * (size_t)E, 0);
   for (int e = 0; e < E; ++e) gt[2 * (size_t)e] = INT64_MAX;
   HIP_CHECK(hipMemcpy(dRetreatGT_, gt.data(), gt.size() * 8, hipMemcpyHostToDevice));
-  HIP_CHECK(hipMemset(dRqCtl_, 0, 2 * sizeof(unsigned)));
+  HIP_CHECK(hipMemset(dRqCtl_, 0, 3 * sizeof(unsigned)));
   // entry i = {task, stage, seq, kind << 8 | domain}; seq = i: free for ticket i
   std::vector<int> en((size_t)s_.retreatCap * 4, 0);
   for (unsigned i = 0; i < s_.retreatCap; ++i) en[(size_t)i * 4 + 2] = (int)i;

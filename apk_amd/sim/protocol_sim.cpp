@@ -132,7 +132,7 @@ struct Sim {
   std::vector<int> exec;                     // per task: completions
   std::vector<uint64_t> result;              // per task
   std::vector<int> retreatCount;             // per event x domain
-  unsigned rqCtl[2] = {0, 0};
+  unsigned rqCtl[3] = {0, 0, 0};
   std::vector<int> rqEntry;                  // cap x 4
   std::vector<Ckpt> rqSlot;                  // cap
   std::atomic<long> retreats{0}, resumed{0}, refused{0}, lost{0}, yields{0};

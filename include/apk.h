@@ -308,7 +308,8 @@ typedef struct apk_yield_params {
   int* retreat_count;            /* [events * APK_RETREAT_DOMAINS], 0 at job start */
   long long* retreat_gt;         /* [2 * events] or NULL: [2e] earliest checkpoint
                                     start (host sets INT64_MAX), [2e+1] latest exit (0) */
-  unsigned int* rq_ctl;          /* resume queue tickets: [0] head, [1] tail; 0 at job start */
+  unsigned int* rq_ctl;          /* resume queue tickets, 3 words: [0] head, [1] tail,
+                                    [2] reserved tickets not yet claimed; 0 at job start */
   int* rq_entry;                 /* [rq_capacity * 4], a ring: ticket t uses entry t %
                                     rq_capacity = {task, stage, seq, kind << 8 | domain
                                     (xcd * 4 + shader engine of the retreating block)};

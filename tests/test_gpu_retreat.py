@@ -87,7 +87,7 @@ class RetreatJob:
         self.set_gt = T.zeros(1, dtype=i64, device="cuda")
         self.rcount = T.zeros(apk.RETREAT_DOMAINS, dtype=i32, device="cuda")
         self.rgt = T.zeros(2, dtype=i64, device="cuda")
-        self.rq_ctl = T.zeros(2, dtype=i32, device="cuda")
+        self.rq_ctl = T.zeros(3, dtype=i32, device="cuda")
         self.rq_entry = T.zeros(4 * self.RB, dtype=i32, device="cuda")
         self.rq_slots = T.zeros(self.RB * apk.ckpt_floats(engine), dtype=T.float32, device="cuda")
         rows = 2 * self.blocks + self.RB
