@@ -26,11 +26,6 @@ __device__ __forceinline__ unsigned fetch_add_u32(unsigned* p, unsigned v) {
 __device__ __forceinline__ int fetch_add_i32(int* p, int v) {
   return __hip_atomic_fetch_add(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-__device__ __forceinline__ int cas_i32(int* p, int expected, int desired) {
-  __hip_atomic_compare_exchange_strong(p, &expected, desired, __ATOMIC_RELAXED,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return expected;  // previous value
-}
 __device__ __forceinline__ void atomic_max_u64(unsigned long long* p,
                                                unsigned long long v) {
   __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -40,11 +35,6 @@ __device__ __forceinline__ void atomic_min_i64(long long* p, long long v) {
 }
 __device__ __forceinline__ void atomic_max_i64(long long* p, long long v) {
   __hip_atomic_fetch_max(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ unsigned cas_u32(unsigned* p, unsigned expected, unsigned desired) {
-  __hip_atomic_compare_exchange_strong(p, &expected, desired, __ATOMIC_RELAXED,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return expected;  // previous value
 }
 
 // ---------------------------------------------------------------------------

@@ -18,9 +18,6 @@ struct DevPlat {
   static __device__ __forceinline__ unsigned fetch_add(unsigned* p, unsigned v) {
     return fetch_add_u32(p, v);
   }
-  static __device__ __forceinline__ unsigned cas(unsigned* p, unsigned e, unsigned d) {
-    return cas_u32(p, e, d);
-  }
   static __device__ __forceinline__ unsigned load(const unsigned* p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
@@ -29,9 +26,6 @@ struct DevPlat {
   }
   static __device__ __forceinline__ void store(int* p, int v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  static __device__ __forceinline__ void release() {
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
   }
   // The resume ring's payload (checkpoint slot, entry fields) is written
   // through with agent-coherent stores (CPOL_SC1 / relaxed agent atomics),

@@ -13,10 +13,9 @@
 // inline for the kernels, plain inline for the simulator) and passes a
 // platform P with static members:
 //   unsigned fetch_add(unsigned*, unsigned)   relaxed, device-wide
-//   unsigned cas(unsigned*, unsigned e, unsigned d) -> previous value
 //   unsigned load(const unsigned*), int load(const int*)   relaxed
 //   void store(int*, int)                     relaxed
-//   void release(), acquire()                 device-wide fences
+//   void acquire()                            device-wide acquire fence
 //   void publish_fence()                      orders the caller's earlier
 //                                             payload stores (written by the
 //                                             platform's publishing stores)

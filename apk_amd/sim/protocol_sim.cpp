@@ -52,14 +52,9 @@ struct HostPlat {
   static unsigned fetch_add(unsigned* p, unsigned v) {
     return __atomic_fetch_add(p, v, __ATOMIC_RELAXED);
   }
-  static unsigned cas(unsigned* p, unsigned e, unsigned d) {
-    __atomic_compare_exchange_n(p, &e, d, false, __ATOMIC_RELAXED, __ATOMIC_RELAXED);
-    return e;
-  }
   static unsigned load(const unsigned* p) { return __atomic_load_n(p, __ATOMIC_RELAXED); }
   static int load(const int* p) { return __atomic_load_n(p, __ATOMIC_RELAXED); }
   static void store(int* p, int v) { __atomic_store_n(p, v, __ATOMIC_RELAXED); }
-  static void release() { __atomic_thread_fence(__ATOMIC_RELEASE); }
   static void acquire() { __atomic_thread_fence(__ATOMIC_ACQUIRE); }
   // host payload stores are plain: publishing them takes a release fence
   static void publish_fence() { __atomic_thread_fence(__ATOMIC_RELEASE); }
