@@ -10,7 +10,8 @@ them. Pinned:
   * C bit-identical to the unpreempted run, and every task's fingerprint
     equal to its tile's fingerprint in that run (fp32 MFMA128 and bf16);
   * exactly-once: every task id completed once, 32 * ceil(R/32) tickets
-    reserved and popped, no resume error;
+    reserved and popped, none left counted as unclaimed, no resume error --
+    also with every worker retreating at once;
   * the urgent output bit-identical to the same GEMM run alone;
   * the device timeline is ordered: flag raised <= first checkpoint start
     <= last retreat exit.
@@ -182,6 +183,7 @@ def _check(job, ref, r):
     assert t0 < r["set_gt"] < t1, (f"flag raised at {r['set_gt']} outside the background run "
                                    f"[{t0}, {t1}]: the two streams did not run concurrently")
     assert head == tail == job.RB, (head, tail, r["set_gt"] - t0, t1 - t0, r["rgt"] - t0)
+    assert int(r["ctl"][2]) == 0, f"{int(r['ctl'][2])} reserved tickets left unclaimed"
     assert int(st[:, 5].sum()) == job.RB and int(st[:, 6].sum()) == job.RB
     assert int(st[:, 7].sum()) == 0, "resume entries lost"
     assert r["set_gt"] > 0 and r["set_gt"] <= r["rgt"][0] <= r["rgt"][1]
@@ -218,3 +220,24 @@ def test_retreat_bf16(torch_gpu, apk):
     ref = job.run(apk.POLL_STAGE, apk.RESUME_CKPT_FULL, preempt=False)
     for resume in (apk.RESUME_CKPT_FULL, apk.RESUME_CKPT_ACC):
         _check(job, ref, job.run(apk.POLL_STAGE, resume))
+
+
+@pytest.mark.parametrize("resume", [1, 2])
+def test_retreat_every_worker(torch_gpu, apk, resume):
+    """Every worker retreats at once (retreat = the grid): 256 tickets reserved
+    together, then claimed together by the 256-block continuation."""
+    say(f"building mfma128 mass-retreat job M=N=1024 K=4096 kc=128, resume={resume}")
+    blocks = apk.device_info().cu_count
+    job = RetreatJob(torch_gpu, apk, apk.ENGINE_MFMA128, 1024, 1024, 4096, 128, 256, 256, 256,
+                     passes=16, retreat=blocks)
+    ref = job.run(apk.POLL_STAGE, apk.RESUME_CKPT_FULL, preempt=False)
+    r = job.run(apk.POLL_STAGE, resume)
+    assert (_bits(r["C"]) == _bits(ref["C"])).all(), "C differs from the unpreempted run"
+    assert (r["exec"] == 1).all(), "exactly-once violated"
+    head, tail, left = (int(x) for x in r["ctl"])
+    st = r["stats"]
+    assert head == tail and left == 0, (head, tail, left)
+    # every block on a CU of its own, 8 per (XCD, shader engine) domain: all retreat
+    assert tail == job.RB == blocks, (tail, job.RB)
+    assert int(st[:, 5].sum()) == tail and int(st[:, 6].sum()) == tail
+    assert int(st[:, 7].sum()) == 0, "resume entries lost"
