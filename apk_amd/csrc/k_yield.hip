@@ -341,8 +341,13 @@ k_persistent_yield(const apk_yield_params) {
           // Accumulators hold stages [0, s); stages s, s+1 (issue sites: every
           // live stage) go to ring slots slot, slot+1, ... (from the
           // checkpoint, or s, s+1 fetched again), and the site at s gets a
-          // fresh sample.
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+          // fresh sample. A resume-queue slot was written by another block,
+          // maybe on another XCD: acquire at agent scope (an invalidate of
+          // this XCD's L2) before reading it. The cooperative arm reads back
+          // what the same threads stored to the same addresses, which needs
+          // no fence, and an L2 invalidate per wave would also drop the
+          // operand panels the XCD's other blocks are reading.
+          if constexpr (retreatArm) __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
           Ckpt<E>::load_acc(acc, src);
           if (srcKind == FULL) {
             Ckpt<E>::load_ring(ring, src, slot, live_at(s));
