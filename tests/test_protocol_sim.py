@@ -50,6 +50,20 @@ def test_retreat_quota_over_fewer_domains():
     assert rc == 0, line
 
 
+@pytest.mark.parametrize("resume", ["full", "acc", "restart"])
+def test_retreat_every_worker_many_events(resume):
+    """Every one of 64 blocks retreats at each of up to 40 generations: whole
+    grids reserve tickets together and whole continuations claim them
+    together, the case a claim loop of compare-and-swaps serialised."""
+    rc, line, f = run("--arm", "retreat", "--resume", resume, "--seed", 2, "--blocks", 64,
+                      "--retreat", 64, "--passes", 32, "--events", 40, "--mean-gap-us", 500,
+                      "--work-ns", 20000)
+    assert rc == 0, line
+    fired = int(re.search(r"events fired=(\d+)", line).group(1))
+    n = int(re.search(r"retreats (\d+)", line).group(1))
+    assert fired >= 20 and n >= 10 * 64 and f"resumed {n}" in line, line
+
+
 def test_coop_poll_every_4():
     rc, line, _ = run("--arm", "coop", "--poll-every", 4, "--seed", 7)
     assert rc == 0, line
