@@ -87,12 +87,22 @@ k_persistent_yield(const apk_yield_params) {
       make_rsrc((const char*)P().flag + (size_t)(bid % copies()) * APK_FLAG_STRIDE, 4);
   const bool isSetter = P().flag_set != nullptr && P().sched != nullptr && bid == 0;
   constexpr bool retreatArm = RETREAT && POLL != APK_POLL_OFF;
-  // A retreat-arm continuation is the set of blocks that retreats, all of
-  // it, at the next generation: at its stage sites it reads the flag itself
+  auto domain = [&] { return (int)xcc_id() * APK_SES_PER_XCD + (int)se_id(); };
+  auto quota = [&] { return (P().retreat + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS; };
+  // Retreat arm: whether this block may still retreat at a later generation
+  // (uniform). The first grid's blocks register in their (XCD, shader
+  // engine) domain as they start, in the row of retreat_count after the
+  // events' rows: the first ceil(R / 32) of each domain are the ones that
+  // retreat at generation 1. A continuation that follows an earlier
+  // generation retreats, all of it, at the next one. Blocks that may retreat
+  // poll at every site; the others only at the first stage of each new task
+  // (where the stop sentinel is seen), so the every-site polls cost the
+  // background on 32 * ceil(R / 32) blocks instead of on all of them.
+  bool mayRetreat = false;
+  // The blocks that may retreat read the flag itself at their stage sites
   // (one load, one barrier) rather than the sample issued a stage (or a pair
   // of stages) earlier, to act that much sooner.
-  const bool syncPoll = retreatArm && !SYS && POLL == APK_POLL_STAGE &&
-                        P().continuation != 0 && P().launch_epoch > 0;
+  bool syncPoll = false;
   const int* myFlag = (const int*)((const char*)P().flag + (size_t)(bid % copies()) * APK_FLAG_STRIDE);
 
   const uint32_t wl = wave_lds(ring);
@@ -102,6 +112,18 @@ k_persistent_yield(const apk_yield_params) {
   if (tid < 2) s_setter[tid] = 0;
   if (P().run_gt && bid == 0 && tid == 0) P().run_gt[0] = wall_ticks();
   __syncthreads();
+  if constexpr (retreatArm) {
+    if (P().continuation == 0) {
+      if (tid == 0)
+        s_u32 = (unsigned)fetch_add_i32(
+            &P().retreat_count[(size_t)P().num_events * APK_RETREAT_DOMAINS + domain()], 1);
+      __syncthreads();
+      mayRetreat = (int)uniform(s_u32) < quota();
+      __syncthreads();
+    } else {
+      mayRetreat = P().launch_epoch > 0 && P().launch_epoch < P().num_events;
+    }
+  }
 
   int lastSeen = 0;     // uniform: every thread derives it from the same samples
   int fLatest = 0;      // freshest landed sample, for the task-boundary stop check
@@ -309,10 +331,15 @@ k_persistent_yield(const apk_yield_params) {
       else
         return (E::GROUP == 2 || S - st >= 2) ? 2 : S - st;
     };
+    int siteStride = pollStride;  // uniform: the gap between this job's sites
     for (;;) {  // (re)entries of the stage loop of this job
       if (srcKind != AS_IS) {
+        syncPoll = retreatArm && !SYS && POLL == APK_POLL_STAGE && mayRetreat;
+        siteStride = retreatArm && !mayRetreat ? S + 2 : pollStride;
         if (!pollable) {
           nextSite = S + 2;
+        } else if (retreatArm && !mayRetreat) {
+          nextSite = s == 0 ? 0 : S + 2;  // a new task's first stage only
         } else if (POLL == APK_POLL_CHUNK && pollEvery > 1) {
           // the next chunk boundary c at or after s whose running count
           // chunksDone + c is a multiple of poll_every
@@ -426,7 +453,7 @@ k_persistent_yield(const apk_yield_params) {
                 break;
               }
             }
-            nextSite += pollStride;
+            nextSite += siteStride;
           }
           const int aheadSlot = slot_after_next(slot);
           const bool carry = s + 1 == nextSite;  // s+1 is a site
@@ -452,7 +479,7 @@ k_persistent_yield(const apk_yield_params) {
           // polled at all.
           const bool site = POLL != APK_POLL_OFF && s == nextSite;
           const bool check = site && s != siteDone;
-          if (site) nextSite += pollStride;
+          if (site) nextSite += siteStride;
           auto poll = [&]() -> bool {
             if (!check) return true;
             int f = uniform(flagring[site_flag(slot)]);
@@ -601,29 +628,24 @@ k_persistent_yield(const apk_yield_params) {
         // earlier generation, all of it -- it holds the CUs the previous
         // generation freed, and it must complete for the next continuation
         // (queued behind it) to start.
-        const int quota = (P().retreat + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS;
-        const int dom = (int)xcc_id() * APK_SES_PER_XCD + (int)se_id();
         const int role = proto::retreat_role(P().continuation != 0, P().launch_epoch, f);
+        const bool mine = mayRetreat;  // by quota: registered among the first at start
+        if (P().continuation == 0) mayRetreat = false;  // no later generation is its turn
         if (role == proto::RETREAT_NONE) continue;  // not this block's turn: keep working
-        const bool newest = role == proto::RETREAT_ALL;
+        if (role == proto::RETREAT_BY_QUOTA && !mine) continue;
         unsigned t = RQ_NONE;
         if (tid == 0) {
-          int* rc = &P().retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + dom];
-          int c = 0;
-          if (newest)  // counted, but the count decides nothing: no round trip
-            __hip_atomic_fetch_add(rc, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          else
-            c = fetch_add_i32(rc, 1);
-          if (newest || c < quota) {
-            t = rq_reserve(P().rq_ctl, P().rq_capacity, P().rq_entry);
-            if (t & RQ_FULL) {  // the ring stayed full: keep working
-              stat(ST_ERRORS, 1);
-              t = RQ_NONE;
-            }
+          // counted (the retreats of generation f per domain), no round trip
+          __hip_atomic_fetch_add(&P().retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + domain()],
+                                 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          t = rq_reserve(P().rq_ctl, P().rq_capacity, P().rq_entry);
+          if (t & RQ_FULL) {  // the ring stayed full: keep working
+            stat(ST_ERRORS, 1);
+            t = RQ_NONE;
           }
         }
         const unsigned tk = bcast(t);
-        if (tk == RQ_NONE) continue;  // quota taken (or queue full): keep working
+        if (tk == RQ_NONE) continue;  // the ring stayed full: keep working
         float* dst = P().rq_slots + (size_t)(tk % P().rq_capacity) * Ckpt<E>::SLOT_FLOATS;
         // always drain: nothing may land in LDS after the block exits
         const int64_t tSave = save_state(dst, true, false, true);
@@ -636,8 +658,7 @@ k_persistent_yield(const apk_yield_params) {
         lds_sync();
         if (tid == 0) {
           rq_publish(P().rq_entry + (size_t)(tk % P().rq_capacity) * 4, tk, (int)task,
-                     rkind > 0 ? s : 0, rkind,
-                     (int)xcc_id() * APK_SES_PER_XCD + (int)se_id());
+                     rkind > 0 ? s : 0, rkind, domain());
           const int64_t t1 = wall_ticks();
           stat(ST_RETREATS, 1);
           stat(ST_SAVE, (uint64_t)(t1 - tSave));

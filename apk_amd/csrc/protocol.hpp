@@ -194,7 +194,9 @@ APK_PROTO_FN int first_seen(int flag_at_start, int launch_epoch, int num_events)
 }
 
 // Which blocks of the retreat arm retreat at generation f: the first grid,
-// by quota, at f = 1; afterwards only the newest continuation (launched
+// by quota, at f = 1 (the first ceil(R / 32) blocks of each domain to start:
+// they are chosen as they register, so only they need to poll at every
+// site); afterwards only the newest continuation (launched
 // after generation launch_epoch, so f > launch_epoch), all of it -- it holds
 // the CUs the previous generation freed, and it must complete for the next
 // continuation (queued behind it) to start. Every other block keeps working.

@@ -342,10 +342,12 @@ int main(int argc, char** argv) {
                                             : uniform_schedule(seed, 150, 400, events);
     const double settleUs = 20000.0, schedUs = gaps.back() / 1e3;
     const double usPerTask = drainEstUs / bgTasks;
-    // Sized to outlast the schedule with margin; arrivals that still find the
-    // job finished are reported and left out of the latency.
+    // Sized to outlast the schedule with margin (the drain estimate, taken on
+    // a cold clock over a short drain, overstates the task time by up to a
+    // third); arrivals that still find the job finished are reported and left
+    // out of the latency.
     const unsigned jobTasks =
-        (unsigned)std::min(1.3 * (settleUs + schedUs + 20000.0) / usPerTask, 2.0e9);
+        (unsigned)std::min(1.6 * (settleUs + schedUs + 20000.0) / usPerTask, 2.0e9);
     rig.reserveTasks(jobTasks, oracle ? jobTasks : 0);
     const int keepCu = std::min(events, 64);  // urgent outputs kept per event
     float* dCuAll;
@@ -498,10 +500,19 @@ int main(int argc, char** argv) {
     HIP_CHECK(hipGetLastError());
     const auto [as0, ae0] = rig.readRunGT();
     const double usPerTaskWarm = (ae0 - as0) * tickUs / aloneTasks;
+    // The same length on the kernel with polls off, against which every
+    // arm's cost is stated.
+    rig.reset(false);
+    rig.launch(APK_POLL_OFF, 1, APK_RESUME_RESTART, 0, aloneTasks, false, 0, false, bgStream);
+    HIP_CHECK(hipStreamSynchronize(bgStream));
+    HIP_CHECK(hipGetLastError());
+    const auto [os0, oe0] = rig.readRunGT();
+    const double usPerTaskOff = (oe0 - os0) * tickUs / aloneTasks;
     const double jobUs = (jobEnd - jobStart) * tickUs;
     const double flopTask = 2.0 * geo.tile_m * geo.tile_n * (double)K;
     const double tfJob = flopTask * jobTasks / (jobUs * 1e-6) / 1e12;
     const double tfAlone = flopTask / (usPerTaskWarm * 1e-6) / 1e12;
+    const double tfOff = flopTask / (usPerTaskOff * 1e-6) / 1e12;
     const double tileUs = usPerTaskWarm * blocks / (K / kChunk);
     printf("\n--- continuous retreat arm: %zu arrivals within the job (%d after it ended, %d "
            "not run), poll %s every %d, %d retreats per arrival, resume %s ---\n",
@@ -525,6 +536,9 @@ int main(int argc, char** argv) {
            tileUs, raise.empty() ? -1.0 : percentile(raise, 0.5) / tileUs);
     printf("background: %.2f TFLOP/s over the job with arrivals vs %.2f alone (after it) -> retreat "
            "overhead %.2f%%\n", tfJob, tfAlone, (tfAlone / tfJob - 1.0) * 100.0);
+    printf("background alone with polls off: %.2f TFLOP/s -> the job with arrivals %.2f%% below "
+           "it, the polled kernel alone %.2f%% below it\n", tfOff, (1.0 - tfJob / tfOff) * 100.0,
+           (1.0 - tfAlone / tfOff) * 100.0);
     printf("retreats %llu | resumed %llu | save %.2f us per retreat | arrivals without a "
            "retreat %d | late drains %d | resume errors %llu | lost %u\n", retreats, resumed,
            retreats ? saveTicks * tickUs / retreats : 0.0, noRetreat, lateDrains, errors,

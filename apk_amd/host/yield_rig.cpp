@@ -61,7 +61,7 @@ YieldRig::YieldRig(const RigShape& s, const std::vector<uint8_t>& A,
   if (U_ > 0) dUHash_ = dalloc<unsigned long long>((size_t)E * U_);
   dStats_ = dalloc<unsigned long long>((size_t)(s.blocks + s.extraRows) * APK_STATS_PER_BLOCK);
   if (s.retreatCap) {
-    dRetreatCount_ = dalloc<int>((size_t)E * APK_RETREAT_DOMAINS);
+    dRetreatCount_ = dalloc<int>((size_t)(E + 1) * APK_RETREAT_DOMAINS);  // + registrations
     dRetreatGT_ = dalloc<long long>(2 * (size_t)E);
     dRqCtl_ = dalloc<unsigned>(3);
     dRqEntry_ = dalloc<int>((size_t)s.retreatCap * 4);
@@ -201,7 +201,7 @@ void YieldRig::launch(int poll, int pollEvery, int resume, int poison, unsigned 
 
 void YieldRig::resetRetreat() {
   const int E = s_.events > 0 ? s_.events : 1;
-  HIP_CHECK(hipMemset(dRetreatCount_, 0, (size_t)E * APK_RETREAT_DOMAINS * sizeof(int)));
+  HIP_CHECK(hipMemset(dRetreatCount_, 0, (size_t)(E + 1) * APK_RETREAT_DOMAINS * sizeof(int)));
   std::vector<long long> gt(2 * (size_t)E, 0);
   for (int e = 0; e < E; ++e) gt[2 * (size_t)e] = INT64_MAX;
   HIP_CHECK(hipMemcpy(dRetreatGT_, gt.data(), gt.size() * 8, hipMemcpyHostToDevice));

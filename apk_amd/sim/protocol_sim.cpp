@@ -127,6 +127,7 @@ struct Sim {
   std::vector<int> exec;                     // per task: completions
   std::vector<uint64_t> result;              // per task
   std::vector<int> retreatCount;             // per event x domain
+  std::vector<int> regCount;                 // first grid's blocks per domain, as they start
   unsigned rqCtl[3] = {0, 0, 0};
   std::vector<int> rqEntry;                  // cap x 4
   std::vector<Ckpt> rqSlot;                  // cap
@@ -143,6 +144,7 @@ struct Sim {
     exec.assign(numTasks, 0);
     result.assign(numTasks, 0);
     retreatCount.assign((size_t)c.events * c.domains, 0);
+    regCount.assign(c.domains, 0);
     if (c.cap <= 0) c.cap = 4 * c.retreatN;
     rqEntry.assign((size_t)c.cap * 4, 0);
     for (int i = 0; i < c.cap; ++i) rqEntry[(size_t)i * 4 + 2] = i;  // seq = i: free
@@ -158,6 +160,14 @@ struct Sim {
     const int quota = (c.retreatN + c.domains - 1) / c.domains;
     int lastSeen = 0, chunksDone = 0;  // chunksDone: stage boundaries of completed tasks
     if (cont) lastSeen = proto::first_seen(HostPlat::load(&flag), epoch, c.events);
+    // Retreat arm: the first grid's first `quota` blocks of each domain to
+    // start retreat at generation 1; a continuation after an earlier
+    // generation retreats at the next one. Only such blocks poll at every
+    // site; the others at a task's first stage.
+    bool mayRetreat = false;
+    if (c.retreat)
+      mayRetreat = cont ? epoch > 0 && epoch < c.events
+                        : __atomic_fetch_add(&regCount[dom], 1, __ATOMIC_RELAXED) < quota;
     proto::TaskQueue<HostPlat> tq(ctr.data(), c.tilesM, c.tilesN, numTasks);
     const unsigned T = (unsigned)(c.tilesM * c.tilesN);
     for (;;) {
@@ -211,7 +221,9 @@ struct Sim {
       if (kind >= 0) enter(ck, kind);
       bool retreated = false;
       while (s < S) {
-        if ((chunksDone + s) % c.pollEvery == 0) {  // every poll_every-th boundary passed
+        // every poll_every-th boundary passed (a block that can no longer
+        // retreat: a task's first stage)
+        if ((!c.retreat || mayRetreat) ? (chunksDone + s) % c.pollEvery == 0 : s == 0) {
           int f = HostPlat::load(&flag);
           if (f > c.events) f = c.events;
           if (f > lastSeen) {
@@ -227,29 +239,29 @@ struct Sim {
             }
             if (c.retreat) {
               const int role = proto::retreat_role(cont, epoch, f);
-              if (role != proto::RETREAT_NONE) {
-                int cnt = __atomic_fetch_add(&retreatCount[(size_t)ev * c.domains + dom], 1,
-                                             __ATOMIC_RELAXED);
-                if (role == proto::RETREAT_ALL || cnt < quota) {
-                  unsigned t = proto::rq_reserve<HostPlat>(rqCtl, (unsigned)c.cap,
-                                                           rqEntry.data());
-                  if (t & proto::RQ_FULL) {
-                    refused.fetch_add(1);
+              const bool chosen = mayRetreat;
+              if (!cont) mayRetreat = false;
+              if (role == proto::RETREAT_ALL || (role == proto::RETREAT_BY_QUOTA && chosen)) {
+                __atomic_fetch_add(&retreatCount[(size_t)ev * c.domains + dom], 1,
+                                   __ATOMIC_RELAXED);
+                unsigned t = proto::rq_reserve<HostPlat>(rqCtl, (unsigned)c.cap,
+                                                         rqEntry.data());
+                if (t & proto::RQ_FULL) {
+                  refused.fetch_add(1);
+                } else {
+                  int* en = &rqEntry[(size_t)(t % (unsigned)c.cap) * 4];
+                  const int rk = c.resume;
+                  if (c.bug == B_PUBLISH_EARLY) {
+                    proto::rq_publish<HostPlat>(en, t, (int)task, rk > 0 ? s : 0, rk, dom);
+                    spin_ns(20000);
+                    rqSlot[t % (unsigned)c.cap] = mine;
                   } else {
-                    int* en = &rqEntry[(size_t)(t % (unsigned)c.cap) * 4];
-                    const int rk = c.resume;
-                    if (c.bug == B_PUBLISH_EARLY) {
-                      proto::rq_publish<HostPlat>(en, t, (int)task, rk > 0 ? s : 0, rk, dom);
-                      spin_ns(20000);
-                      rqSlot[t % (unsigned)c.cap] = mine;
-                    } else {
-                      rqSlot[t % (unsigned)c.cap] = mine;
-                      proto::rq_publish<HostPlat>(en, t, (int)task, rk > 0 ? s : 0, rk, dom);
-                    }
-                    retreats.fetch_add(1);
-                    retreated = true;
-                    break;
+                    rqSlot[t % (unsigned)c.cap] = mine;
+                    proto::rq_publish<HostPlat>(en, t, (int)task, rk > 0 ? s : 0, rk, dom);
                   }
+                  retreats.fetch_add(1);
+                  retreated = true;
+                  break;
                 }
               }
             } else {

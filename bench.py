@@ -198,11 +198,18 @@ def preemption_metrics(events, trials):
     re50, re99 = grab(rt, r"urgent GEMM done after the flag \(us\): p50 ([\d.]+) \| p99 ([\d.]+)")
     bad, total = grab(rt, r"SAFETY: (\d+) of (\d+) task fingerprints", int)
     tf_job, = grab(rt, r"background: ([\d.]+) TFLOP/s over the job")
+    tf_off, below, idle = grab(rt, r"background alone with polls off: ([\d.]+) TFLOP/s -> the "
+                                   r"job with arrivals ([-\d.]+)% below it, the polled kernel "
+                                   r"alone ([-\d.]+)% below it")
     out["retreat_latency_us"] = {"p50": r50, "p99": r99, "events": n_in,
                                  "p50_over_tile": round(r50 / tile_us, 3),
                                  "mode": "continuous job, accumulator-only checkpoints"}
     out["retreat_urgent_done_us"] = {"p50": re50, "p99": re99}
     out["retreat_background_tflops"] = tf_job
+    # the whole cost of being preemptible this way: polls, retreats, resumes
+    # and the urgent GEMMs' CUs, against the same kernel with polls off
+    out["retreat_background_overhead_pct"] = {"vs_polls_off": below, "polls_off_tflops": tf_off,
+                                              "no_arrivals_vs_polls_off": idle}
     out["corrupt_yields"] = bad
     out["retreat_tasks_checked"] = total
     out["oracle"] = "PASS" if ("ORACLE: PASS" in rt and "yield: PASS" in rt) else "FAIL"
@@ -242,6 +249,8 @@ def bf16_metrics():
     tile_us, = grab(rt, r"tile \(k-chunk\) time at full residency: ([\d.]+) us")
     bad, total = grab(rt, r"SAFETY: (\d+) of (\d+) task fingerprints", int)
     ovh, = grab(rt, r"retreat overhead ([-\d.]+)%")
+    _, below = grab(rt, r"background alone with polls off: ([\d.]+) TFLOP/s -> the job "
+                        r"with arrivals ([-\d.]+)% below it")
     return {"workload": "cfg5: bf16 GEMM M=N=K=8192 (2 passes of 1024 256x256 tiles), fp32 "
                         "accumulate, 256 workers, no yields, after 1.5 s of the same runs",
             "tflops": round(tf, 2), "peak": 2516.6, "frac": round(tf / 2516.6, 4),
@@ -251,7 +260,9 @@ def bf16_metrics():
             "retreat_latency_us": {"p50": r50, "p99": r99, "events": n_in,
                                    "tile_us": tile_us, "p50_over_tile": round(r50 / tile_us, 3),
                                    "mode": "continuous job, tiles re-queued from k = 0",
-                                   "background_overhead_pct": ovh, "corrupt_tasks": bad,
+                                   "background_overhead_pct": ovh,
+                                   "background_below_polls_off_pct": below,
+                                   "corrupt_tasks": bad,
                                    "tasks_checked": total,
                                    "oracle": "PASS" if ("ORACLE: PASS" in rt and
                                                         "yield: PASS" in rt) else "FAIL"}}

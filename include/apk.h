@@ -292,20 +292,26 @@ typedef struct apk_yield_params {
    * retreat = R > 0: the urgent kernel has R workgroups. The hardware deals
    * a kernel's workgroups round-robin to the XCDs and their shader engines
    * (APK_RETREAT_DOMAINS in all), starting wherever its pointers stand, and a
-   * workgroup only runs on a CU of its own shader engine. So at a new
-   * generation e the first ceil(R / 32) blocks of EVERY shader engine to see
-   * it (counted in retreat_count[(e-1) * 32 + xcd * 4 + se]; 32 * ceil(R/32)
-   * blocks in all) drain their loads,
+   * workgroup only runs on a CU of its own shader engine. So at generation
+   * 1 ceil(R / 32) blocks of EVERY shader engine -- the first grid's first
+   * ceil(R / 32) of each to start, as they register in the last row of
+   * retreat_count -- and at each later generation the newest continuation
+   * (launch_epoch), all of it, retreat (counted in retreat_count[(e-1) * 32 +
+   * xcd * 4 + se]; 32 * ceil(R/32) blocks in all): they drain their loads,
    * checkpoint their tile into the resume queue (per `resume`: accumulators
    * + live LDS stages, accumulators only, or nothing = restart from k = 0)
    * and exit, so that the kernel waiting on another stream is dispatched
    * onto their CUs. Every
    * worker pops the resume queue before taking a new task, so the tile is
    * finished by whichever worker (of this launch or of a later relaunch on
-   * any stream) pops its entry; its k order never changes. The urgent job
+   * any stream) pops its entry; its k order never changes. Only blocks that
+   * may still retreat poll at every site; the others poll at the first stage
+   * of each new task (so obs_gt, when given, logs them late). The urgent job
    * is not run inside this kernel (Au may be NULL). 0 = cooperative arm. */
   int retreat;
-  int* retreat_count;            /* [events * APK_RETREAT_DOMAINS], 0 at job start */
+  int* retreat_count;            /* [(events + 1) * APK_RETREAT_DOMAINS], 0 at job start:
+                                    rows 0..events-1 the retreats of each generation,
+                                    row `events` the first grid's registrations */
   long long* retreat_gt;         /* [2 * events] or NULL: [2e] earliest checkpoint
                                     start (host sets INT64_MAX), [2e+1] latest exit (0) */
   unsigned int* rq_ctl;          /* resume queue tickets, 3 words: [0] head, [1] tail,

@@ -86,7 +86,8 @@ class RetreatJob:
         self.unxt = T.zeros(apk.QUEUE_WORDS, dtype=i32, device="cuda")
         self.flag = T.zeros(apk.FLAG_STRIDE // 4, dtype=i32, device="cuda")
         self.set_gt = T.zeros(1, dtype=i64, device="cuda")
-        self.rcount = T.zeros(apk.RETREAT_DOMAINS, dtype=i32, device="cuda")
+        # one event's retreats, then the first grid's registrations
+        self.rcount = T.zeros(2 * apk.RETREAT_DOMAINS, dtype=i32, device="cuda")
         self.rgt = T.zeros(2, dtype=i64, device="cuda")
         self.rq_ctl = T.zeros(3, dtype=i32, device="cuda")
         self.rq_entry = T.zeros(4 * self.RB, dtype=i32, device="cuda")
