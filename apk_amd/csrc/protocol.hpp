@@ -105,7 +105,10 @@ constexpr int64_t RQ_WAIT_TICKS = 2000000;
 
 // Takes the next ticket with one fetch-add (no CAS loop: the producers of one
 // generation arrive together, and a CAS loop would serialise them round trip
-// by round trip) and waits, bounded, for its entry to be free. A ticket whose
+// by round trip) and waits, bounded, for its entry to be free -- unless the
+// ticket is its entry's first (t < cap), which the host's seq = i set free
+// before the job: a ring with an entry for every retreat of a job then takes
+// no second round trip before the checkpoint. A ticket whose
 // entry stays taken for `wait` ticks is returned with RQ_FULL set: the caller
 // does not retreat and counts an error (that ticket's consumer then reports
 // it lost after its own bounded wait; no task is lost, the producer keeps its
@@ -115,7 +118,7 @@ APK_PROTO_FN unsigned rq_reserve(unsigned* ctl, unsigned cap, const int* entries
                                  int64_t wait = RQ_WAIT_TICKS) {
   const unsigned t = P::fetch_add(&ctl[1], 1u);
   const int* en = entries + (size_t)(t % cap) * 4;
-  if (P::load(&en[2]) != (int)t) {
+  if (t >= cap && P::load(&en[2]) != (int)t) {
     const int64_t deadline = P::ticks() + wait;
     while (P::load(&en[2]) != (int)t) {
       if (P::ticks() > deadline) return t | RQ_FULL;

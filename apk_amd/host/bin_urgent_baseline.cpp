@@ -199,6 +199,12 @@ int main(int argc, char** argv) {
     // worth of entries in its ring (each event's are read back well before
     // the next arrival)
     rs.retreatCap = (unsigned)(continuous ? 4 * retreatBlocks : retreatBlocks);
+    if (continuous && resume == APK_RESUME_RESTART) {
+      // no checkpoints to hold: an entry per retreat of the whole job, so
+      // that no ticket waits for its entry to come free
+      rs.retreatCap = (unsigned)retreatBlocks * (unsigned)(std::max(events, 1) + 8);
+      rs.retreatSlots = false;
+    }
     rs.extraRows = retreatBlocks + blocks;  // continuation + drain relaunch
     rs.hashTasks = (unsigned)bgTasks;
     if (oracle) rs.oracleTasks = (unsigned)bgTasks;
@@ -513,7 +519,10 @@ int main(int argc, char** argv) {
     const double tfJob = flopTask * jobTasks / (jobUs * 1e-6) / 1e12;
     const double tfAlone = flopTask / (usPerTaskWarm * 1e-6) / 1e12;
     const double tfOff = flopTask / (usPerTaskOff * 1e-6) / 1e12;
-    const double tileUs = usPerTaskWarm * blocks / (K / kChunk);
+    // the k-chunk time at full residency of the kernel with polls off (what
+    // the latency is stated against), and of the polled kernel alone
+    const double tileUs = usPerTaskOff * blocks / (K / kChunk);
+    const double tileUsPolled = usPerTaskWarm * blocks / (K / kChunk);
     printf("\n--- continuous retreat arm: %zu arrivals within the job (%d after it ended, %d "
            "not run), poll %s every %d, %d retreats per arrival, resume %s ---\n",
            raise.size(), afterJob, notRun, pollS.c_str(), pollEvery, retreatBlocks,
@@ -532,8 +541,9 @@ int main(int argc, char** argv) {
     if (!cont.empty())
       printf("continuation starts after the flag (us): p50 %.2f | p99 %.2f\n",
              percentile(cont, 0.5), percentile(cont, 0.99));
-    printf("tile (k-chunk) time at full residency: %.2f us -> p50 latency = %.3f tiles\n",
-           tileUs, raise.empty() ? -1.0 : percentile(raise, 0.5) / tileUs);
+    printf("tile (k-chunk) time at full residency: %.2f us -> p50 latency = %.3f tiles (polled "
+           "kernel: %.2f us -> %.3f)\n", tileUs, raise.empty() ? -1.0 : percentile(raise, 0.5) / tileUs,
+           tileUsPolled, raise.empty() ? -1.0 : percentile(raise, 0.5) / tileUsPolled);
     printf("background: %.2f TFLOP/s over the job with arrivals vs %.2f alone (after it) -> retreat "
            "overhead %.2f%%\n", tfJob, tfAlone, (tfAlone / tfJob - 1.0) * 100.0);
     printf("background alone with polls off: %.2f TFLOP/s -> the job with arrivals %.2f%% below "

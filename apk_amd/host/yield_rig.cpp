@@ -65,7 +65,8 @@ YieldRig::YieldRig(const RigShape& s, const std::vector<uint8_t>& A,
     dRetreatGT_ = dalloc<long long>(2 * (size_t)E);
     dRqCtl_ = dalloc<unsigned>(3);
     dRqEntry_ = dalloc<int>((size_t)s.retreatCap * 4);
-    dRqSlots_ = dalloc<float>((size_t)s.retreatCap * apk_yield_ckpt_floats(s.engine));
+    if (s.retreatSlots)
+      dRqSlots_ = dalloc<float>((size_t)s.retreatCap * apk_yield_ckpt_floats(s.engine));
   }
   if (s.oracleTasks) {
     dExec_ = dalloc<int>(s.oracleTasks);

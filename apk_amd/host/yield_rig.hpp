@@ -27,6 +27,7 @@ struct RigShape {
   // of stats kept for relaunched (continuation) blocks after the first
   // `blocks` rows.
   unsigned retreatCap = 0;
+  bool retreatSlots = true;  // checkpoint slots for the ring (none: restart only)
   int extraRows = 0;
 };
 

@@ -210,7 +210,29 @@ def preemption_metrics(events, trials):
     # and the urgent GEMMs' CUs, against the same kernel with polls off
     out["retreat_background_overhead_pct"] = {"vs_polls_off": below, "polls_off_tflops": tf_off,
                                               "no_arrivals_vs_polls_off": idle}
-    out["corrupt_yields"] = bad
+    # The same job with retreating tiles re-queued from k = 0 (no checkpoint:
+    # the ring then holds an entry for every retreat of the job, so no
+    # ticket waits for its entry), paying half a tile of redone work per
+    # retreat instead of the accumulator save and restore.
+    rr = run_bin("urgent_baseline", CFG3 + CFG3_URGENT +
+                 ["--bg-tasks", 4096, "--urgent-blocks", 4, "--arrival", "exp",
+                  "--mean-gap-us", 2000, "--yield", 1, "--retreat", 4, "--oracle", 1,
+                  "--continuous", 1, "--events", events, "--resume", "restart"], timeout=600)
+    q50, q99 = grab(rr, r"flag raised -> urgent GEMM starts \(us\): p50 ([\d.]+) \| "
+                        r"p90 [\d.]+ \| p99 ([\d.]+)")
+    tile_off, = grab(rr, r"tile \(k-chunk\) time at full residency: ([\d.]+) us")
+    _, below_r, _ = grab(rr, r"background alone with polls off: ([\d.]+) TFLOP/s -> the "
+                             r"job with arrivals ([-\d.]+)% below it, the polled kernel "
+                             r"alone ([-\d.]+)% below it")
+    bad_r, total_r = grab(rr, r"SAFETY: (\d+) of (\d+) task fingerprints", int)
+    n_r, = grab(rr, r"continuous retreat arm: (\d+) arrivals within the job", int)
+    out["retreat_restart"] = {"p50": q50, "p99": q99, "events": n_r,
+                              "p50_over_tile": round(q50 / tile_off, 3), "tile_us": tile_off,
+                              "background_below_polls_off_pct": below_r,
+                              "corrupt_tasks": bad_r, "tasks_checked": total_r,
+                              "oracle": "PASS" if ("ORACLE: PASS" in rr and
+                                                   "yield: PASS" in rr) else "FAIL"}
+    out["corrupt_yields"] = bad + bad_r
     out["retreat_tasks_checked"] = total
     out["oracle"] = "PASS" if ("ORACLE: PASS" in rt and "yield: PASS" in rt) else "FAIL"
     # No preemption: the urgent GEMM waits for the background to drain (one
