@@ -744,8 +744,13 @@ k_persistent_yield(const apk_yield_params) {
     else chunksDone += S / chunkStages;
   }
 
-  if (P().run_gt && tid == 0 && fetch_add_u32(P().exit_count, 1u) == gridDim.x - 1)
-    P().run_gt[1] = wall_ticks();
+  // The last exit is the latest one: an atomic max that returns nothing, so
+  // a retreating block's CU is not held for a round trip (a count returning
+  // "last block?" held it ~0.5 us before the urgent kernel could have it).
+  if (P().run_gt && tid == 0) {
+    atomic_max_i64(&P().run_gt[1], wall_ticks());
+    __hip_atomic_fetch_add(P().exit_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   if (P().stats && tid == 0) {
     // Added, not stored: relaunches (retreat-arm continuations) may share rows.
     unsigned long long* st = P().stats + (size_t)row() * APK_STATS_PER_BLOCK;

@@ -284,7 +284,8 @@ typedef struct apk_yield_params {
    * it; the resumed tile then differs). 0 = drain. */
   int naive;
   /* run timeline (src/urgent_baseline.cu:66-88), may be NULL: run_gt[0] =
-   * block 0's start, run_gt[1] = exit of the last block; exit_count must be
+   * block 0's start, run_gt[1] = exit of the last block (0 at launch: the
+   * latest exit is kept with an atomic max); exit_count counts the exits and must be
    * 0 at launch */
   long long* run_gt;
   unsigned int* exit_count;
