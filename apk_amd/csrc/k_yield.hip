@@ -624,7 +624,8 @@ k_persistent_yield(const apk_yield_params) {
         // kernel's R workgroups land in R domains the host cannot name, so
         // free ceil(R / 32) CUs in every (XCD, shader engine) domain.
         // Which blocks retreat at generation f (launch_epoch in the params):
-        // the first grid by quota at f = 1; a continuation that follows an
+        // of the first grid at f = 1, the ceil(R / 32) blocks per domain that
+        // registered first when the grid started; a continuation that follows an
         // earlier generation, all of it -- it holds the CUs the previous
         // generation freed, and it must complete for the next continuation
         // (queued behind it) to start.

@@ -9,7 +9,8 @@
 // flag every `poll_every` stages, and at a new generation either
 //   coop     pop the event's urgent tiles, checkpoint, serve them, restore
 //            (src/yield.cu:95-204 is the reference's claim/serve loop), or
-//   retreat  (first grid by quota at generation 1, afterwards the newest
+//   retreat  (first grid at generation 1: the first `quota` blocks of each
+//            domain to start, which alone poll at every site; afterwards the newest
 //            continuation) reserve a resume ticket, checkpoint into its slot,
 //            publish, exit; a continuation launched after the event resumes
 //            the ring's checkpoints.
