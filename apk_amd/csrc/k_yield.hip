@@ -146,6 +146,7 @@ k_persistent_yield(const apk_yield_params) {
          ST_RESTORE = APK_ST_RESTORE, ST_INFLIGHT = APK_ST_INFLIGHT,
          ST_RETREATS = APK_ST_RETREATS, ST_RESUMED = APK_ST_RESUMED, ST_ERRORS = APK_ST_ERRORS,
          ST_STALE = APK_ST_STALE, ST_CHECKPOINTS = APK_ST_CHECKPOINTS,
+         ST_DECLINED = APK_ST_DECLINED,
          ST_INFLIGHT_ALL = APK_ST_INFLIGHT_ALL, ST_STALE_ALL = APK_ST_STALE_ALL };
   auto stat = [&](int k, uint64_t v) { s_stats[k] += v; };  // thread 0 only
 
@@ -246,7 +247,7 @@ k_persistent_yield(const apk_yield_params) {
               tk = (int)q;
               stat(ST_RESUMED, 1);
               // a restart entry carries no checkpoint: free it at once
-              if (kind == 0) rq_release(en, q, P().rq_capacity);
+              if (kind == 0) rq_release(P().rq_ctl, en, q, P().rq_capacity);
             } else {
               stat(ST_ERRORS, 1);  // never published within the deadline: the task is lost
               t = 0xfffffffeu;
@@ -398,7 +399,8 @@ k_persistent_yield(const apk_yield_params) {
               // (load_acc / the ring restore wait for them): free the entry
               __syncthreads();
               if (tid == 0)
-                rq_release(P().rq_entry + (size_t)((unsigned)rqHeld % P().rq_capacity) * 4,
+                rq_release(P().rq_ctl,
+                           P().rq_entry + (size_t)((unsigned)rqHeld % P().rq_capacity) * 4,
                            (unsigned)rqHeld, P().rq_capacity);
               rqHeld = -1;
             }
@@ -636,17 +638,22 @@ k_persistent_yield(const apk_yield_params) {
         if (role == proto::RETREAT_BY_QUOTA && !mine) continue;
         unsigned t = RQ_NONE;
         if (tid == 0) {
-          // counted (the retreats of generation f per domain), no round trip
-          __hip_atomic_fetch_add(&P().retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + domain()],
-                                 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           t = rq_reserve(P().rq_ctl, P().rq_capacity, P().rq_entry);
-          if (t & RQ_FULL) {  // the ring stayed full: keep working
+          if (t == RQ_FULL) {  // the ring holds capacity tickets: declined, keep working
+            stat(ST_DECLINED, 1);
+            t = RQ_NONE;
+          } else if (t & RQ_STUCK) {  // its entry never freed: keep working, report it
             stat(ST_ERRORS, 1);
             t = RQ_NONE;
+          } else {
+            // counted (the retreats of generation f per domain), no round trip
+            __hip_atomic_fetch_add(
+                &P().retreat_count[(size_t)ev * APK_RETREAT_DOMAINS + domain()], 1,
+                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
           }
         }
         const unsigned tk = bcast(t);
-        if (tk == RQ_NONE) continue;  // the ring stayed full: keep working
+        if (tk == RQ_NONE) continue;  // declined: keep working
         float* dst = P().rq_slots + (size_t)(tk % P().rq_capacity) * Ckpt<E>::SLOT_FLOATS;
         // always drain: nothing may land in LDS after the block exits
         const int64_t tSave = save_state(dst, true, false, true);
@@ -791,10 +798,12 @@ static int validate(const apk_yield_params* p, int poll, int oracle, int blocks)
     APK_REQUIRE(p->block_base >= 0 && p->obs_stride >= 0,
                 "persistent_yield: block_base=%d obs_stride=%d", p->block_base, p->obs_stride);
     if (p->retreat > 0) {
-      APK_REQUIRE(p->num_events > 0 && p->retreat_count && p->rq_ctl && p->rq_entry &&
-                      p->rq_capacity > 0,
+      APK_REQUIRE(p->num_events > 0 && p->retreat_count && p->rq_ctl && p->rq_entry,
                   "persistent_yield: the retreat arm needs events, retreat_count and a resume "
                   "queue");
+      APK_REQUIRE(p->rq_capacity >= 2,
+                  "persistent_yield: rq_capacity=%u, the resume ring needs at least 2 entries",
+                  p->rq_capacity);
       APK_REQUIRE(p->rq_slots || p->resume == APK_RESUME_RESTART,
                   "persistent_yield: checkpointing retreats need rq_slots");
       APK_REQUIRE(p->Au == nullptr, "persistent_yield: the retreat arm runs no urgent job");

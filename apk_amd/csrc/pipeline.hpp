@@ -43,6 +43,7 @@ struct DevPlat {
 using TaskQueue = proto::TaskQueue<DevPlat>;
 using proto::RQ_FULL;
 using proto::RQ_NONE;
+using proto::RQ_STUCK;
 // Thread-0 only, each of them.
 __device__ __forceinline__ unsigned rq_reserve(unsigned* ctl, unsigned cap, const int* en) {
   return proto::rq_reserve<DevPlat>(ctl, cap, en);
@@ -55,8 +56,8 @@ __device__ __forceinline__ void rq_publish(int* en, unsigned ticket, int task, i
 __device__ __forceinline__ int rq_wait_ready(const int* en, unsigned h) {
   return proto::rq_wait_ready<DevPlat>(en, h);
 }
-__device__ __forceinline__ void rq_release(int* en, unsigned h, unsigned cap) {
-  proto::rq_release<DevPlat>(en, h, cap);
+__device__ __forceinline__ void rq_release(unsigned* ctl, int* en, unsigned h, unsigned cap) {
+  proto::rq_release<DevPlat>(ctl, en, h, cap);
 }
 
 // ---------------------------------------------------------------------------

@@ -85,43 +85,61 @@ struct TaskQueue {
 };
 
 // ---------------------------------------------------------------------------
-// Resume queue of the retreat arm: a bounded ring of `cap` entries, tickets
-// [head, tail) in ctl[0..1], and in ctl[2] the count of reserved tickets not
-// yet claimed. Entry i = {task, stage, seq, kind << 8 |
+// Resume queue of the retreat arm: a bounded ring of `cap` entries (cap >= 2),
+// tickets [head, tail) in ctl[0..1], in ctl[2] the count of reserved tickets
+// not yet claimed, and in ctl[3] the count of tickets reserved and not yet
+// released (the ring's occupancy). Entry i = {task, stage, seq, kind << 8 |
 // domain} with its checkpoint slot i; ticket t uses entry t % cap. `seq`
 // orders the entry's rounds (bounded MPMC ring with per-entry sequence
 // numbers): seq == t means free for ticket t, t + 1 published by ticket t's
 // producer, and the consumer of ticket t sets it to t + cap once it has read
-// the checkpoint back. A producer that finds its entry still taken after a
-// bounded wait declines the retreat (the ring is full); a consumer claims the
-// oldest reserved ticket and waits, bounded, for its producer (a resident
-// block on its exit path). The host sets seq = i for every entry before a job.
+// the checkpoint back. With cap == 1 "published by t" (t + 1) and "free for
+// t + 1" (t + cap) would be the same value, hence cap >= 2.
+//
+// A producer first takes a unit of occupancy, and only then a ticket: when
+// the ring already holds `cap` unreleased tickets it declines the retreat
+// without taking one (the block keeps its tile and works on), so every ticket
+// taken is published and claimed -- a full ring leaves no hole in the ticket
+// order. Occupancy also bounds the wait for the ticket's entry: if at most
+// `cap` tickets are unreleased once ticket t is taken, then at least
+// t + 1 - cap of the tickets below t have been released, so either ticket
+// t - cap (the entry's previous user) is released or some later ticket is --
+// and claims go in ticket order, so t - cap has then been claimed by a
+// resident block that releases it once its producer has published and its
+// checkpoint is read back. Every wait in the ring thus ends on other blocks'
+// progress; the deadlines below only keep a block that stopped from hanging
+// the grid, and a run that hits one reports it as an error.
+// The host sets seq = i for every entry and ctl[0..3] = 0 before a job.
 constexpr unsigned RQ_NONE = 0xffffffffu;
-constexpr unsigned RQ_FULL = 0x80000000u;
+constexpr unsigned RQ_FULL = 0xfffffffeu;   // declined: the ring holds cap tickets
+constexpr unsigned RQ_STUCK = 0x80000000u;  // flag on a ticket whose entry never freed
 // Longest wait for an entry: 20 ms at the 100 MHz clock. A producer
-// publishes within microseconds; running out means a lost task, which the
-// exactly-once counts then report.
+// publishes, and a consumer reads back, within microseconds.
 constexpr int64_t RQ_WAIT_TICKS = 2000000;
 
-// Takes the next ticket with one fetch-add (no CAS loop: the producers of one
-// generation arrive together, and a CAS loop would serialise them round trip
-// by round trip) and waits, bounded, for its entry to be free -- unless the
-// ticket is its entry's first (t < cap), which the host's seq = i set free
-// before the job: a ring with an entry for every retreat of a job then takes
-// no second round trip before the checkpoint. A ticket whose
-// entry stays taken for `wait` ticks is returned with RQ_FULL set: the caller
-// does not retreat and counts an error (that ticket's consumer then reports
-// it lost after its own bounded wait; no task is lost, the producer keeps its
-// tile).
+// Takes a unit of occupancy (or declines: RQ_FULL), then the next ticket with
+// one fetch-add (no CAS loop: the producers of one generation arrive
+// together, and a CAS loop would serialise them round trip by round trip),
+// and waits for its entry to be free -- unless the ticket is its entry's
+// first (t < cap), which the host's seq = i set free before the job: a ring
+// with an entry for every retreat of a job then takes no second round trip
+// before the checkpoint. A ticket whose entry is still taken after `wait`
+// ticks (a block holding it stopped) is returned with RQ_STUCK set; the
+// caller counts an error and keeps its tile, and the claimant of that ticket
+// reports it lost.
 template <class P>
 APK_PROTO_FN unsigned rq_reserve(unsigned* ctl, unsigned cap, const int* entries,
                                  int64_t wait = RQ_WAIT_TICKS) {
+  if (P::fetch_add(&ctl[3], 1u) >= cap) {  // as in rq_pop: give back, decline
+    P::fetch_add(&ctl[3], ~0u);
+    return RQ_FULL;
+  }
   const unsigned t = P::fetch_add(&ctl[1], 1u);
   const int* en = entries + (size_t)(t % cap) * 4;
   if (t >= cap && P::load(&en[2]) != (int)t) {
     const int64_t deadline = P::ticks() + wait;
     while (P::load(&en[2]) != (int)t) {
-      if (P::ticks() > deadline) return t | RQ_FULL;
+      if (P::ticks() > deadline) return t | RQ_STUCK;
       P::pause();
     }
   }
@@ -176,11 +194,14 @@ APK_PROTO_FN int rq_wait_ready(const int* en, unsigned h, int64_t wait = RQ_WAIT
   }
 }
 // Once every reader of ticket h's checkpoint is done (their loads complete):
-// frees the entry for ticket h + cap.
+// frees the entry for ticket h + cap, then gives back the ticket's unit of
+// occupancy (a producer admitted by it waits for the seq store if it reads
+// the entry first).
 template <class P>
-APK_PROTO_FN void rq_release(int* en, unsigned h, unsigned cap) {
+APK_PROTO_FN void rq_release(unsigned* ctl, int* en, unsigned h, unsigned cap) {
   P::publish_fence();
   P::store(&en[2], (int)(h + cap));
+  P::fetch_add(&ctl[3], ~0u);
 }
 
 // ---------------------------------------------------------------------------

@@ -482,12 +482,13 @@ int main(int argc, char** argv) {
         if (k < events) uBad += memcmp(cu.data() + k * n, uRefBits.data(), n * 4) != 0;
     }
     const EventResult er = rig.readEvents(0);
-    unsigned long long retreats = 0, resumed = 0, errors = 0, saveTicks = 0;
+    unsigned long long retreats = 0, resumed = 0, errors = 0, saveTicks = 0, declined = 0;
     for (int b = 0; b < blocks + rs.extraRows; ++b) {
       const unsigned long long* st = &er.stats[(size_t)b * APK_STATS_PER_BLOCK];
       retreats += st[APK_ST_RETREATS];
       resumed += st[APK_ST_RESUMED];
       errors += st[APK_ST_ERRORS];
+      declined += st[APK_ST_DECLINED];
       saveTicks += st[APK_ST_SAVE];
     }
     // The background alone again, now that the engine clock has settled
@@ -550,9 +551,10 @@ int main(int argc, char** argv) {
            "it, the polled kernel alone %.2f%% below it\n", tfOff, (1.0 - tfJob / tfOff) * 100.0,
            (1.0 - tfAlone / tfOff) * 100.0);
     printf("retreats %llu | resumed %llu | save %.2f us per retreat | arrivals without a "
-           "retreat %d | late drains %d | resume errors %llu | lost %u\n", retreats, resumed,
+           "retreat %d | late drains %d | resume errors %llu | lost %u | declined (ring full) "
+           "%llu | unreleased %u\n", retreats, resumed,
            retreats ? saveTicks * tickUs / retreats : 0.0, noRetreat, lateDrains, errors,
-           rr.tail - rr.head);
+           rr.tail - rr.head, declined, rr.unreleased);
     printf("SAFETY: %lld of %u task fingerprints differ from the unpreempted tile | urgent "
            "outputs not bit-identical: %lld of %d kept\n", hashBad, jobTasks, uBad,
            std::min(events, keepCu + 1));
@@ -561,7 +563,8 @@ int main(int argc, char** argv) {
              oracleBad == 0 ? "PASS" : "FAIL", oracleBad);
     if (csvPath[0]) printf("raw per-arrival records: %s\n", csvPath);
     const bool pass = hashBad == 0 && uBad == 0 && rr.tail == rr.head && errors == 0 &&
-                      oracleBad == 0 && !raise.empty();
+                      rr.unclaimed == 0 && rr.unreleased == 0 && oracleBad == 0 &&
+                      !raise.empty();
     printf("yield: %s\n", pass ? "PASS" : "FAIL");
     return pass ? 0 : 1;
   }
@@ -645,6 +648,7 @@ int main(int argc, char** argv) {
         rr = rig.readRetreat(1);
       }
       if (rr.tail != rr.head) lost += rr.tail - rr.head;
+      if (rr.unreleased != 0) ++errors;  // an entry claimed but never released
       if (rr.tail == 0) ++noRetreat;
       const EventResult er = rig.readEvents(0);
       for (int b = 0; b < blocks + retreatBlocks; ++b) {

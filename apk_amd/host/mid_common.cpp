@@ -460,9 +460,16 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
     printf("per yield: save %.2f us, urgent %.2f us, restore %.2f us\n",
            tSave / dev.wall_mhz / yields, tUrg / dev.wall_mhz / yields,
            tRest / dev.wall_mhz / yields);
+  // With tasks cycling the grid, C holds only the last pass's writes: its
+  // bit-identity says nothing about the earlier passes, which the
+  // fingerprints cover.
+  const bool cycles = tasks > (unsigned)totalTiles;
   printf("resumed background: %lld of %lld task fingerprints differ from the unpreempted "
          "tile%s | C bit-identical to the unpreempted run: %s\n", hashBad, hashed,
-         hashAll ? "" : " (not hashed: too many tasks)", cBits ? "yes" : "NO");
+         hashAll ? "" : " (not hashed: too many tasks)",
+         cycles ? (cBits ? "last pass yes (tasks cycle the grid; see fingerprints)"
+                         : "last pass NO (tasks cycle the grid; see fingerprints)")
+                : (cBits ? "yes" : "NO"));
   if (!lat.empty()) {
     printf("latency set->last (us): p50 %.2f | p90 %.2f | p99 %.2f  (excl setter p50 %.2f, "
            "setter-last %.1f%%)\n", percentile(lat, 0.5), percentile(lat, 0.9),

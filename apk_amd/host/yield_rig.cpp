@@ -63,7 +63,7 @@ YieldRig::YieldRig(const RigShape& s, const std::vector<uint8_t>& A,
   if (s.retreatCap) {
     dRetreatCount_ = dalloc<int>((size_t)(E + 1) * APK_RETREAT_DOMAINS);  // + registrations
     dRetreatGT_ = dalloc<long long>(2 * (size_t)E);
-    dRqCtl_ = dalloc<unsigned>(3);
+    dRqCtl_ = dalloc<unsigned>(APK_RQ_CTL_WORDS);
     dRqEntry_ = dalloc<int>((size_t)s.retreatCap * 4);
     if (s.retreatSlots)
       dRqSlots_ = dalloc<float>((size_t)s.retreatCap * apk_yield_ckpt_floats(s.engine));
@@ -206,7 +206,7 @@ void YieldRig::resetRetreat() {
   std::vector<long long> gt(2 * (size_t)E, 0);
   for (int e = 0; e < E; ++e) gt[2 * (size_t)e] = INT64_MAX;
   HIP_CHECK(hipMemcpy(dRetreatGT_, gt.data(), gt.size() * 8, hipMemcpyHostToDevice));
-  HIP_CHECK(hipMemset(dRqCtl_, 0, 3 * sizeof(unsigned)));
+  HIP_CHECK(hipMemset(dRqCtl_, 0, APK_RQ_CTL_WORDS * sizeof(unsigned)));
   // entry i = {task, stage, seq, kind << 8 | domain}; seq = i: free for ticket i
   std::vector<int> en((size_t)s_.retreatCap * 4, 0);
   for (unsigned i = 0; i < s_.retreatCap; ++i) en[(size_t)i * 4 + 2] = (int)i;
@@ -275,10 +275,12 @@ RetreatResult YieldRig::readRetreat(int nEvents) const {
   HIP_CHECK(hipMemcpy(r.retreatGT.data(), dRetreatGT_, 2 * (size_t)n * 8, hipMemcpyDeviceToHost));
   HIP_CHECK(hipMemcpy(r.count.data(), dRetreatCount_, r.count.size() * sizeof(int),
                       hipMemcpyDeviceToHost));
-  unsigned ctl[2];
+  unsigned ctl[APK_RQ_CTL_WORDS];
   HIP_CHECK(hipMemcpy(ctl, dRqCtl_, sizeof ctl, hipMemcpyDeviceToHost));
   r.head = ctl[0];
   r.tail = ctl[1];
+  r.unclaimed = ctl[2];
+  r.unreleased = ctl[3];
   // the domains of the last min(tail, capacity) retreats, oldest first
   const unsigned n4 = std::min(r.tail, s_.retreatCap);
   std::vector<int> en((size_t)s_.retreatCap * 4);

@@ -35,8 +35,10 @@ struct RigShape {
 struct RetreatResult {
   std::vector<long long> setGT;       // flag raised (apk_raise_flag)
   std::vector<long long> retreatGT;   // [2e] earliest checkpoint start, [2e+1] latest exit
-  std::vector<int> count;             // [e * 32 + domain] blocks that asked for a retreat slot
+  std::vector<int> count;             // [e * 32 + domain] blocks that retreated
   unsigned head = 0, tail = 0;        // resume tickets popped / reserved
+  unsigned unclaimed = 0;             // reserved tickets not yet claimed (0 once drained)
+  unsigned unreleased = 0;            // reserved tickets not yet released (0 once drained)
   std::vector<int> xcd;               // per reserved ticket: domain (xcd * 4 + se) that retreated
 };
 

@@ -23,12 +23,18 @@
 // wrong stage, a lost or duplicated stage, or a stale checkpoint changes the
 // result. Checked at the end: every task ran to completion exactly once with
 // the expected result, every fired event's urgent tiles ran exactly once
-// (coop), and the resume ring is empty with no lost or refused entry.
+// (coop), and the resume ring is empty -- every ticket claimed and released,
+// no wait run out (lost, stuck). Retreats the ring declined because it was
+// full ("refused") are allowed: the declining block keeps its tile.
 //
+// --rq-wait-us sets the ring's wait deadlines (the kernels' 20 ms by default).
 // --bug plants one mistake, to show that the checks see it:
 //   publish-early   (retreat) publish the ticket before writing the slot
 //   resume-skip     resume one stage past the checkpointed stage
 //   no-release      (retreat) never free a consumed ring entry
+//   no-gate         (retreat) reserve without the occupancy gate: take a ticket
+//                   first and decline when its entry stays taken past the
+//                   deadline (this leaves a hole in the ticket order)
 //   double-serve    (coop) serve the urgent tile popped by the previous block again
 //
 // Exit status 0 when every check passes, 1 otherwise; one summary line.
@@ -97,7 +103,7 @@ uint64_t expected(unsigned tile, int S, bool urgent) {
 }
 
 enum Resume { R_FULL = 2, R_ACC = 1, R_RESTART = 0 };
-enum Bug { B_NONE, B_PUBLISH_EARLY, B_RESUME_SKIP, B_NO_RELEASE, B_DOUBLE_SERVE };
+enum Bug { B_NONE, B_PUBLISH_EARLY, B_RESUME_SKIP, B_NO_RELEASE, B_NO_GATE, B_DOUBLE_SERVE };
 
 struct Config {
   bool retreat = false;
@@ -105,6 +111,7 @@ struct Config {
   double meanGapUs = 300;
   int workNs = 2000, pollEvery = 1, resume = R_FULL, retreatN = 32, cap = 0, urgentTiles = 4;
   int domains = APK_RETREAT_DOMAINS;
+  int64_t rqWaitTicks = proto::RQ_WAIT_TICKS;
   unsigned seed = 21;
   Bug bug = B_NONE;
 };
@@ -129,10 +136,10 @@ struct Sim {
   std::vector<uint64_t> result;              // per task
   std::vector<int> retreatCount;             // per event x domain
   std::vector<int> regCount;                 // first grid's blocks per domain, as they start
-  unsigned rqCtl[3] = {0, 0, 0};
+  unsigned rqCtl[APK_RQ_CTL_WORDS] = {0, 0, 0, 0};
   std::vector<int> rqEntry;                  // cap x 4
   std::vector<Ckpt> rqSlot;                  // cap
-  std::atomic<long> retreats{0}, resumed{0}, refused{0}, lost{0}, yields{0};
+  std::atomic<long> retreats{0}, resumed{0}, refused{0}, stuck{0}, lost{0}, yields{0};
   std::atomic<int> running{0};
   std::atomic<int> fired{0};
 
@@ -150,6 +157,22 @@ struct Sim {
     rqEntry.assign((size_t)c.cap * 4, 0);
     for (int i = 0; i < c.cap; ++i) rqEntry[(size_t)i * 4 + 2] = i;  // seq = i: free
     rqSlot.assign(c.cap, Ckpt{});
+  }
+
+  // The planted no-gate mistake: the reservation without its occupancy gate
+  // (ticket first; a ticket whose entry stays taken past the deadline is
+  // declined after it was taken).
+  unsigned reserve_ungated() {
+    const unsigned t = HostPlat::fetch_add(&rqCtl[1], 1u);
+    const int* en = &rqEntry[(size_t)(t % (unsigned)c.cap) * 4];
+    const int64_t deadline = HostPlat::ticks() + c.rqWaitTicks;
+    while (t >= (unsigned)c.cap && HostPlat::load(&en[2]) != (int)t) {
+      if (HostPlat::ticks() > deadline) return proto::RQ_FULL;
+      HostPlat::pause();
+    }
+    HostPlat::fetch_add(&rqCtl[3], 1u);  // keep the occupancy count balanced
+    HostPlat::fetch_add(&rqCtl[2], 1u);
+    return t;
   }
 
   // One block: `cont` for a continuation launched after generation `epoch`.
@@ -180,7 +203,7 @@ struct Sim {
         const unsigned q = proto::rq_pop<HostPlat>(rqCtl);
         if (q != proto::RQ_NONE) {
           int* en = &rqEntry[(size_t)(q % (unsigned)c.cap) * 4];
-          const int ready = proto::rq_wait_ready<HostPlat>(en, q);
+          const int ready = proto::rq_wait_ready<HostPlat>(en, q, c.rqWaitTicks);
           if (ready == 0) {
             lost.fetch_add(1);
             continue;
@@ -189,7 +212,7 @@ struct Sim {
           kind = ready - 1;
           if (kind > 0) ck = rqSlot[q % (unsigned)c.cap];
           ck.stage = en[1];
-          if (c.bug != B_NO_RELEASE) proto::rq_release<HostPlat>(en, q, (unsigned)c.cap);
+          if (c.bug != B_NO_RELEASE) proto::rq_release<HostPlat>(rqCtl, en, q, (unsigned)c.cap);
           resumed.fetch_add(1);
         }
       }
@@ -243,12 +266,14 @@ struct Sim {
               const bool chosen = mayRetreat;
               if (!cont) mayRetreat = false;
               if (role == proto::RETREAT_ALL || (role == proto::RETREAT_BY_QUOTA && chosen)) {
-                __atomic_fetch_add(&retreatCount[(size_t)ev * c.domains + dom], 1,
-                                   __ATOMIC_RELAXED);
-                unsigned t = proto::rq_reserve<HostPlat>(rqCtl, (unsigned)c.cap,
-                                                         rqEntry.data());
-                if (t & proto::RQ_FULL) {
+                const unsigned t = c.bug == B_NO_GATE
+                                       ? reserve_ungated()
+                                       : proto::rq_reserve<HostPlat>(rqCtl, (unsigned)c.cap,
+                                                                     rqEntry.data(), c.rqWaitTicks);
+                if (t == proto::RQ_FULL) {
                   refused.fetch_add(1);
+                } else if (t & proto::RQ_STUCK) {
+                  stuck.fetch_add(1);
                 } else {
                   int* en = &rqEntry[(size_t)(t % (unsigned)c.cap) * 4];
                   const int rk = c.resume;
@@ -260,6 +285,8 @@ struct Sim {
                     rqSlot[t % (unsigned)c.cap] = mine;
                     proto::rq_publish<HostPlat>(en, t, (int)task, rk > 0 ? s : 0, rk, dom);
                   }
+                  __atomic_fetch_add(&retreatCount[(size_t)ev * c.domains + dom], 1,
+                                     __ATOMIC_RELAXED);
                   retreats.fetch_add(1);
                   retreated = true;
                   break;
@@ -311,6 +338,7 @@ Bug parse_bug(const std::string& s) {
   if (s == "publish-early") return B_PUBLISH_EARLY;
   if (s == "resume-skip") return B_RESUME_SKIP;
   if (s == "no-release") return B_NO_RELEASE;
+  if (s == "no-gate") return B_NO_GATE;
   if (s == "double-serve") return B_DOUBLE_SERVE;
   return B_NONE;
 }
@@ -340,6 +368,7 @@ int main(int argc, char** argv) {
     else if (k == "--urgent-tiles") c.urgentTiles = atoi(v);
     else if (k == "--domains") c.domains = atoi(v);
     else if (k == "--seed") c.seed = (unsigned)atoi(v);
+    else if (k == "--rq-wait-us") c.rqWaitTicks = (int64_t)(atof(v) * 100.0);
     else if (k == "--bug") bug = v;
     else {
       fprintf(stderr, "unknown option %s\n", k.c_str());
@@ -349,7 +378,7 @@ int main(int argc, char** argv) {
   c.bug = parse_bug(bug);
   if (c.blocks < 1 || c.stages < 2 || c.events < 0 || c.pollEvery < 1 || c.domains < 1 ||
       c.domains > APK_RETREAT_DOMAINS || c.urgentTiles < 1 || c.tilesM < 1 || c.tilesN < 1 ||
-      c.passes < 1) {
+      c.passes < 1 || (c.cap != 0 && c.cap < 2) || c.rqWaitTicks < 0) {
     fprintf(stderr, "bad configuration\n");
     return 2;
   }
@@ -419,16 +448,21 @@ int main(int argc, char** argv) {
       }
     }
   const long left = (long)(HostPlat::load(&sim.rqCtl[1]) - HostPlat::load(&sim.rqCtl[0]));
+  const long unclaimed = (int)HostPlat::load(&sim.rqCtl[2]);
+  const long unreleased = (int)HostPlat::load(&sim.rqCtl[3]);
   const bool ok = dup == 0 && miss == 0 && wrong == 0 && uBad == 0 && left == 0 &&
-                  sim.lost.load() == 0 && sim.refused.load() == 0 &&
+                  unclaimed == 0 && unreleased == 0 && sim.lost.load() == 0 &&
+                  sim.stuck.load() == 0 &&
                   (!c.retreat || sim.resumed.load() == sim.retreats.load());
   printf("%s arm=%s blocks=%d tasks=%u stages=%d resume=%s events fired=%d | tasks: dup %ld "
-         "miss %ld wrong %ld | %s %ld | resumed %ld | ring left %ld lost %ld refused %ld | "
-         "drains %d | urgent bad %ld unclaimed %ld | bug=%s\n",
+         "miss %ld wrong %ld | %s %ld | resumed %ld | ring left %ld lost %ld refused %ld "
+         "stuck %ld unreleased %ld unclaimed tickets %ld | drains %d | urgent bad %ld "
+         "unclaimed %ld | bug=%s\n",
          ok ? "PASS" : "FAIL", c.retreat ? "retreat" : "coop", c.blocks, sim.numTasks, c.stages,
          c.resume == R_FULL ? "full" : c.resume == R_ACC ? "acc" : "restart", fired, dup, miss,
          wrong, c.retreat ? "retreats" : "yields",
          c.retreat ? sim.retreats.load() : sim.yields.load(), sim.resumed.load(), left,
-         sim.lost.load(), sim.refused.load(), drains, uBad, uUnclaimed, bug.c_str());
+         sim.lost.load(), sim.refused.load(), sim.stuck.load(), unreleased, unclaimed, drains,
+         uBad, uUnclaimed, bug.c_str());
   return ok ? 0 : 1;
 }

@@ -201,13 +201,19 @@ enum {
                            stage had not yet written its LDS bytes */
   APK_ST_RETREATS = 5,  /* retreats (retreat arm) */
   APK_ST_RESUMED = 6,   /* resume-queue entries taken */
-  APK_ST_ERRORS = 7,    /* resume entries never published in time (lost) */
+  APK_ST_ERRORS = 7,    /* resume-ring waits that ran out (a block holding an
+                           entry stopped): entries never published in time
+                           (lost), or entries never freed for a reserved
+                           ticket; 0 in every correct run */
   APK_ST_STALE = 8,     /* resumed checkpoints holding LDS stages that differ
                            from the stages once every load had landed (naive
                            only); each resumes a wrong tile */
   APK_ST_CHECKPOINTS = 9, /* checkpoints taken (issue sites: every observer) */
   APK_ST_INFLIGHT_ALL = 10, /* APK_ST_INFLIGHT over every checkpoint taken */
-  APK_ST_STALE_ALL = 11     /* APK_ST_STALE over every checkpoint taken */
+  APK_ST_STALE_ALL = 11,    /* APK_ST_STALE over every checkpoint taken */
+  APK_ST_DECLINED = 12      /* retreats declined because the resume ring held
+                               rq_capacity unreleased tickets (the block kept
+                               its tile and worked on; nothing is lost) */
 };
 
 /* Work queue: every persistent kernel pops tasks from APK_QUEUE_WORDS
@@ -218,6 +224,8 @@ enum {
  * when it is empty. Task u always computes tile u mod (tilesM * tilesN). */
 #define APK_QUEUE_WORDS 16
 #define APK_QUEUE_XCDS 8
+/* Control words of the retreat arm's resume ring (apk_yield_params.rq_ctl). */
+#define APK_RQ_CTL_WORDS 4
 /* Dispatch domains of the retreat arm: a workgroup is dealt round-robin to
  * one of the 8 XCDs and then to one of its 4 shader engines, and runs only
  * on a CU of that shader engine. */
@@ -315,16 +323,22 @@ typedef struct apk_yield_params {
                                     row `events` the first grid's registrations */
   long long* retreat_gt;         /* [2 * events] or NULL: [2e] earliest checkpoint
                                     start (host sets INT64_MAX), [2e+1] latest exit (0) */
-  unsigned int* rq_ctl;          /* resume queue tickets, 3 words: [0] head, [1] tail,
-                                    [2] reserved tickets not yet claimed; 0 at job start */
+  unsigned int* rq_ctl;          /* resume queue tickets, 4 words: [0] head, [1] tail,
+                                    [2] reserved tickets not yet claimed, [3] tickets
+                                    reserved and not yet released; 0 at job start */
   int* rq_entry;                 /* [rq_capacity * 4], a ring: ticket t uses entry t %
                                     rq_capacity = {task, stage, seq, kind << 8 | domain
                                     (xcd * 4 + shader engine of the retreating block)};
                                     seq = t: free, t + 1: published, set to t + capacity
                                     once read back. At job start entry i holds seq = i. */
   float* rq_slots;               /* rq_capacity * apk_yield_ckpt_floats(engine) floats */
-  unsigned int rq_capacity;      /* entries in the ring; a retreat that finds its entry
-                                    still in use (ring full) is declined */
+  unsigned int rq_capacity;      /* entries in the ring, at least 2 (APK_EINVAL
+                                    otherwise). A retreat that finds rq_capacity
+                                    tickets unreleased is declined before it takes a
+                                    ticket (APK_ST_DECLINED; the block keeps its tile).
+                                    Sizing: 32 * ceil(retreat / 32) entries hold one
+                                    generation's retreats, so none is declined while
+                                    each generation is resumed before the next. */
   int continuation;              /* 1: a relaunch joining a running job -- generations
                                     already raised when it starts are not acted on */
   int block_base;                /* this launch's first row in obs_gt columns and stats */

@@ -120,6 +120,10 @@ def test_python_constants_match_header():
     assert int(defines["APK_QUEUE_XCDS"]) == apk_amd.QUEUE_XCDS
     assert int(defines["APK_SES_PER_XCD"]) == apk_amd.SES_PER_XCD
     assert int(defines["APK_RETREAT_DOMAINS"]) == apk_amd.RETREAT_DOMAINS == 32
+    assert int(defines["APK_RQ_CTL_WORDS"]) == apk_amd.RQ_CTL_WORDS == 4
+    stats = dict(re.findall(r"(APK_ST_\w+) = (\d+)", text))
+    assert int(stats["APK_ST_DECLINED"]) == apk_amd.ST_DECLINED == 12
+    assert int(stats["APK_ST_ERRORS"]) == apk_amd.ST_ERRORS == 7
 
 
 def test_retreat_arm_rejects_bad_args():
@@ -135,6 +139,11 @@ def test_retreat_arm_rejects_bad_args():
     assert call() == apk_amd.APK_EINVAL and b"resume queue" in lib.apk_last_error()
     p.num_events = 1
     p.retreat_count = p.rq_ctl = p.rq_entry = fake
+    # a ring of one entry cannot tell "published by ticket t" (seq t + 1)
+    # from "free for ticket t + 1" (t + capacity): at least 2 entries
+    for cap in (0, 1):
+        p.rq_capacity = cap
+        assert call() == apk_amd.APK_EINVAL and b"at least 2 entries" in lib.apk_last_error()
     p.rq_capacity = 2
     assert call() == apk_amd.APK_EINVAL and b"rq_slots" in lib.apk_last_error()
     p.rq_slots = fake

@@ -8,10 +8,16 @@ and exits non-zero on any violation):
         run's, the urgent output is bit-identical, every task runs once;
   cfg4  fp32 M=N=K=8192, 3-stage LDS ring, >= 25,000 k-stage yields with
         checkpoint/resume: C bit-identical to the unpreempted run, float64
-        within 1e-5 rel-Frobenius, exactly-once; plus the issue site;
-  cfg5  bf16 M=N=K=8192, 256x256 tiles, yields at k-stage and tile-boundary
-        sites: C bit-identical, float64 (bf16-rounded inputs) within 1e-2,
-        exactly-once; the 1e8-task tiny oracle at 1, 2 and 4 blocks per CU.
+        within 1e-5 rel-Frobenius, exactly-once; plus the issue site, where
+        >= 25,000 checkpoints are taken while a live stage is still in flight
+        (the buffer-conflicting yields) and the drain keeps every one exact;
+  cfg5  bf16 M=N=K=8192, 256x256 tiles at 1 block per CU and the 128x128
+        tile at 2 and 4 blocks per CU, yields at k-stage (and for 256x256
+        tile-boundary) sites: C bit-identical, float64 (bf16-rounded inputs)
+        within 1e-2, exactly-once; the 1e8-task tiny oracle at 1, 2 and 4
+        blocks per CU.
+When tasks cycle the grid (more tasks than tiles) C holds the last pass, so
+every task's fingerprint against its unpreempted tile is checked as well.
 """
 import os
 import re
@@ -52,12 +58,20 @@ def grab(text, pattern, cast=int):
     return tuple(cast(g) for g in m.groups())
 
 
+def assert_identical(out):
+    """C bit-identical to the unpreempted run (its last pass, when tasks cycle
+    the grid) and no task fingerprint differing from its unpreempted tile."""
+    bad, hashed = grab(out, r"resumed background: (\d+) of (\d+) task fingerprints differ")
+    assert bad == 0 and hashed > 0, (bad, hashed)
+    assert re.search(r"C bit-identical to the unpreempted run: (yes|last pass yes)", out), out[-2000:]
+
+
 def test_cfg4_stage_yields_25k():
     out = run_bin("midyield", *CFG4, "--mode", "events", "--poll", "stage", "--events", 26000,
                   "--oracle", 1)
     yields, = grab(out, r"yields: (\d+)")
     assert yields >= 25000
-    assert "C bit-identical to the unpreempted run: yes" in out
+    assert_identical(out)
     corrupt, = grab(out, r"SAFETY: (\d+)/")
     assert corrupt == 0
     assert "ORACLE: PASS" in out
@@ -69,9 +83,14 @@ def test_cfg4_issue_site(disc):
                   disc, "--events", 4000, "--oracle", 1)
     assert "ORACLE: PASS" in out
     if disc == "drain":
-        assert "C bit-identical to the unpreempted run: yes" in out
+        assert_identical(out)
         stale, = grab(out, r"stale checkpoints: (\d+)")
         assert stale == 0
+        # every observer checkpoints at an issue site; the buffer-conflicting
+        # ones found the newest stage's loads still landing when the drain began
+        ckpts, inflight = grab(out, r"\(of all (\d+) checkpoints: (\d+)\)")
+        say(f"  issue-site checkpoints {ckpts}, live stage in flight at {inflight}")
+        assert inflight >= 25000, (ckpts, inflight)
     else:
         # the drain is load-bearing: without it some checkpoints are stale,
         # and exactly those resumes differ from the unpreempted tile
@@ -85,7 +104,26 @@ def test_cfg4_issue_site(disc):
 def test_cfg5_bf16_yields(poll):
     out = run_bin("tcyield", *CFG5, "--mode", "events", "--poll", poll, "--events", 1500,
                   "--oracle", 1)
-    assert "C bit-identical to the unpreempted run: yes" in out
+    assert_identical(out)
+    corrupt, = grab(out, r"SAFETY: (\d+)/")
+    assert corrupt == 0
+    assert "ORACLE: PASS" in out
+
+
+CFG5_128 = ["--tiles-m", 64, "--tiles-n", 64, "--gemm-k", 8192, "--k", 256, "--urgent-m", 256,
+            "--urgent-n", 256, "--urgent-k", 256, "--verify-rows", 32]
+
+
+@pytest.mark.parametrize("engine,blocks", [("bf16x128", 512), ("bf16x128", 1024),
+                                           ("bf16x128k32", 512)])
+def test_cfg5_bf16x128_yields_multi_block(engine, blocks):
+    """cfg5 at 2 and 4 blocks per CU (the 256x256 tile cannot hold them):
+    128x128 bf16 tiles, k-stage yields with checkpoint/resume."""
+    out = run_bin("tcyield", *CFG5_128, "--engine", engine, "--blocks", blocks, "--mode",
+                  "events", "--poll", "stage", "--events", 1500, "--oracle", 1)
+    yields, = grab(out, r"yields: (\d+)")
+    assert yields >= 1000
+    assert_identical(out)
     corrupt, = grab(out, r"SAFETY: (\d+)/")
     assert corrupt == 0
     assert "ORACLE: PASS" in out

@@ -90,15 +90,22 @@ def test_mfma128_single_tile_and_idle_workers(torch_gpu, apk):
     assert_queue_drained(nxt, 1, 64)  # one tile taken; every worker's last pop failed
 
 
-def test_cfg2_full_size_sampled_rows(torch_gpu, apk):
-    # BASELINE cfg2 shape: M=N=K=4096, 128x128 tiles, K walked in 32-chunks.
-    say("mfma128 cfg2 M=N=K=4096 kc=32")
-    A, B = oracle.fill_uniform_pm1(21, 4096, 4096, 4096)
-    C, recs, _ = run_persistent(torch_gpu, apk, apk.ENGINE_MFMA128, A, B, 32)
+@pytest.fixture(scope="module")
+def cfg2_operands():
+    return oracle.fill_uniform_pm1(21, 4096, 4096, 4096)
+
+
+@pytest.mark.parametrize("kc", [32, 64, 128])
+def test_cfg2_full_size_sampled_rows(torch_gpu, apk, cfg2_operands, kc):
+    # BASELINE cfg2 shape: M=N=K=4096, 128x128 tiles, K walked in kc-chunks
+    # (the per-tile K set {32, 64, 128}).
+    say(f"mfma128 cfg2 M=N=K=4096 kc={kc}")
+    A, B = cfg2_operands
+    C, recs, _ = run_persistent(torch_gpu, apk, apk.ENGINE_MFMA128, A, B, kc)
     assert not np.isnan(C).any()
     rows = [0, 127, 128, 2049, 4095]
     for r in rows:
         ref = oracle.gemm_f64_rows(A, B, r, 1)
         assert oracle.rel_frobenius(C[r:r + 1], ref) <= FROB_F32, r
     assert (recs["block"] >= 0).all()
-    assert len(recs["block"]) == 32 * 32 * 128
+    assert len(recs["block"]) == 32 * 32 * (4096 // kc)

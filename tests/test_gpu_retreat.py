@@ -52,7 +52,8 @@ def _streams():
 
 
 class RetreatJob:
-    def __init__(self, torch, apk, engine, M, N, K, kc, Mu, Nu, Ku, passes, retreat, seed=21):
+    def __init__(self, torch, apk, engine, M, N, K, kc, Mu, Nu, Ku, passes, retreat, seed=21,
+                 cap=None):
         T = torch
         self.t, self.apk, self.engine = T, apk, engine
         g = apk.geometry(engine)
@@ -65,6 +66,7 @@ class RetreatJob:
         self.R = retreat
         D = apk.RETREAT_DOMAINS
         self.RB = D * ((retreat + D - 1) // D)
+        self.cap = cap or self.RB  # resume ring entries
         self.blocks = apk.device_info().cu_count * min(
             1, apk.yield_occupancy(engine, apk.POLL_STAGE))
         if g.elem_bytes == 2:   # bf16 bit patterns; B passed transposed (N x K)
@@ -89,9 +91,10 @@ class RetreatJob:
         # one event's retreats, then the first grid's registrations
         self.rcount = T.zeros(2 * apk.RETREAT_DOMAINS, dtype=i32, device="cuda")
         self.rgt = T.zeros(2, dtype=i64, device="cuda")
-        self.rq_ctl = T.zeros(3, dtype=i32, device="cuda")
-        self.rq_entry = T.zeros(4 * self.RB, dtype=i32, device="cuda")
-        self.rq_slots = T.zeros(self.RB * apk.ckpt_floats(engine), dtype=T.float32, device="cuda")
+        self.rq_ctl = T.zeros(apk.RQ_CTL_WORDS, dtype=i32, device="cuda")
+        self.rq_entry = T.zeros(4 * self.cap, dtype=i32, device="cuda")
+        self.rq_slots = T.zeros(self.cap * apk.ckpt_floats(engine), dtype=T.float32,
+                                device="cuda")
         rows = 2 * self.blocks + self.RB
         self.stats = T.zeros(rows * apk.STATS_PER_BLOCK, dtype=i64, device="cuda")
         self.task_hash = T.zeros(self.num_tasks, dtype=i64, device="cuda")
@@ -112,7 +115,7 @@ class RetreatJob:
         p.exec_count = self.exec_count.data_ptr()
         p.retreat, p.retreat_count, p.retreat_gt = self.R, self.rcount.data_ptr(), self.rgt.data_ptr()
         p.rq_ctl, p.rq_entry = self.rq_ctl.data_ptr(), self.rq_entry.data_ptr()
-        p.rq_slots, p.rq_capacity = self.rq_slots.data_ptr(), self.RB
+        p.rq_slots, p.rq_capacity = self.rq_slots.data_ptr(), self.cap
         p.continuation, p.block_base = continuation, block_base
         if not continuation:
             p.run_gt, p.exit_count = self.run_gt.data_ptr(), self.exit_count.data_ptr()
@@ -124,8 +127,8 @@ class RetreatJob:
                   self.exit_count):
             x.zero_()
         # resume ring: entry i starts free for ticket i (seq = i)
-        self.rq_entry.view(self.RB, 4)[:, 2] = self.t.arange(self.RB, dtype=self.t.int32,
-                                                             device="cuda")
+        self.rq_entry.view(self.cap, 4)[:, 2] = self.t.arange(self.cap, dtype=self.t.int32,
+                                                              device="cuda")
         self.rgt[0] = np.iinfo(np.int64).max
         self.rgt[1] = 0
         self.dC.fill_(float("nan"))
@@ -185,6 +188,7 @@ def _check(job, ref, r):
                                    f"[{t0}, {t1}]: the two streams did not run concurrently")
     assert head == tail == job.RB, (head, tail, r["set_gt"] - t0, t1 - t0, r["rgt"] - t0)
     assert int(r["ctl"][2]) == 0, f"{int(r['ctl'][2])} reserved tickets left unclaimed"
+    assert int(r["ctl"][3]) == 0, f"{int(r['ctl'][3])} reserved tickets left unreleased"
     assert int(st[:, 5].sum()) == job.RB and int(st[:, 6].sum()) == job.RB
     assert int(st[:, 7].sum()) == 0, "resume entries lost"
     assert r["set_gt"] > 0 and r["set_gt"] <= r["rgt"][0] <= r["rgt"][1]
@@ -235,10 +239,38 @@ def test_retreat_every_worker(torch_gpu, apk, resume):
     r = job.run(apk.POLL_STAGE, resume)
     assert (_bits(r["C"]) == _bits(ref["C"])).all(), "C differs from the unpreempted run"
     assert (r["exec"] == 1).all(), "exactly-once violated"
-    head, tail, left = (int(x) for x in r["ctl"])
+    head, tail, left, held = (int(x) for x in r["ctl"])
     st = r["stats"]
-    assert head == tail and left == 0, (head, tail, left)
+    assert head == tail and left == 0 and held == 0, (head, tail, left, held)
     # every block on a CU of its own, 8 per (XCD, shader engine) domain: all retreat
     assert tail == job.RB == blocks, (tail, job.RB)
     assert int(st[:, 5].sum()) == tail and int(st[:, 6].sum()) == tail
     assert int(st[:, 7].sum()) == 0, "resume entries lost"
+
+
+@pytest.mark.parametrize("resume", [1, 2])
+def test_retreat_ring_smaller_than_a_generation(torch_gpu, apk, resume):
+    """Every worker asks to retreat at once into a ring of 64 entries: the
+    ring admits as many retreats as it has entries free and declines the rest
+    before they take a ticket (the declining block keeps its tile), so nothing
+    is lost -- C bit-identical, every task once, every ticket claimed and
+    released, no resume error."""
+    say(f"building mfma128 small-ring retreat job M=N=1024 K=4096 kc=128, cap 64, resume={resume}")
+    blocks = apk.device_info().cu_count
+    job = RetreatJob(torch_gpu, apk, apk.ENGINE_MFMA128, 1024, 1024, 4096, 128, 256, 256, 256,
+                     passes=16, retreat=blocks, cap=64)
+    ref = job.run(apk.POLL_STAGE, apk.RESUME_CKPT_FULL, preempt=False)
+    r = job.run(apk.POLL_STAGE, resume)
+    assert (_bits(r["C"]) == _bits(ref["C"])).all(), "C differs from the unpreempted run"
+    assert (r["exec"] == 1).all(), (f"exactly-once violated: {int((r['exec'] > 1).sum())} dup, "
+                                   f"{int((r['exec'] == 0).sum())} missed")
+    want = ref["task_hash"][np.arange(job.num_tasks) % job.tiles]
+    assert (r["task_hash"] == want).all(), "task fingerprints differ"
+    head, tail, left, held = (int(x) for x in r["ctl"])
+    st = r["stats"]
+    retreats, declined = int(st[:, apk.ST_RETREATS].sum()), int(st[:, apk.ST_DECLINED].sum())
+    say(f"retreats {retreats} declined {declined} tickets {tail}")
+    assert head == tail == retreats and left == 0 and held == 0, (head, tail, left, held)
+    assert int(st[:, apk.ST_RESUMED].sum()) == retreats
+    assert int(st[:, apk.ST_ERRORS].sum()) == 0, "resume-ring wait ran out"
+    assert retreats >= 64 and declined > 0 and retreats + declined == blocks, (retreats, declined)

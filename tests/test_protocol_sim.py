@@ -4,8 +4,10 @@ here for the host) driven by std::thread blocks under random preemption.
 
 Every arm and resume mode must pass its end checks (each task completed once
 with the order-sensitive expected result, each fired event's urgent tiles
-served once, the resume ring empty with nothing lost or refused), and each
-planted protocol mistake must be caught by the check that names it."""
+served once, the resume ring empty: every ticket claimed and released, no
+wait run out), also with a ring smaller than one generation's retreats, where
+retreats are declined ("refused") and nothing may be lost; and each planted
+protocol mistake must be caught by the check that names it."""
 import os
 import re
 import subprocess
@@ -14,15 +16,17 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 SIM = os.path.join(ROOT, "apk_amd", "bin", "protocol_sim")
+SIM_BIN = SIM  # the sanitizer gate reruns these cases on instrumented builds
 # A job that outlasts the events: 8192 tasks of 16 stages on 16 blocks.
 JOB = ["--tiles-m", "16", "--tiles-n", "16", "--passes", "32", "--stages", "16",
        "--mean-gap-us", "100", "--events", "200", "--blocks", "16"]
 
 
-def run(*args):
-    assert os.access(SIM, os.X_OK), "apk_amd/bin/protocol_sim not built"
-    r = subprocess.run([SIM] + JOB + [str(a) for a in args], capture_output=True, text=True,
-                       timeout=120)
+def run(*args, sim=None, job=True, timeout=120):
+    sim = sim or SIM
+    assert os.access(sim, os.X_OK), f"{sim} not built"
+    r = subprocess.run([sim] + (JOB if job else []) + [str(a) for a in args],
+                       capture_output=True, text=True, timeout=timeout)
     line = r.stdout.strip().splitlines()[-1] if r.stdout.strip() else r.stderr
     fields = {k: int(v) for k, v in re.findall(r"([a-z]+(?: [a-z]+)?) (-?\d+)", line)}
     return r.returncode, line, fields
@@ -73,10 +77,65 @@ def test_coop_poll_every_4():
     ("publish-early", "retreat", [], r"wrong [1-9]"),
     ("resume-skip", "retreat", [], r"wrong [1-9]"),
     ("resume-skip", "coop", [], r"wrong [1-9]"),
-    ("no-release", "retreat", ["--cap", 16], r"refused [1-9]"),
+    ("no-release", "retreat", ["--cap", 16], r"unreleased [1-9]"),
+    ("no-gate", "retreat", ["--cap", 2, "--retreat", 16, "--domains", 16, "--rq-wait-us", 500],
+     r"ring left [1-9]"),
     ("double-serve", "coop", [], r"urgent bad [1-9]"),
 ])
 def test_planted_mistakes_are_caught(bug, arm, extra, caught):
     rc, line, _ = run("--arm", arm, "--bug", bug, "--seed", 11, *extra)
     assert rc == 1, line
     assert line.startswith("FAIL") and re.search(caught, line), line
+
+
+@pytest.mark.parametrize("resume", ["full", "acc", "restart"])
+@pytest.mark.parametrize("cap", [2, 3])
+def test_retreat_ring_smaller_than_a_generation(resume, cap):
+    """16 retreats per generation into a ring of 2 or 3 entries: the ring
+    declines retreats once it holds `cap` unreleased tickets (the block keeps
+    its tile), and every task still completes exactly once with nothing lost,
+    stuck, unclaimed or unreleased."""
+    rc, line, f = run("--arm", "retreat", "--resume", resume, "--retreat", 16, "--domains", 16,
+                      "--cap", cap, "--seed", 4)
+    assert rc == 0, line
+    assert f["refused"] > 0 and f["miss"] == 0 and f["lost"] == 0 and f["ring left"] == 0, line
+    assert f["stuck"] == 0 and f["unreleased"] == 0, line
+    n = int(re.search(r"retreats (\d+)", line).group(1))
+    assert n > 0 and f"resumed {n}" in line, line
+
+
+@pytest.mark.parametrize("extra", [
+    # a full ring while tiles are long (12 ms stages): one refusal per job
+    ["--retreat", 4, "--domains", 4, "--work-ns", 12000000],
+    # more retreats per generation than domains hold blocks
+    ["--retreat", 6, "--domains", 2, "--work-ns", 8000000],
+])
+def test_retreat_full_ring_long_tiles(extra):
+    """Small jobs whose ring fills while every other block is deep in a long
+    tile: a declined retreat used to strand a later published ticket."""
+    rc, line, f = run("--arm", "retreat", "--resume", "full", "--blocks", 8, "--cap", 2,
+                      "--tiles-m", 4, "--tiles-n", 4, "--passes", 4, "--stages", 4,
+                      "--events", 4, "--mean-gap-us", 30000, "--seed", 1, *extra, job=False)
+    assert rc == 0, line
+    assert f["refused"] > 0 and f["miss"] == 0 and f["lost"] == 0 and f["ring left"] == 0, line
+
+
+def test_ring_of_one_entry_is_rejected():
+    """With one entry, "published by ticket t" and "free for ticket t + 1"
+    are the same sequence number: the simulator refuses it, as the C ABI does."""
+    rc, line, _ = run("--arm", "retreat", "--cap", 1)
+    assert rc == 2 and "bad configuration" in line, line
+
+
+@pytest.mark.parametrize("seed", [6, 7])
+def test_retreat_short_ring_waits(seed):
+    """The ring's deadlines cut to 2 ms (the kernels use 20 ms): with the
+    occupancy gate every wait ends on other blocks' progress, so nothing runs
+    out. Six blocks, so that the threads fit the host's cores and none is
+    descheduled for milliseconds in the middle of a publish (on the GPU a wave
+    is never descheduled; on an oversubscribed CPU a 2 ms deadline can expire
+    on the OS scheduler alone)."""
+    rc, line, f = run("--arm", "retreat", "--resume", "full", "--blocks", 6, "--retreat", 6,
+                      "--domains", 6, "--cap", 2, "--seed", seed, "--rq-wait-us", 2000)
+    assert rc == 0, line
+    assert f["refused"] > 0 and f["stuck"] == 0 and f["lost"] == 0, line
