@@ -55,16 +55,32 @@
 
 namespace {
 
+// The protocol orders its payload with fences around relaxed flag accesses
+// (as the kernels do). ThreadSanitizer cannot model standalone fences, so
+// its build (APK_SIM_TSAN) carries the same orderings on the accesses
+// themselves -- acquire loads and release stores, which order at least as
+// much -- and then reports any plain access to shared state (checkpoint
+// slots, results) that no protocol step orders.
+#ifdef APK_SIM_TSAN
+constexpr int kLoadOrder = __ATOMIC_ACQUIRE, kStoreOrder = __ATOMIC_RELEASE;
+#else
+constexpr int kLoadOrder = __ATOMIC_RELAXED, kStoreOrder = __ATOMIC_RELAXED;
+#endif
 struct HostPlat {
   static unsigned fetch_add(unsigned* p, unsigned v) {
     return __atomic_fetch_add(p, v, __ATOMIC_RELAXED);
   }
-  static unsigned load(const unsigned* p) { return __atomic_load_n(p, __ATOMIC_RELAXED); }
-  static int load(const int* p) { return __atomic_load_n(p, __ATOMIC_RELAXED); }
-  static void store(int* p, int v) { __atomic_store_n(p, v, __ATOMIC_RELAXED); }
+  static unsigned load(const unsigned* p) { return __atomic_load_n(p, kLoadOrder); }
+  static int load(const int* p) { return __atomic_load_n(p, kLoadOrder); }
+  static void store(int* p, int v) { __atomic_store_n(p, v, kStoreOrder); }
+#ifdef APK_SIM_TSAN
+  static void acquire() {}
+  static void publish_fence() {}
+#else
   static void acquire() { __atomic_thread_fence(__ATOMIC_ACQUIRE); }
   // host payload stores are plain: publishing them takes a release fence
   static void publish_fence() { __atomic_thread_fence(__ATOMIC_RELEASE); }
+#endif
   static int64_t ticks() {  // 100 MHz, as the device wall clock
     return std::chrono::duration_cast<std::chrono::nanoseconds>(
                std::chrono::steady_clock::now().time_since_epoch()).count() / 10;
@@ -141,6 +157,10 @@ struct Sim {
   std::vector<Ckpt> rqSlot;                  // cap
   std::atomic<long> retreats{0}, resumed{0}, refused{0}, stuck{0}, lost{0}, yields{0};
   std::atomic<int> running{0};
+  // The first grid starts together, as a kernel launch does: its blocks wait
+  // for `go`, set once every thread exists (thread creation under the
+  // sanitizers takes milliseconds, longer than a whole small job).
+  std::atomic<bool> go{false};
   std::atomic<int> fired{0};
 
   explicit Sim(const Config& cfg) : c(cfg) {
@@ -178,6 +198,7 @@ struct Sim {
   // One block: `cont` for a continuation launched after generation `epoch`.
   // The spawner counts the block in `running` before starting its thread.
   void block(int bid, bool cont, int epoch) {
+    while (!go.load(std::memory_order_acquire)) std::this_thread::yield();
     std::mt19937 rng(c.seed * 7919u + (unsigned)bid * 131u + (unsigned)epoch);
     const int home = bid & (APK_QUEUE_XCDS - 1);
     const int dom = bid % c.domains;
@@ -390,6 +411,7 @@ int main(int argc, char** argv) {
     threads.emplace_back(&Sim::block, &sim, bid, cont, epoch);
   };
   for (int b = 0; b < c.blocks; ++b) spawn(b, false, 0);
+  sim.go.store(true, std::memory_order_release);
 
   // Host: raise the generations at exponential gaps while blocks still run;
   // retreat arm: after each, the "urgent kernel" (a short wait) and the
