@@ -17,9 +17,9 @@ BIN_DIR = os.path.join(_HERE, "bin")
 HEADER = os.path.join(ROOT, "include", "apk.h")
 
 APK_OK, APK_EINVAL, APK_EHIP, APK_ERANGE = 0, 1, 2, 3
-ENGINE_VALU64, ENGINE_MFMA128, ENGINE_BF16X256, ENGINE_BF16X128, ENGINE_BF16X128K32 = range(5)
+ENGINE_VALU64, ENGINE_MFMA128, ENGINE_BF16X256, ENGINE_BF16X128, ENGINE_BF16X256X128 = range(5)
 ENGINES = {"valu64": ENGINE_VALU64, "mfma128": ENGINE_MFMA128, "bf16x256": ENGINE_BF16X256,
-           "bf16x128": ENGINE_BF16X128, "bf16x128k32": ENGINE_BF16X128K32}
+           "bf16x128": ENGINE_BF16X128, "bf16x256x128": ENGINE_BF16X256X128}
 
 
 class ApkError(RuntimeError):

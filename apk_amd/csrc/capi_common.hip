@@ -57,9 +57,9 @@ extern "C" int apk_engine_geometry_of(int engine, apk_engine_geometry* out) {
       *out = {apk::EngBf16x128::TM, apk::EngBf16x128::TN, apk::EngBf16x128::KS,
               apk::EngBf16x128::THREADS, apk::EngBf16x128::LDS_BYTES, 2, 1};
       return APK_OK;
-    case APK_ENGINE_BF16X128K32:
-      *out = {apk::EngBf16x128K32::TM, apk::EngBf16x128K32::TN, apk::EngBf16x128K32::KS,
-              apk::EngBf16x128K32::THREADS, apk::EngBf16x128K32::LDS_BYTES, 2, 1};
+    case APK_ENGINE_BF16X256X128:
+      *out = {apk::EngBf16x256x128::TM, apk::EngBf16x256x128::TN, apk::EngBf16x256x128::KS,
+              apk::EngBf16x256x128::THREADS, apk::EngBf16x256x128::LDS_BYTES, 2, 1};
       return APK_OK;
     default:
       apk::set_error("unknown engine %d", engine);

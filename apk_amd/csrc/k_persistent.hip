@@ -121,6 +121,8 @@ static int validate_persistent_gemm(const void* A, const void* B, float* C, int 
   APK_REQUIRE(kChunk > 0 && kChunk % E::KS == 0 && K % kChunk == 0,
               "persistent_gemm: k_chunk=%d must divide K=%d and be a multiple "
               "of %d", kChunk, K, E::KS);
+  APK_REQUIRE(K % KAlign<E>::value == 0, "persistent_gemm: K=%d must be a multiple of %d", K,
+              KAlign<E>::value);
   APK_REQUIRE((size_t)M * K * E::ELEM_BYTES < (1ull << 31) &&
                   (size_t)K * N * E::ELEM_BYTES < (1ull << 31) &&
                   (size_t)M * N < (1ull << 31),
@@ -231,8 +233,8 @@ extern "C" int apk_persistent_gemm(int engine, const void* A, const void* B,
       return launch_persistent_gemm<EngBf16x128>(A, B, C, M, N, K, k_chunk,
                                                  next_task, log, blocks,
                                                  as_stream(stream));
-    case APK_ENGINE_BF16X128K32:
-      return launch_persistent_gemm<EngBf16x128K32>(A, B, C, M, N, K, k_chunk,
+    case APK_ENGINE_BF16X256X128:
+      return launch_persistent_gemm<EngBf16x256x128>(A, B, C, M, N, K, k_chunk,
                                                     next_task, log, blocks,
                                                     as_stream(stream));
     default:
@@ -257,7 +259,7 @@ extern "C" int apk_persistent_gemm_occupancy(int engine, int* blocks_per_cu) {
     }
     case APK_ENGINE_BF16X256: return occupancy_of<EngBf16x256>(blocks_per_cu);
     case APK_ENGINE_BF16X128: return occupancy_of<EngBf16x128>(blocks_per_cu);
-    case APK_ENGINE_BF16X128K32: return occupancy_of<EngBf16x128K32>(blocks_per_cu);
+    case APK_ENGINE_BF16X256X128: return occupancy_of<EngBf16x256x128>(blocks_per_cu);
     default:
       set_error("occupancy: unknown engine %d", engine);
       return APK_EINVAL;
@@ -282,8 +284,8 @@ extern "C" int apk_persistent_gemm_noalloc(int engine, const void* A, const void
     case APK_ENGINE_BF16X128:
       rc = validate_persistent_gemm<EngBf16x128>(A, B, C, M, N, K, k_chunk, blocks);
       break;
-    case APK_ENGINE_BF16X128K32:
-      rc = validate_persistent_gemm<EngBf16x128K32>(A, B, C, M, N, K, k_chunk, blocks);
+    case APK_ENGINE_BF16X256X128:
+      rc = validate_persistent_gemm<EngBf16x256x128>(A, B, C, M, N, K, k_chunk, blocks);
       break;
     default:
       set_error("persistent_gemm_noalloc: unknown engine %d", engine);
@@ -315,8 +317,8 @@ extern "C" int apk_urgent_gemm(int engine, const void* A, const void* B, float* 
       return launch_urgent_tiles<EngBf16x256>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));
     case APK_ENGINE_BF16X128:
       return launch_urgent_tiles<EngBf16x128>(A, B, C, M, N, K, start_gt, end_gt, as_stream(stream));
-    case APK_ENGINE_BF16X128K32:
-      return launch_urgent_tiles<EngBf16x128K32>(A, B, C, M, N, K, start_gt, end_gt,
+    case APK_ENGINE_BF16X256X128:
+      return launch_urgent_tiles<EngBf16x256x128>(A, B, C, M, N, K, start_gt, end_gt,
                                                  as_stream(stream));
     default:
       set_error("urgent_gemm: unknown engine %d", engine);

@@ -777,6 +777,8 @@ static int validate(const apk_yield_params* p, int poll, int oracle, int blocks)
   APK_REQUIRE(p->k_chunk > 0 && p->k_chunk % E::KS == 0 && p->K % p->k_chunk == 0,
               "persistent_yield: k_chunk=%d must divide K=%d and be a multiple of %d",
               p->k_chunk, p->K, E::KS);
+  APK_REQUIRE(p->K % KAlign<E>::value == 0, "persistent_yield: K=%d must be a multiple of %d",
+              p->K, KAlign<E>::value);
   APK_REQUIRE((size_t)p->M * p->K * E::ELEM_BYTES < (1ull << 31) &&
                   (size_t)p->K * p->N * E::ELEM_BYTES < (1ull << 31),
               "persistent_yield: operands above 2 GiB are not supported");
@@ -820,9 +822,10 @@ static int validate(const apk_yield_params* p, int poll, int oracle, int blocks)
   }
   if (p->Au) {
     APK_REQUIRE(p->Bu && p->Cu && p->Mu > 0 && p->Nu > 0 && p->Ku > 0 &&
-                    p->Mu % E::TM == 0 && p->Nu % E::TN == 0 && p->Ku % E::KS == 0,
+                    p->Mu % E::TM == 0 && p->Nu % E::TN == 0 &&
+                    p->Ku % KAlign<E>::value == 0,
                 "persistent_yield: urgent job %dx%dx%d vs %dx%dx%d granularity", p->Mu,
-                p->Nu, p->Ku, E::TM, E::TN, E::KS);
+                p->Nu, p->Ku, E::TM, E::TN, KAlign<E>::value);
   }
   if (oracle)
     APK_REQUIRE(p->exec_count && (p->u_exec_count || !p->Au),
@@ -889,8 +892,8 @@ extern "C" int apk_persistent_yield(int engine, int poll, int oracle,
       return launch_e<EngBf16x256>(poll, oracle, params, blocks, as_stream(stream));
     case APK_ENGINE_BF16X128:
       return launch_e<EngBf16x128>(poll, oracle, params, blocks, as_stream(stream));
-    case APK_ENGINE_BF16X128K32:
-      return launch_e<EngBf16x128K32>(poll, oracle, params, blocks, as_stream(stream));
+    case APK_ENGINE_BF16X256X128:
+      return launch_e<EngBf16x256x128>(poll, oracle, params, blocks, as_stream(stream));
     default:
       set_error("persistent_yield: unknown engine %d", engine);
       return APK_EINVAL;
@@ -904,7 +907,7 @@ extern "C" long long apk_yield_ckpt_floats(int engine) {
     case APK_ENGINE_MFMA128: return Ckpt<EngMfma128>::SLOT_FLOATS;
     case APK_ENGINE_BF16X256: return Ckpt<EngBf16x256>::SLOT_FLOATS;
     case APK_ENGINE_BF16X128: return Ckpt<EngBf16x128>::SLOT_FLOATS;
-    case APK_ENGINE_BF16X128K32: return Ckpt<EngBf16x128K32>::SLOT_FLOATS;
+    case APK_ENGINE_BF16X256X128: return Ckpt<EngBf16x256x128>::SLOT_FLOATS;
     default: return -1;
   }
 }
@@ -946,8 +949,8 @@ extern "C" int apk_persistent_yield_occupancy(int engine, int poll, int* blocks_
     case APK_ENGINE_MFMA128: return yield_occupancy_of<EngMfma128>(poll, blocks_per_cu);
     case APK_ENGINE_BF16X256: return yield_occupancy_of<EngBf16x256>(poll, blocks_per_cu);
     case APK_ENGINE_BF16X128: return yield_occupancy_of<EngBf16x128>(poll, blocks_per_cu);
-    case APK_ENGINE_BF16X128K32:
-      return yield_occupancy_of<EngBf16x128K32>(poll, blocks_per_cu);
+    case APK_ENGINE_BF16X256X128:
+      return yield_occupancy_of<EngBf16x256x128>(poll, blocks_per_cu);
     default:
       set_error("occupancy: engine %d", engine);
       return APK_EINVAL;

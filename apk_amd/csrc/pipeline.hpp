@@ -3,6 +3,7 @@
 // bit-exact tile fingerprint, and checkpoint save/restore of accumulators and
 // LDS stages.
 #pragma once
+#include <type_traits>
 #include "device.hpp"
 
 #define APK_PROTO_FN __device__ __forceinline__
@@ -108,13 +109,39 @@ __device__ __forceinline__ void wait_landed() {
 }
 // Load i (< GROUP * LOADS) of the next group's stages: d0 for the first
 // stage, d1 for the second.
+// The multiple of K (and of an urgent GEMM's K) an engine's tiles need:
+// E::K_ALIGN where the engine states one (a load region spanning two
+// stages), else one stage.
+template <class E, class = void>
+struct KAlign {
+  static constexpr int value = E::KS;
+};
+template <class E>
+struct KAlign<E, std::void_t<decltype(E::K_ALIGN)>> {
+  static constexpr int value = E::K_ALIGN;
+};
+
+// An engine whose loads do not map one to one onto stages (a load region
+// spanning both stages of a group) supplies its own E::issue_group.
+template <class E, class = void>
+struct HasIssueGroup {
+  static constexpr bool value = false;
+};
+template <class E>
+struct HasIssueGroup<E, std::void_t<decltype(&E::issue_group)>> {
+  static constexpr bool value = true;
+};
 template <class E>
 __device__ __forceinline__ void issue_group_one(const typename E::Ctx& c,
                                                 const typename E::Lane& ln,
                                                 const typename E::Dst& d0,
                                                 const typename E::Dst& d1, int i) {
-  if (i < E::LOADS) E::issue_one(c, ln, d0, i);
-  else E::issue_one(c, ln, d1, i - E::LOADS);
+  if constexpr (HasIssueGroup<E>::value) {
+    E::issue_group(c, ln, d0, d1, i);
+  } else {
+    if (i < E::LOADS) E::issue_one(c, ln, d0, i);
+    else E::issue_one(c, ln, d1, i - E::LOADS);
+  }
 }
 
 // Non-preemptible K loop over stages [0, S) of one tile. hook(s) runs

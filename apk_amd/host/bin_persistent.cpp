@@ -6,10 +6,10 @@
 // results/raw/phase1_tiles.csv), same stdout lines and the same per-task CSV
 // schema "task,block,smid,start_cyc,end_cyc,dur_cyc,dur_us" (extra columns
 // tile,chunk appended). Additions:
-//   --engine valu64|mfma128|bf16x256|bf16x128|bf16x128k32
+//   --engine valu64|mfma128|bf16x256|bf16x128|bf16x256x128
 //                             tile engine (valu64 = the reference's 64x64
 //                             fmaf tile; mfma128 = 128x128 on fp32 MFMA;
-//                             bf16x256 / bf16x128(k32) = bf16 MFMA tiles on the
+//                             bf16x256 / bf16x128 / bf16x256x128 = bf16 MFMA tiles on the
 //                             reference's tcyield data, normal(0,1) rounded
 //                             to bf16, B passed transposed); --dtype
 //                             fp32|bf16 picks valu64 or bf16x256
@@ -54,9 +54,9 @@ int main(int argc, char** argv) {
   else if (engName == "mfma128") engine = APK_ENGINE_MFMA128;
   else if (engName == "bf16x256") engine = APK_ENGINE_BF16X256;
   else if (engName == "bf16x128") engine = APK_ENGINE_BF16X128;
-  else if (engName == "bf16x128k32") engine = APK_ENGINE_BF16X128K32;
+  else if (engName == "bf16x256x128") engine = APK_ENGINE_BF16X256X128;
   if (engine < 0) {
-    fprintf(stderr, "unknown --engine %s (valu64|mfma128|bf16x256|bf16x128|bf16x128k32)\n",
+    fprintf(stderr, "unknown --engine %s (valu64|mfma128|bf16x256|bf16x128|bf16x256x128)\n",
             engName.c_str());
     return 1;
   }

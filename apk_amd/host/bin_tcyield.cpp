@@ -12,9 +12,9 @@
 // The reference's 128x128 fp16 wmma tile becomes the BF16X256 engine:
 // 256x256 tiles of bf16 operands with fp32 accumulation on
 // v_mfma_f32_32x32x16_bf16 (B held transposed on the device); --engine
-// bf16x128 selects the 128x128 bf16 tile that runs at 2 and 4 blocks per CU
-// (--blocks 512 / 1024), bf16x128k32 the same tile with 32-deep k-stages (1 or
-// 2 blocks per CU, faster). Inputs are normal(0,1) rounded to bf16; the float64
+// bf16x128 selects the one-wave 128x128 bf16 tile built for 4 blocks per CU
+// (--blocks 1024), bf16x256x128 the four-wave 256x128 tile built for 2 blocks
+// per CU (--blocks 512). Inputs are normal(0,1) rounded to bf16; the float64
 // reference multiplies the bf16-quantized values (src/tcyield.cu:459-473).
 // --poll pe is the chunk (tile-boundary) poll, --poll issue the
 // window-forcing issue site (checkpoint before any wait). Every other flag and

@@ -19,7 +19,7 @@
 //  * the background is the preemptible kernel with polling off (tasks cycle
 //    the tile grid, src/urgent_baseline.cu:78-80), the urgent job is
 //    apk_persistent_gemm with --urgent-blocks workers over its own tiles.
-// Additions: --engine valu64|mfma128|bf16x256|bf16x128|bf16x128k32 (or --dtype fp32|bf16),
+// Additions: --engine valu64|mfma128|bf16x256|bf16x128|bf16x256x128 (or --dtype fp32|bf16),
 // --gemm-k K (background depth, walked
 // in --k chunks), --urgent-m/-n/-k (urgent GEMM shape; default
 // urgent-blocks tiles of depth --gemm-k, as the reference), --arrival
@@ -100,10 +100,10 @@ int main(int argc, char** argv) {
                      : engName == "valu64"   ? APK_ENGINE_VALU64
                      : engName == "bf16x256" ? APK_ENGINE_BF16X256
                      : engName == "bf16x128" ? APK_ENGINE_BF16X128
-                     : engName == "bf16x128k32" ? APK_ENGINE_BF16X128K32
+                     : engName == "bf16x256x128" ? APK_ENGINE_BF16X256X128
                                              : -1;
   if (engine < 0) {
-    fprintf(stderr, "unknown --engine %s (valu64|mfma128|bf16x256|bf16x128|bf16x128k32)\n",
+    fprintf(stderr, "unknown --engine %s (valu64|mfma128|bf16x256|bf16x128|bf16x256x128)\n",
             engName.c_str());
     return 1;
   }

@@ -53,7 +53,7 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
                      : engName == "valu64"   ? APK_ENGINE_VALU64
                      : engName == "bf16x256" ? APK_ENGINE_BF16X256
                      : engName == "bf16x128" ? APK_ENGINE_BF16X128
-                     : engName == "bf16x128k32" ? APK_ENGINE_BF16X128K32
+                     : engName == "bf16x256x128" ? APK_ENGINE_BF16X256X128
                                              : -1;
   const int naive = disc == "naive" ? 1 : 0;
   const int poison = disc == "poison" ? 1 : 0;

@@ -28,7 +28,7 @@
 // the next stages' loads go out, the flag is polled right behind them and a
 // yield checkpoints before any wait, so --discipline naive can save a stage
 // still in flight.
-// Additions: --engine valu64|mfma128|bf16x256|bf16x128|bf16x128k32 (default valu64;
+// Additions: --engine valu64|mfma128|bf16x256|bf16x128|bf16x256x128 (default valu64;
 // --dtype fp32|bf16 picks the default or bf16x256),
 // --dump-obs PATH (the OBS1 observation matrix), --gemm-k K (depth of
 // the background GEMM, default --k), --resume ckpt|acc|restart, --urgent-m/

@@ -38,13 +38,16 @@ enum {
  *             tile, src/tcyield.cu:91-356). Operands are bf16 (uint16 bit
  *             patterns): A is M x K row-major and B is passed TRANSPOSED, as
  *             Bt = N x K row-major (C = A . Bt^T); C is fp32 M x N.
- *  BF16X128 : 128x128 tile of the same bf16 GEMM (same operand layout),
- *             256 threads, 16-deep k-stages, 33 KiB of LDS: runs at 2 and
- *             4 blocks per CU, where the 256x256 tile cannot (configs[4] of
- *             the reference's study at 2 and 4 blocks/CU).
- *  BF16X128K32 : the same 128x128 bf16 tile with 32-deep k-stages (64 KiB
- *             of LDS): up to 2 blocks per CU, and faster than BF16X128 at
- *             1 and 2 blocks per CU; C is bit-identical to BF16X128's.
+ *  BF16X128 : 128x128 tile of the same bf16 GEMM (same operand layout) on
+ *             ONE wave (64 threads), 32 KiB of LDS: 4 blocks per CU, where
+ *             the 256x256 tile cannot run (configs[4] of the reference's
+ *             study at 4 blocks/CU). K must be a multiple of 32.
+ *  BF16X256X128 : 256x128 tile (256 rows of A, 128 of Bt) of the same bf16
+ *             GEMM on 256 threads, 48 KiB of LDS: 2 blocks per CU
+ *             (configs[4] at 2 blocks/CU). K must be a multiple of 32.
+ * Both take 16-deep k-stages in pairs (sites every 32 k), and every bf16
+ * engine forms each output's sum in the same k order: their C is
+ * bit-identical to each other's and to BF16X256's on the same operands.
  * For the fp32 engines A is M x K and B is K x N, row-major fp32.
  */
 enum {
@@ -52,7 +55,7 @@ enum {
   APK_ENGINE_MFMA128 = 1,
   APK_ENGINE_BF16X256 = 2,
   APK_ENGINE_BF16X128 = 3,
-  APK_ENGINE_BF16X128K32 = 4,
+  APK_ENGINE_BF16X256X128 = 4,
   APK_ENGINE_COUNT = 5
 };
 

@@ -71,7 +71,9 @@ def vm_waits_in_compute_blocks(asm_text, min_math=32):
     per pair of stages, when nothing else is in flight); when the whole stage
     is one basic block that wait is in it. Any other vmcnt wait in a compute
     block (after the barrier or after the math has started, or a second one)
-    stalls the prefetch on every stage.
+    stalls the prefetch on every stage. In a one-wave workgroup the compiler
+    drops s_barrier and leaves a "; wave barrier" marker in its place, which
+    counts as the barrier here.
     """
     out = []
     kernel, label, lines = None, None, []
@@ -83,7 +85,7 @@ def vm_waits_in_compute_blocks(asm_text, min_math=32):
             for l in lines:
                 if re.search(r'\bv_(mfma|fmac_f32|fma_f32)', l):
                     math_seen = True
-                if re.search(r'\bs_barrier\b', l) and pending and not math_seen:
+                if re.search(r'\bs_barrier\b|; wave barrier', l) and pending and not math_seen:
                     pending, accepted = None, True  # the stage wait
                 m = re.search(r's_waitcnt\b.*vmcnt\((\d+)\)', l)
                 if m:
@@ -105,7 +107,7 @@ def vm_waits_in_compute_blocks(asm_text, min_math=32):
             else:
                 label = mb.group(1)
             continue
-        if l.startswith('\t') and not l.lstrip().startswith(';'):
+        if l.startswith('\t') and (not l.lstrip().startswith(';') or 'wave barrier' in l):
             lines.append(l)
     flush()
     return out

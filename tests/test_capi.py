@@ -35,6 +35,13 @@ def test_engine_geometry():
     assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (256, 256, 32, 512)
     assert (g.elem_bytes, g.b_transposed) == (2, 1)
     assert g.lds_bytes <= 160 * 1024
+    # the small bf16 tiles: 4 (one wave each) and 2 blocks per CU fit LDS
+    g = apk_amd.geometry(apk_amd.ENGINE_BF16X128)
+    assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (128, 128, 16, 64)
+    assert (g.elem_bytes, g.b_transposed) == (2, 1) and 4 * g.lds_bytes <= 160 * 1024
+    g = apk_amd.geometry(apk_amd.ENGINE_BF16X256X128)
+    assert (g.tile_m, g.tile_n, g.k_stage, g.threads) == (256, 128, 16, 256)
+    assert (g.elem_bytes, g.b_transposed) == (2, 1) and 2 * g.lds_bytes <= 160 * 1024
     with pytest.raises(apk_amd.ApkError):
         apk_amd.geometry(99)
 
@@ -47,6 +54,10 @@ def test_engine_geometry():
     (apk_amd.ENGINE_VALU64, 0, 64, 64, 64, 1, "empty"),
     (apk_amd.ENGINE_BF16X256, 256, 128, 64, 64, 4, "multiples"),
     (apk_amd.ENGINE_BF16X256, 256, 256, 64, 48, 4, "k_chunk"),
+    # the small bf16 tiles load two 16-deep stages as one 32-deep region
+    (apk_amd.ENGINE_BF16X128, 128, 128, 48, 48, 4, "multiple of 32"),
+    (apk_amd.ENGINE_BF16X256X128, 256, 128, 80, 16, 4, "multiple of 32"),
+    (apk_amd.ENGINE_BF16X256X128, 128, 128, 64, 16, 4, "multiples"),
     (7, 64, 64, 64, 64, 1, "engine"),
 ])
 def test_persistent_gemm_rejects_bad_args(engine, M, N, K, kc, blocks, frag):

@@ -1,7 +1,8 @@
 """GPU parity of the bf16 MFMA engines (v_mfma_f32_32x32x16_bf16, fp32
 accumulation) through the C ABI: APK_ENGINE_BF16X256 (256x256 tile, 1 block
-per CU) and APK_ENGINE_BF16X128 (128x128 tile, run here at 2 and 4 blocks
-per CU, the occupancies at which the 256x256 tile cannot run).
+per CU), APK_ENGINE_BF16X128 (128x128 tile on one wave, 4 blocks per CU) and
+APK_ENGINE_BF16X256X128 (256x128 tile, 2 blocks per CU) -- the occupancies at
+which the 256x256 tile cannot run.
 
 What is pinned:
   * operand/accumulator lane layouts: small-integer bf16 inputs make every
@@ -11,7 +12,7 @@ What is pinned:
     src/tcyield.cu:459-473): rel-Frobenius <= 1e-2 against float64 on the
     bf16-quantized inputs (the bf16 bar), and in practice far below;
   * determinism: the k order is fixed, so C is bit-identical for every
-    k_chunk and worker count;
+    k_chunk and worker count, and across the three engines;
   * the yield path: stage and chunk polls with checkpoint/resume give C
     bit-identical to the unpreempted run, and the oracle counts are exact.
 B is passed transposed (Bt = N x K row-major): C = A . Bt^T.
@@ -24,11 +25,12 @@ from gpu_util import assert_queue_drained, dev, say
 
 pytestmark = pytest.mark.gpu
 
-ENGS = ["bf16x256", "bf16x128", "bf16x128k32"]
+ENGS = ["bf16x256", "bf16x128", "bf16x256x128"]
 
 
 def tile_of(apk, eng):
-    return apk.geometry(eng).tile_m
+    g = apk.geometry(eng)
+    return g.tile_m, g.tile_n
 
 
 def bits_of_small_ints(rng, shape, lo=-3, hi=3):
@@ -57,15 +59,15 @@ def run_bf16(torch, apk, A_bits, Bt_bits, k_chunk, blocks=None, eng=None):
 @pytest.mark.parametrize("name", ENGS)
 def test_bf16_layout_exact_small_integers(torch_gpu, apk, name):
     eng = apk.ENGINES[name]
-    T = tile_of(apk, eng)
-    M, N, K = 2 * T, T, 96
+    TM, TN = tile_of(apk, eng)
+    M, N, K = 2 * TM, TN, 96
     say(f"{name} layout: small integers, M={M} N={N} K={K}")
     rng = np.random.default_rng(5)
     A_bits, A = bits_of_small_ints(rng, (M, K))
     Bt_bits, Bt = bits_of_small_ints(rng, (N, K))
     C, nxt = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=K, blocks=3, eng=eng)
     ref = (A.astype(np.int64) @ Bt.astype(np.int64).T).astype(np.float32)
-    assert_queue_drained(nxt, (M // T) * (N // T), blocks=3)
+    assert_queue_drained(nxt, (M // TM) * (N // TN), blocks=3)
     assert np.array_equal(C, ref)
 
 
@@ -97,32 +99,32 @@ def test_bf16_bit_identical_across_chunks_and_workers(torch_gpu, apk, name):
         assert np.array_equal(C0.view(np.uint32), C1.view(np.uint32)), (kc, blocks)
 
 
-@pytest.mark.parametrize("K", [512, 160])
-def test_bf16x128_stage_depths_bit_identical(torch_gpu, apk, K):
-    """The 128x128 bf16 tile with 16-deep and with 32-deep k-stages forms
-    every output's sum in the same k order, so C is bit-identical; K = 160
-    is 10 stages of 16 but 5 of 32 (the last pair's second stage zeros)."""
-    say(f"bf16x128 vs bf16x128k32, M=N=256 K={K}")
-    A_bits, A, B_bits, B = oracle.fill_normal_bf16(13, 256, 256, K)
+@pytest.mark.parametrize("K", [512, 96])
+def test_bf16_engines_bit_identical(torch_gpu, apk, K):
+    """The three bf16 tiles form every output's sum in the same k order (k
+    steps of 16, ascending), so C is bit-identical across them; K = 96 is 3
+    stages of 32 for the 256x256 tile (its last pair's second stage zeros)
+    and 3 load regions of 32 for the other two."""
+    say(f"bf16x256 vs bf16x128 vs bf16x256x128, M=N=512 K={K}")
+    A_bits, A, B_bits, B = oracle.fill_normal_bf16(13, 512, 512, K)
     Bt_bits = np.ascontiguousarray(B_bits.T)
-    C16, _ = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=K, blocks=3,
-                      eng=apk.ENGINES["bf16x128"])
-    C32, _ = run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=K, blocks=3,
-                      eng=apk.ENGINES["bf16x128k32"])
-    assert np.array_equal(C16.view(np.uint32), C32.view(np.uint32))
-    assert oracle.rel_frobenius(C32, oracle.gemm_f64(A, B, threads=8)) <= 1e-5
+    C = {name: run_bf16(torch_gpu, apk, A_bits, Bt_bits, k_chunk=K, blocks=3,
+                        eng=apk.ENGINES[name])[0] for name in ENGS}
+    for name in ENGS[1:]:
+        assert np.array_equal(C[name].view(np.uint32), C["bf16x256"].view(np.uint32)), name
+    assert oracle.rel_frobenius(C["bf16x256"], oracle.gemm_f64(A, B, threads=8)) <= 1e-5
 
 
-def test_bf16x128_runs_at_4_blocks_per_cu(apk):
-    """The 128x128 tile's plain and yield kernels fit 4 blocks per CU (128
-    registers and 33 KiB of LDS per block) with 16-deep k-stages and 2 with
-    32-deep ones (64 KiB); the 256x256 tile fits one."""
+def test_bf16_small_tiles_run_at_2_and_4_blocks_per_cu(apk):
+    """The one-wave 128x128 tile's plain and yield kernels fit 4 blocks per CU
+    (32 KiB of LDS per block, one wave per SIMD), the 256x128 tile's 2 (48 KiB,
+    two waves per SIMD); the 256x256 tile fits one."""
     e128, e256 = apk.ENGINES["bf16x128"], apk.ENGINES["bf16x256"]
-    e128d = apk.ENGINES["bf16x128k32"]
-    assert apk.occupancy(e128) >= 4 and apk.occupancy(e128d) >= 2
+    e256x128 = apk.ENGINES["bf16x256x128"]
+    assert apk.occupancy(e128) >= 4 and apk.occupancy(e256x128) >= 2
     for poll in (apk.POLL_OFF, apk.POLL_CHUNK, apk.POLL_STAGE, apk.POLL_ISSUE):
         assert apk.yield_occupancy(e128, poll) >= 4, poll
-        assert apk.yield_occupancy(e128d, poll) >= 2, poll
+        assert apk.yield_occupancy(e256x128, poll) >= 2, poll
     assert apk.occupancy(e256) == 1
 
 
@@ -134,11 +136,11 @@ class Bf16Job:
         T = torch
         self.t, self.apk = torch, apk
         self.eng = apk.ENGINE_BF16X256 if eng is None else eng
-        self.tile = tile_of(apk, self.eng)
+        self.tm, self.tn = tile_of(apk, self.eng)
         self.M, self.N, self.K, self.kc = M, N, K, kc
         self.Mu, self.Nu, self.Ku = Mu, Nu, Ku
-        self.tiles = (M // self.tile) * (N // self.tile)
-        self.U = (Mu // self.tile) * (Nu // self.tile)
+        self.tiles = (M // self.tm) * (N // self.tn)
+        self.U = (Mu // self.tm) * (Nu // self.tn)
         self.num_tasks = self.tiles * passes
         self.events, self.blocks = events, blocks
         A_bits, self.A, B_bits, self.B = oracle.fill_normal_bf16(seed, M, N, K)
@@ -208,8 +210,8 @@ class Bf16Job:
 
 
 # (engine, blocks per CU or a block count): the 256x256 tile on 64 workers,
-# the 128x128 tile at 2 and 4 blocks on every CU.
-JOBS = [("bf16x256", 64), ("bf16x128", "2/CU"), ("bf16x128", "4/CU"), ("bf16x128k32", "2/CU")]
+# the 128x128 tile at 4 (and 2) blocks on every CU, the 256x128 tile at 2.
+JOBS = [("bf16x256", 64), ("bf16x128", "2/CU"), ("bf16x128", "4/CU"), ("bf16x256x128", "2/CU")]
 
 
 @pytest.fixture(scope="module", params=JOBS, ids=lambda j: f"{j[0]}-{j[1]}".replace("/", "per"))
@@ -219,10 +221,10 @@ def bf16_job(torch_gpu, apk, request):
     blocks = b if isinstance(b, int) else apk.device_info().cu_count * int(b.split("/")[0])
     for poll in (apk.POLL_CHUNK, apk.POLL_STAGE):  # every worker resident
         assert apk.yield_occupancy(eng, poll) * apk.device_info().cu_count >= blocks
-    T = tile_of(apk, eng)
+    TM, TN = tile_of(apk, eng)
     # 9 tasks per block: the job outlasts the 24 events the setter (block 0)
     # raises 3 us apart at its own poll sites.
-    tiles = (512 // T) ** 2
+    tiles = (512 // TM) * (512 // TN)
     passes = -(-9 * blocks // tiles)
     say(f"building {name} yield job M=N=512 K=1024 kc=64 on {blocks} blocks ({passes} passes), "
         "urgent 256x512x256")
@@ -241,9 +243,8 @@ def test_bf16_yield_bit_identical(bf16_job, apk, poll, resume):
     assert fired == j.events and yields >= fired
     assert np.array_equal(r["C"].view(np.uint32), ref["C"].view(np.uint32))
     # every task's fingerprint equals its tile's fingerprint in the unpreempted C
-    T = j.tile
-    tn = j.N // T
-    th = np.array([oracle.tile_hash(ref["C"], (t // tn) * T, (t % tn) * T, T, T)
+    tn = j.N // j.tn
+    th = np.array([oracle.tile_hash(ref["C"], (t // tn) * j.tm, (t % tn) * j.tn, j.tm, j.tn)
                    for t in range(j.tiles)], dtype=np.uint64)
     assert np.array_equal(r["task_hash"], th[np.arange(j.num_tasks) % j.tiles])
     # every claimed event's urgent output equals the non-preemptible urgent GEMM
@@ -272,25 +273,30 @@ def test_bf16_float64_and_oracle(bf16_job, apk):
 
 @pytest.fixture(scope="module", params=ENGS)
 def bf16_odd_job(torch_gpu, apk, request):
-    # 5 k-stages (K = 160 for the 32-deep stages of the 256x256 tile, 80 for
-    # the 16-deep stages of the 128x128 tile): the stage loop takes them in
-    # pairs (0,1), (2,3), (4, a stage of zeros); the urgent job's 3 stages end
-    # the same way.
+    # An odd number of pairs. The 256x256 tile: 5 k-stages of 32 (K = 160),
+    # taken in pairs (0,1), (2,3), (4, a stage of zeros), the urgent job's 3
+    # stages ending the same way. The 128x128 and 256x128 tiles load a pair
+    # of 16-deep stages as one region, so their tiles hold whole pairs: 5
+    # pairs (K = 160, sites 0, 2, ..., 8), the urgent job 3 (K = 96).
     eng = apk.ENGINES[request.param]
     ks = apk.geometry(eng).k_stage
-    T = tile_of(apk, eng)
-    passes = 1536 // (512 // T) ** 2  # 24 tasks per block
-    say(f"building {request.param} odd-length yield job M=N=512 K={5 * ks} kc={ks}, urgent "
-        f"256x256x{3 * ks}")
-    return Bf16Job(torch_gpu, apk, 512, 512, 5 * ks, ks, 256, 256, 3 * ks, events=24, blocks=64,
+    K, Ku = (5 * ks, 3 * ks) if ks == 32 else (160, 96)
+    TM, TN = tile_of(apk, eng)
+    # 48 tasks per block: the job outlasts the 24 events the setter raises
+    # 3 us apart (the one-wave tile finishes 24 short tiles in about 70 us)
+    passes = 3072 // ((512 // TM) * (512 // TN))
+    say(f"building {request.param} odd-length yield job M=N=512 K={K} kc={K // 5}, urgent "
+        f"256x256x{Ku}")
+    return Bf16Job(torch_gpu, apk, 512, 512, K, K // 5, 256, 256, Ku, events=24, blocks=64,
                    passes=passes, eng=eng)
 
 
 @pytest.mark.parametrize("resume", [0, 1, 2])
 def test_bf16_odd_length_pairs_yield(bf16_odd_job, apk, resume):
-    """Yields at every site of odd-length tiles, incl. the last pair whose second
-    stage is all zeros (checkpointed and restored with the pair): C bit-identical
-    to the unpreempted run, within tolerance of float64, urgent outputs equal the
+    """Yields at every site of tiles with an odd number of pairs, incl. the
+    last pair (for the 256x256 tile the one whose second stage is all zeros,
+    checkpointed and restored with the pair): C bit-identical to the
+    unpreempted run, within tolerance of float64, urgent outputs equal the
     non-preemptible urgent GEMM, every task and event counted once."""
     j = bf16_odd_job
     say(f"engine {j.eng} odd-length pairs, stage yields, resume={resume}")
@@ -301,9 +307,11 @@ def test_bf16_odd_length_pairs_yield(bf16_odd_job, apk, resume):
     # The setter (block 0) raises each event at its first poll site past the
     # event's time, so the site an event lands on depends on how long the
     # setter spends before each site; with the short 16-deep stages of the
-    # 128x128 tile, a job of 24 events can land none at site 4. Jobs are
-    # repeated, each checked in full, until an event has.
-    sites = np.zeros(5, dtype=np.int64)
+    # small tiles, a job of 24 events can land none at the last site. Jobs
+    # are repeated, each checked in full, until an event has.
+    S = j.K // apk.geometry(j.eng).k_stage
+    last = (S - 1) // 2 * 2
+    sites = np.zeros(S, dtype=np.int64)
     for attempt in range(16):
         r = j.run(apk.POLL_STAGE, resume=resume, use_oracle=True)
         fired = int((r["set_gt"] != 0).sum())
@@ -313,11 +321,11 @@ def test_bf16_odd_length_pairs_yield(bf16_odd_job, apk, resume):
         for e in range(j.events):
             assert np.array_equal(r["Cu"][e].view(np.uint32), uref.view(np.uint32)), e
         assert (r["exec"] == 1).all() and (r["u_exec"] == j.U).all()
-        # sites are the pair boundaries 0, 2, 4; site 4 is the pair with the zero stage
-        assert set(np.unique(r["site"]).tolist()) <= {0, 2, 4}
-        sites += np.bincount(r["site"], minlength=5)
-        if sites[4] > 0:
+        # sites are the pair boundaries 0, 2, ..., last
+        assert set(np.unique(r["site"]).tolist()) <= set(range(0, last + 1, 2))
+        sites += np.bincount(r["site"], minlength=S)
+        if sites[last] > 0:
             break
-    assert sites[4] > 0
+    assert sites[last] > 0
     say(f"  {attempt + 1} job(s), {j.events} events each, at sites {sites.tolist()}, "
         "bit-identical, float64 within 1e-5")

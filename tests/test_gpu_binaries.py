@@ -111,9 +111,9 @@ def test_persistent_prints_engine_clock(tmp_path):
                                             (("--dtype", "bf16"), 4, 1),
                                             (("--engine", "bf16x128"), 8, 2),
                                             (("--engine", "bf16x128"), 8, 4),
-                                            (("--engine", "bf16x128k32"), 8, 2)])
+                                            (("--engine", "bf16x256x128"), 8, 2)])
 def test_persistent_bf16_engines(tmp_path, sel, tiles, bpc):
-    """persistent --engine bf16x256|bf16x128 (--dtype bf16 = bf16x256): the
+    """persistent --engine bf16x256|bf16x128|bf16x256x128 (--dtype bf16 = bf16x256): the
     bf16 tiles on the reference's tcyield data (normal(0,1) rounded to bf16),
     float64 check passes, one record per (tile, chunk) in the reference's CSV
     schema."""

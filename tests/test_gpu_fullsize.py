@@ -114,13 +114,16 @@ CFG5_128 = ["--tiles-m", 64, "--tiles-n", 64, "--gemm-k", 8192, "--k", 256, "--u
             "--urgent-n", 256, "--urgent-k", 256, "--verify-rows", 32]
 
 
-@pytest.mark.parametrize("engine,blocks", [("bf16x128", 512), ("bf16x128", 1024),
-                                           ("bf16x128k32", 512)])
-def test_cfg5_bf16x128_yields_multi_block(engine, blocks):
-    """cfg5 at 2 and 4 blocks per CU (the 256x256 tile cannot hold them):
-    128x128 bf16 tiles, k-stage yields with checkpoint/resume."""
-    out = run_bin("tcyield", *CFG5_128, "--engine", engine, "--blocks", blocks, "--mode",
-                  "events", "--poll", "stage", "--events", 1500, "--oracle", 1)
+@pytest.mark.parametrize("engine,blocks", [("bf16x128", 1024), ("bf16x256x128", 512),
+                                           ("bf16x128", 512)])
+def test_cfg5_bf16_small_tiles_yields_multi_block(engine, blocks):
+    """cfg5 at 4 and 2 blocks per CU (the 256x256 tile cannot hold them): the
+    one-wave 128x128 tile at 4 (and 2), the 256x128 tile at 2; k-stage yields
+    with checkpoint/resume."""
+    tiles_m = ["--tiles-m", 32] if engine == "bf16x256x128" else []
+    # flags are read first match first: the tile rows go ahead of CFG5_128's
+    out = run_bin("tcyield", *tiles_m, *CFG5_128, "--engine", engine, "--blocks", blocks,
+                  "--mode", "events", "--poll", "stage", "--events", 1500, "--oracle", 1)
     yields, = grab(out, r"yields: (\d+)")
     assert yields >= 1000
     assert_identical(out)

@@ -43,11 +43,11 @@ def test_urgent_fp32_matches_persistent(torch_gpu, apk, name):
     assert 0 < start <= end
 
 
-@pytest.mark.parametrize("name", ["bf16x256", "bf16x128", "bf16x128k32"])
+@pytest.mark.parametrize("name", ["bf16x256", "bf16x128", "bf16x256x128"])
 def test_urgent_bf16_matches_persistent(torch_gpu, apk, name):
     eng = apk.ENGINES[name]
-    T = apk.geometry(eng).tile_m
-    M, N, K = 2 * T, T, 512
+    g = apk.geometry(eng)
+    M, N, K = 2 * g.tile_m, g.tile_n, 512
     say(f"urgent_gemm {name} {M}x{N}x{K} vs persistent_gemm")
     A_bits, A, B_bits, B = oracle.fill_normal_bf16(9, M, N, K)
     Bt = np.ascontiguousarray(B_bits.T)

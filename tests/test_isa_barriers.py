@@ -74,3 +74,9 @@ def test_vm_wait_checker_catches_the_pattern():
     assert vm_waits_in_compute_blocks("\n".join(pair)) == []
     twice = ["_Z1kv:", ".LBB0_1:", "\ts_waitcnt vmcnt(4)", "\ts_waitcnt vmcnt(0)", "\ts_barrier"] + body
     assert vm_waits_in_compute_blocks("\n".join(twice)) == [("_Z1kv", ".LBB0_1", "s_waitcnt vmcnt(0)")]
+    # one-wave workgroups: the compiler's "; wave barrier" marker stands for
+    # the dropped s_barrier
+    wave = ["_Z1kv:", ".LBB0_1:", "\ts_waitcnt vmcnt(0)", "\t; wave barrier"] + body
+    assert vm_waits_in_compute_blocks("\n".join(wave)) == []
+    wave_late = wave + ["\ts_waitcnt vmcnt(0)"]
+    assert vm_waits_in_compute_blocks("\n".join(wave_late)) == [("_Z1kv", ".LBB0_1", "s_waitcnt vmcnt(0)")]
