@@ -2,8 +2,7 @@
 #include <stdarg.h>
 #include <string.h>
 #include "capi.hpp"
-#include "engine_bf16x128.hpp"
-#include "engine_bf16x256.hpp"
+#include "engine_bf16.hpp"
 #include "engine_mfma128.hpp"
 #include "engine_valu64.hpp"
 

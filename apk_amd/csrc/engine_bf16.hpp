@@ -1,46 +1,73 @@
-// engine_bf16x128.hpp -- the bf16 tiles for 2 and 4 blocks per CU: output
-// tiles of a bf16 GEMM with fp32 accumulation on the gfx950 matrix cores
-// (v_mfma_f32_32x32x16_bf16), sized for the occupancy points at which the
-// 256x256 tile cannot run (its fp32 accumulator is half of a CU's register
-// file and its ring 128 KiB of the 160 KiB LDS):
-//  EngBf16x128     (engine bf16x128, 4 blocks per CU): a 128x128 tile on ONE
-//                  wave. The wave owns all 4x4 32x32 accumulators (256 fp32
-//                  per lane, in AGPRs) and reads 8 operand fragments per 16
-//                  MFMAs; with one wave per block every block barrier folds
-//                  away (the compiler drops s_barrier for a one-wave
-//                  workgroup), so a block never waits for another wave.
-//  EngBf16x256x128 (engine bf16x256x128, 2 blocks per CU): a 256x128 tile on
-//                  4 waves (2x2, each 128x64: 128 fp32 per lane), two waves
-//                  per SIMD at 2 blocks per CU. Against 128x128 it loads 25%
-//                  fewer operand bytes per FLOP (85 instead of 64 FLOP per
+// engine_bf16.hpp -- the bf16 GEMM tiles: output tiles of C = A . Bt^T with
+// bf16 operands and fp32 accumulation on the gfx950 matrix cores
+// (v_mfma_f32_32x32x16_bf16), fed by a 4-slot LDS ring of
+// buffer_load_dwordx4 ... lds (direct-to-LDS) that is synchronised once per
+// pair of k-stages. One template, three tiles:
+//  EngBf16x256     (engine bf16x256, 1 block per CU): 256x256 on 8 waves
+//                  (2x4, each 128x64: 128 fp32 per lane), two waves per SIMD;
+//                  a 256 KiB fp32 accumulator is half of a CU's register
+//                  file, so no second block fits. A wave takes at most 239
+//                  of its SIMD's 256 registers per lane, so a small kernel
+//                  launched on another stream while the grid runs (the
+//                  retreat arm's flag raise, the clock probes) still finds
+//                  registers on every SIMD. (The same tile on 4 waves of
+//                  128x128 measured 1,382 against 1,286 TFLOP/s at cfg5, but
+//                  its polled kernels take all 512 registers of each SIMD:
+//                  the flag-raise kernel then waits for the job to end.)
+//  EngBf16x128     (engine bf16x128, 4 blocks per CU): 128x128 on ONE wave
+//                  (all 4x4 32x32 accumulators, 256 fp32 per lane, in AGPRs;
+//                  8 operand reads per 16 MFMAs). With one wave per block
+//                  every block barrier folds away (the compiler drops
+//                  s_barrier for a one-wave workgroup). At 4 blocks per CU
+//                  its polled kernels fill every SIMD's registers, so it
+//                  serves the cooperative arm (device-raised generations);
+//                  the retreat arm needs a grid that leaves room in every
+//                  dispatch domain.
+//  EngBf16x256x128 (engine bf16x256x128, 2 blocks per CU): 256x128 on 4 waves
+//                  (2x2, each 128x64), two waves per SIMD; 25% fewer operand
+//                  bytes per FLOP than 128x128 (85 instead of 64 FLOP per
 //                  byte of A and Bt).
 //
-// Operands as for the 256x256 engine: A is M x K row-major bf16, B is passed
-// transposed (Bt = N x K row-major bf16, C = A . Bt^T), both k-contiguous in
-// memory, LDS and operand registers. C is M x N row-major fp32.
+// Operands: A is M x K row-major bf16; B is passed transposed, Bt = N x K
+// row-major bf16, so that both operands are k-contiguous in memory, in LDS
+// and in the MFMA operand registers (8 consecutive k per lane = one 16-byte
+// LDS read). C is M x N row-major fp32.
 //
-// Stages and loads. The stage loops see 16-deep k-stages in a 4-slot ring
-// taken in pairs (GROUP = 2, one barrier per pair; polls and checkpoints at
-// pair boundaries). Memory sees 32-deep load regions: a pair of stages is
-// loaded as ONE region of 64-byte rows (32 k of every A row of the tile,
-// then of every Bt row), so each row costs one full 64-byte request -- with
-// 32-byte rows per stage (one 16-deep stage loaded alone) every request was
-// half used, and the L1 hit rate of the 4-block configuration fell to 10%.
-// Ring slots 2h and 2h+1 are the two halves of region h (the A half and the
-// Bt half); a checkpoint always saves and restores them together (a pair
-// site's live stages are the pair). Tiles need an even number of stages:
-// K a multiple of 32 (K_ALIGN).
+// Stages, pairs and load regions. The stage loops see KS-deep k-stages in a
+// 4-slot ring taken in pairs (GROUP = 2): one barrier per pair, the next
+// pair's loads issued under the current pair's MFMAs, polls and checkpoints
+// at pair boundaries. Memory sees load REGIONS: a pair's two stages are
+// loaded as one region of 2 KS k -- all TM rows of A, then all TN rows of Bt,
+// each row 4 KS bytes -- by one set of loads. Loading each stage alone gives
+// rows half as long: the small tiles' 16-deep stages used half of each
+// 64-byte request (the 4-block configuration's L1 hit rate fell to 10% and
+// its L2 requests doubled), and the 256x256 tile's 32-deep stages half of
+// each 128-byte line. Ring slots 2h and 2h+1 are the two halves of region h
+// (A half, Bt half); a checkpoint always saves and restores them together (a
+// pair site's live stages are the pair), and tiles need an even number of
+// stages (K_ALIGN = 2 KS).
 //
-// LDS layout (both operands): row r of a region is four 16-byte chunks;
-// chunk q is stored at slot q ^ swz(r), swz(r) = (r >> 2) & 3 (the 256x256
-// engine's layout, measured conflict-free for these operand reads).
+// LDS layout (both operands): row r of a region is CHUNKS 16-byte chunks;
+// chunk q is stored at slot q ^ swz(r). 64-byte rows: swz(r) = (r >> 2) & 3.
+// A 32-row operand read (lanes 0-31 chunk 2j, lanes 32-63 chunk 2j+1) then
+// takes the minimum 4 LDS cycles per ds_read_b128 on gfx950: measured with
+// SQ_LDS_BANK_CONFLICT on a probe of this exact access pattern, where
+// ((r >> 1) ^ (r >> 3)) & 3 and (r >> 1) & 3 cost 8 cycles (2-way) and r & 3
+// costs 16; (r >> 2) & 3, (r >> 3) & 3, (r ^ (r >> 2)) & 3 and
+// ((r >> 1) ^ (r >> 2)) & 3 are conflict-free. 128-byte rows: swz(r) =
+// (r >> 1) & 7, so that 16 consecutive rows reading one chunk fall on 16
+// different 16-byte bank groups of the 256-byte bank line (even and odd rows
+// on its two halves, eight distinct slots each).
 //
-// k order: the MFMA k-steps of 16 in ascending k; every output's sum is
-// formed in the same order whatever worker computes it and however often it
-// is checkpointed and resumed.
+// k order: k-steps of 16 in ascending k; every output's sum is formed in the
+// same order whatever tile, worker, stage depth or region depth computes it,
+// and however often it is checkpointed and resumed: the three tiles give
+// bit-identical C.
 //
 // Epilogue: the fp32 tile is staged through LDS one accumulator row block of
-// every wave per pass (32 rows per wave row), row stride TN + 4 floats.
+// every wave per pass (32 rows per wave row), row stride TN + 4 floats (the
+// two half-waves write rows 4 apart, which then fall on different banks),
+// then moved to C with 16-byte coalesced stores (and fingerprinted).
 #pragma once
 #include "device.hpp"
 
@@ -48,14 +75,16 @@ namespace apk {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-template <int TM_, int THREADS_, int BPC_>
-struct EngBf16SmallT {
+template <int TM_, int TN_, int THREADS_, int BPC_, int KS_>
+struct EngBf16T {
   static_assert(TM_ == 128 || TM_ == 256, "128 or 256 tile rows");
-  static_assert(THREADS_ == 64 || THREADS_ == 256, "1 or 4 waves");
-  static constexpr int TM = TM_, TN = 128, KS = 16, NS = 4, GROUP = 2, THREADS = THREADS_;
+  static_assert(TN_ == 128 || TN_ == 256, "128 or 256 tile columns");
+  static_assert(THREADS_ == 64 || THREADS_ == 256 || THREADS_ == 512, "1, 4 or 8 waves");
+  static_assert(KS_ == 16 || KS_ == 32, "16- or 32-deep k-stages");
+  static constexpr int TM = TM_, TN = TN_, KS = KS_, NS = 4, GROUP = 2, THREADS = THREADS_;
   static constexpr int WAVES = THREADS / 64;
-  // Waves WM x WN over the tile; wave (wm, wn) owns a WTM x WTN sub-tile of
-  // RB x CB 32x32 accumulators.
+  // Waves WM x WN over the tile; wave (wm, wn) = (w % WM, w / WM) owns a
+  // WTM x WTN sub-tile of RB x CB 32x32 accumulators.
   static constexpr int WM = WAVES == 1 ? 1 : 2, WN = WAVES / WM;
   static constexpr int WTM = TM / WM, WTN = TN / WN, RB = WTM / 32, CB = WTN / 32;
   static constexpr int MFMAS = RB * CB;                     // per k-step per wave
@@ -66,11 +95,12 @@ struct EngBf16SmallT {
   static constexpr int WAVES_PER_SIMD = (BLOCKS_PER_CU * WAVES + 3) / 4;
   static constexpr int MIN_WAVES_PER_SIMD = WAVES_PER_SIMD;
   static constexpr int ELEM_BYTES = 2;                      // bf16 operands
-  static constexpr int K_ALIGN = 32;                        // an even number of stages
-  static constexpr int ROW_BYTES = 64, CHUNKS = 4;          // region rows: 32 k
-  static constexpr int A_REGION = TM * ROW_BYTES;           // 8 / 16 KiB
-  static constexpr int REGION = A_REGION + TN * ROW_BYTES;  // 16 / 24 KiB
-  static constexpr int STAGE = REGION / 2;                  // a ring slot: half a region
+  static constexpr int RK = 2 * KS;                         // k per load region
+  static constexpr int K_ALIGN = RK;
+  static constexpr int ROW_BYTES = RK * 2, CHUNKS = ROW_BYTES / 16;
+  static constexpr int A_REGION = TM * ROW_BYTES;
+  static constexpr int REGION = A_REGION + TN * ROW_BYTES;
+  static constexpr int STAGE = REGION / 2;                  // a ring slot
   // offset of the Bt rows in a region (the test hook that corrupts an
   // urgent tile's staged B adds to the float there)
   static constexpr int A_STAGE = A_REGION;
@@ -78,9 +108,16 @@ struct EngBf16SmallT {
   static constexpr int RLOADS_A = A_REGION / (THREADS * 16);
   static constexpr int LOADS = RLOADS / 2;                  // per stage
   static constexpr int ROWS_PER_WAVE = 64 / CHUNKS;         // rows of one wave's load
+  static_assert(RLOADS_A * THREADS * 16 == A_REGION && RLOADS * THREADS * 16 == REGION,
+                "whole loads per operand");
+  static_assert(RLOADS % 2 == 0, "a pair's loads split evenly over its stages");
+  // Load i of a wave covers rows (WAVES * i + wave) * ROWS_PER_WAVE + ...; the
+  // swizzle must not see the WAVES * ROWS_PER_WAVE step (one offset register
+  // per load, formed once per tile).
+  static_assert((WAVES * ROWS_PER_WAVE) % 16 == 0, "loads keep the swizzle");
   // Epilogue: one accumulator row block of every wave per pass.
   static constexpr int STORE_PASSES = RB, PASS_ROWS = 32 * WM, STAGE_LD = TN + 4;
-  static constexpr int RING_BYTES = NS * STAGE;             // 32 / 48 KiB
+  static constexpr int RING_BYTES = NS * STAGE;
   static constexpr int EPI_BYTES = PASS_ROWS * STAGE_LD * 4;
   static constexpr int LDS_BYTES = RING_BYTES > EPI_BYTES ? RING_BYTES : EPI_BYTES;
 
@@ -111,15 +148,16 @@ struct EngBf16SmallT {
         for (int r = 0; r < 16; ++r) a.c[i][j][r] = 0.0f;
   }
 
-  static __device__ __forceinline__ int swz(int r) { return (r >> 2) & 3; }
+  static __device__ __forceinline__ int swz(int r) {
+    return CHUNKS == 4 ? (r >> 2) & 3 : (r >> 1) & 7;
+  }
 
   // Direct-to-LDS loads of one region: load i fills rows
   // ROWS_PER_WAVE * (WAVES * i + wave) + lane / CHUNKS of the A rows (i <
   // RLOADS_A) or of the Bt rows; lane l writes slot l % CHUNKS of its row, so
-  // it reads the row's chunk (l % CHUNKS) ^ swz(row) from memory. The
-  // swizzle uses only row bits that i does not change, so each lane's offset
-  // of load i is fixed per tile (one register per load); a region only adds
-  // the scalar k offset.
+  // it reads the row's chunk (l % CHUNKS) ^ swz(row) from memory. Each lane's
+  // offset of load i is fixed per tile (one register per load); a region only
+  // adds the scalar k offset.
   struct Lane {
     uint32_t a[RLOADS_A], b[RLOADS - RLOADS_A];
   };
@@ -138,12 +176,13 @@ struct EngBf16SmallT {
       ln.b[i] = b0 + (uint32_t)(i * WAVES * ROWS_PER_WAVE) * (uint32_t)c.K * 2u;
     return ln;
   }
-  // Scalar parts of the loads of stage t into ring slot `slot`: this wave's
-  // piece of the slot's region (LDS), the byte offset of the region along a
-  // row, and the operand resources. Only the first stage of a pair (t even)
-  // carries the region's loads; k = NO_LOADS marks the second. A region past
-  // the tile's end (t >= S) is read through resources of zero length: every
-  // lane reads zeros and no memory is touched.
+  // The scalar parts of the loads of stage t into ring slot `slot`, formed
+  // once per stage: this wave's 1 KiB piece of the slot's region (LDS), the
+  // byte offset of the region along a row, and the operand resources. Only
+  // the first stage of a pair (t even) carries the region's loads; k =
+  // NO_LOADS marks the second. A region past the tile's end (t >= S) is read
+  // through resources of zero length: every lane reads zeros and no memory
+  // is touched (the refetch that stands in for the pair after a tile's last).
   struct Dst {
     uint32_t lds, k;
     i32x4 ra, rb;
@@ -217,28 +256,33 @@ struct EngBf16SmallT {
     }
   }
 
-  // MFMAs of a pair per load of the next pair issued among them (the loads
-  // go out over the first GROUP * LOADS * IV MFMAs).
-  static constexpr int IV = 2 * MFMAS / (GROUP * LOADS);
-  static_assert(IV >= 1 && IV * GROUP * LOADS <= 2 * MFMAS, "loads spread over the MFMAs");
+  static constexpr int JG = RK / 16;  // MFMA k-steps per pair (one region)
+  // The next pair's loads go out one per IV MFMAs from the pair's start (at
+  // most one per two: issued densely at the front of the pair they have the
+  // rest of it to land).
+  static constexpr int IV_FIT = JG * MFMAS / (GROUP * LOADS);
+  static constexpr int IV = IV_FIT < 2 ? IV_FIT : 2;
+  static_assert(IV >= 1, "loads spread over the MFMAs");
 
-  // One pair: the region in ring slots slot and slot+1, its two k-steps of
-  // MFMAS MFMAs per wave in ascending k, the operands of the second read
-  // while the first's MFMAs run. `pre` runs first (false abandons the pair
-  // before any accumulator changes); `mid(i)`, i = 0..GROUP*LOADS-1, runs
-  // after MFMA (i+1)*IV-1 of the pair: the stage loops issue the next pair's
-  // load i there.
+  // One pair: the region in ring slots slot and slot+1, MFMAS MFMAs per
+  // k-step per wave in ascending k, the operands of k-step j+1 read while
+  // k-step j's MFMAs run. `pre` runs first (returning false abandons the pair
+  // before any accumulator changes); it runs before any operand is in
+  // registers, so a yield inside it (checkpoint, urgent tiles, restore) needs
+  // only the accumulators live. `mid(i)`, i = 0..GROUP*LOADS-1, runs after
+  // MFMA (i+1)*IV-1 of the pair: the stage loops issue the next pair's load i
+  // there.
   template <class Pre, class Mid>
   static __device__ __forceinline__ bool compute(const char* ring, int slot, Acc& acc,
                                                  Pre&& pre, Mid&& mid) {
-    const char* rbase = ring + slot * STAGE;
+    const char* gbase = ring + slot * STAGE;
     Frag f[2];
     if (!pre()) return false;
-    load_frag(rbase, 0, f[0]);
+    load_frag(gbase, 0, f[0]);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      if (j == 0) load_frag(rbase, 1, f[1]);
-      const Frag& c = f[j];
+    for (int j = 0; j < JG; ++j) {
+      if (j + 1 < JG) load_frag(gbase, j + 1, f[(j + 1) & 1]);
+      const Frag& c = f[j & 1];
 #pragma unroll
       for (int m = 0; m < MFMAS; ++m) {
         const int rb = m / CB, cb = m % CB;
@@ -292,9 +336,11 @@ struct EngBf16SmallT {
   }
 };
 
-// 128x128 on one wave, 4 blocks per CU
-using EngBf16x128 = EngBf16SmallT<128, 64, 4>;
-// 256x128 on four waves, 2 blocks per CU
-using EngBf16x256x128 = EngBf16SmallT<256, 256, 2>;
+// 256x256 on eight waves, 1 block per CU: 32-deep stages, 64-k regions
+using EngBf16x256 = EngBf16T<256, 256, 512, 1, 32>;
+// 128x128 on one wave, 4 blocks per CU: 16-deep stages, 32-k regions
+using EngBf16x128 = EngBf16T<128, 128, 64, 4, 16>;
+// 256x128 on four waves, 2 blocks per CU: 16-deep stages, 32-k regions
+using EngBf16x256x128 = EngBf16T<256, 128, 256, 2, 16>;
 
 }  // namespace apk

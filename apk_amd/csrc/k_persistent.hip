@@ -11,8 +11,7 @@
 #include <mutex>
 
 #include "capi.hpp"
-#include "engine_bf16x128.hpp"
-#include "engine_bf16x256.hpp"
+#include "engine_bf16.hpp"
 #include "engine_mfma128.hpp"
 #include "engine_valu64.hpp"
 #include "pipeline.hpp"

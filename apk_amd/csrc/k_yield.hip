@@ -25,8 +25,7 @@
 // from LDS after a barrier (the snapshot discipline of src/midyield.cu:
 // 177-200), so a block never splits across barriers.
 #include "capi.hpp"
-#include "engine_bf16x128.hpp"
-#include "engine_bf16x256.hpp"
+#include "engine_bf16.hpp"
 #include "engine_mfma128.hpp"
 #include "engine_valu64.hpp"
 #include "pipeline.hpp"

@@ -323,8 +323,11 @@ int run_midyield(int argc, char** argv, const MidVariant& v) {
     nEv = std::min(events, 5);
     rig.reset(false);
     const unsigned probe = (unsigned)blocks * 4;
-    const double usPerTask = timed_run(poll, probe, false, 0, false) * 1e3 / probe;
-    const double runUs = usPerTask * tasks;
+    // every block ran 4 tasks of the probe; the run takes ceil(tasks /
+    // blocks) of them (not tasks * the probe's time per task, which assumes
+    // far more tasks than blocks)
+    const double usPerBlockTask = timed_run(poll, probe, false, 0, false) * 1e3 / 4;
+    const double runUs = usPerBlockTask * ((tasks + (unsigned)blocks - 1) / (unsigned)blocks);
     const long long gapNs = (long long)std::min(300000.0, runUs * 1e3 / (2.0 * (nEv + 1)));
     for (int e = 0; e < nEv; ++e) gaps.push_back(gapNs * (e + 1));
     printf("verify: %u tasks (~%.0f us), %d events %.1f us apart\n", tasks, runUs, nEv,

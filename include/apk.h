@@ -33,21 +33,27 @@ enum {
  *  MFMA128  : 128x128 fp32 tile on v_mfma_f32_32x32x2_f32 (fp32 matrix
  *             cores), 256 threads, 3-stage LDS ring fed by buffer_load ... lds.
  *  BF16X256 : 256x256 tile of a bf16 GEMM with fp32 accumulation on
- *             v_mfma_f32_32x32x16_bf16, 512 threads (2 waves per SIMD)
- *             (replaces the reference's fp16 wmma
- *             tile, src/tcyield.cu:91-356). Operands are bf16 (uint16 bit
+ *             v_mfma_f32_32x32x16_bf16, 512 threads (two waves per SIMD),
+ *             1 block per CU (replaces the reference's fp16 wmma tile,
+ *             src/tcyield.cu:91-356). Operands are bf16 (uint16 bit
  *             patterns): A is M x K row-major and B is passed TRANSPOSED, as
- *             Bt = N x K row-major (C = A . Bt^T); C is fp32 M x N.
+ *             Bt = N x K row-major (C = A . Bt^T); C is fp32 M x N. 32-deep
+ *             k-stages in pairs (sites every 64 k): K must be a multiple
+ *             of 64.
  *  BF16X128 : 128x128 tile of the same bf16 GEMM (same operand layout) on
  *             ONE wave (64 threads), 32 KiB of LDS: 4 blocks per CU, where
  *             the 256x256 tile cannot run (configs[4] of the reference's
- *             study at 4 blocks/CU). K must be a multiple of 32.
+ *             study at 4 blocks/CU). K must be a multiple of 32. At 4
+ *             blocks per CU its preemptible kernels take every register
+ *             of every SIMD: generations must be raised by the grid's own
+ *             setter (flag_set/sched), since apk_raise_flag's kernel finds
+ *             no SIMD until blocks exit.
  *  BF16X256X128 : 256x128 tile (256 rows of A, 128 of Bt) of the same bf16
  *             GEMM on 256 threads, 48 KiB of LDS: 2 blocks per CU
  *             (configs[4] at 2 blocks/CU). K must be a multiple of 32.
- * Both take 16-deep k-stages in pairs (sites every 32 k), and every bf16
- * engine forms each output's sum in the same k order: their C is
- * bit-identical to each other's and to BF16X256's on the same operands.
+ * Both take 16-deep k-stages in pairs (sites every 32 k). Every bf16 engine
+ * forms each output's sum in the same k order: their C is bit-identical to
+ * each other's on the same operands.
  * For the fp32 engines A is M x K and B is K x N, row-major fp32.
  */
 enum {
@@ -98,6 +104,7 @@ int apk_get_device_info(int device, apk_device_info* out);
 
 /* Geometry of a tile engine. */
 int apk_engine_geometry_of(int engine, apk_engine_geometry* out);
+
 
 /* Resident blocks per CU of the persistent_gemm kernel of `engine`
  * (replaces cudaOccupancyMaxActiveBlocksPerMultiprocessor,

@@ -46,6 +46,7 @@ def test_engine_geometry():
         apk_amd.geometry(99)
 
 
+
 @pytest.mark.parametrize("engine,M,N,K,kc,blocks,frag", [
     (apk_amd.ENGINE_VALU64, 100, 64, 64, 64, 4, "multiples"),
     (apk_amd.ENGINE_MFMA128, 128, 128, 96, 64, 4, "k_chunk"),
@@ -54,7 +55,9 @@ def test_engine_geometry():
     (apk_amd.ENGINE_VALU64, 0, 64, 64, 64, 1, "empty"),
     (apk_amd.ENGINE_BF16X256, 256, 128, 64, 64, 4, "multiples"),
     (apk_amd.ENGINE_BF16X256, 256, 256, 64, 48, 4, "k_chunk"),
-    # the small bf16 tiles load two 16-deep stages as one 32-deep region
+    # the bf16 tiles load a pair of stages as one region: an even number of
+    # stages (2 x 32 k for the 256x256 tile, 2 x 16 k for the others)
+    (apk_amd.ENGINE_BF16X256, 256, 256, 96, 32, 4, "multiple of 64"),
     (apk_amd.ENGINE_BF16X128, 128, 128, 48, 48, 4, "multiple of 32"),
     (apk_amd.ENGINE_BF16X256X128, 256, 128, 80, 16, 4, "multiple of 32"),
     (apk_amd.ENGINE_BF16X256X128, 128, 128, 64, 16, 4, "multiples"),

@@ -60,7 +60,7 @@ def run_bf16(torch, apk, A_bits, Bt_bits, k_chunk, blocks=None, eng=None):
 def test_bf16_layout_exact_small_integers(torch_gpu, apk, name):
     eng = apk.ENGINES[name]
     TM, TN = tile_of(apk, eng)
-    M, N, K = 2 * TM, TN, 96
+    M, N, K = 2 * TM, TN, 128
     say(f"{name} layout: small integers, M={M} N={N} K={K}")
     rng = np.random.default_rng(5)
     A_bits, A = bits_of_small_ints(rng, (M, K))
@@ -99,12 +99,11 @@ def test_bf16_bit_identical_across_chunks_and_workers(torch_gpu, apk, name):
         assert np.array_equal(C0.view(np.uint32), C1.view(np.uint32)), (kc, blocks)
 
 
-@pytest.mark.parametrize("K", [512, 96])
+@pytest.mark.parametrize("K", [512, 192])
 def test_bf16_engines_bit_identical(torch_gpu, apk, K):
     """The three bf16 tiles form every output's sum in the same k order (k
-    steps of 16, ascending), so C is bit-identical across them; K = 96 is 3
-    stages of 32 for the 256x256 tile (its last pair's second stage zeros)
-    and 3 load regions of 32 for the other two."""
+    steps of 16, ascending), so C is bit-identical across them; K = 192 is 3
+    load regions of 64 for the 256x256 tile and 6 of 32 for the other two."""
     say(f"bf16x256 vs bf16x128 vs bf16x256x128, M=N=512 K={K}")
     A_bits, A, B_bits, B = oracle.fill_normal_bf16(13, 512, 512, K)
     Bt_bits = np.ascontiguousarray(B_bits.T)
@@ -273,14 +272,11 @@ def test_bf16_float64_and_oracle(bf16_job, apk):
 
 @pytest.fixture(scope="module", params=ENGS)
 def bf16_odd_job(torch_gpu, apk, request):
-    # An odd number of pairs. The 256x256 tile: 5 k-stages of 32 (K = 160),
-    # taken in pairs (0,1), (2,3), (4, a stage of zeros), the urgent job's 3
-    # stages ending the same way. The 128x128 and 256x128 tiles load a pair
-    # of 16-deep stages as one region, so their tiles hold whole pairs: 5
-    # pairs (K = 160, sites 0, 2, ..., 8), the urgent job 3 (K = 96).
+    # An odd number of pairs (each pair is one load region): 5 (sites 0, 2,
+    # ..., 8), the urgent job 3.
     eng = apk.ENGINES[request.param]
     ks = apk.geometry(eng).k_stage
-    K, Ku = (5 * ks, 3 * ks) if ks == 32 else (160, 96)
+    K, Ku = 10 * ks, 6 * ks
     TM, TN = tile_of(apk, eng)
     # 48 tasks per block: the job outlasts the 24 events the setter raises
     # 3 us apart (the one-wave tile finishes 24 short tiles in about 70 us)
@@ -294,10 +290,9 @@ def bf16_odd_job(torch_gpu, apk, request):
 @pytest.mark.parametrize("resume", [0, 1, 2])
 def test_bf16_odd_length_pairs_yield(bf16_odd_job, apk, resume):
     """Yields at every site of tiles with an odd number of pairs, incl. the
-    last pair (for the 256x256 tile the one whose second stage is all zeros,
-    checkpointed and restored with the pair): C bit-identical to the
-    unpreempted run, within tolerance of float64, urgent outputs equal the
-    non-preemptible urgent GEMM, every task and event counted once."""
+    last pair: C bit-identical to the unpreempted run, within tolerance of
+    float64, urgent outputs equal the non-preemptible urgent GEMM, every task
+    and event counted once."""
     j = bf16_odd_job
     say(f"engine {j.eng} odd-length pairs, stage yields, resume={resume}")
     ref = j.run(apk.POLL_OFF, events=0)

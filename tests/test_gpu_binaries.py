@@ -224,7 +224,9 @@ def test_phase5_sh(tmp_path):
 
 def test_tcyield(tmp_path):
     """tcyield (src/tcyield.cu:384-842): verify, calibrate, overhead, events."""
-    run_bin("tcyield", "--mode", "verify", "--tasks", 256)
+    # 8 tasks per block: the setter (block 0) raises the 5 events at its own
+    # sites, one per site, and a 256-deep task has only 4 of them
+    run_bin("tcyield", "--mode", "verify", "--tasks", 2048)
     out = run_bin("tcyield", "--mode", "calibrate", "--tasks", 512)
     assert "GFLOP/s" in out
     run_bin("tcyield", "--mode", "overhead", "--poll", "pe", "--tasks", 512, "--reps", 4)
