@@ -75,7 +75,7 @@ namespace apk {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
-template <int TM_, int TN_, int THREADS_, int BPC_, int KS_>
+template <int TM_, int TN_, int THREADS_, int BPC_, int KS_, int IVMAX_>
 struct EngBf16T {
   static_assert(TM_ == 128 || TM_ == 256, "128 or 256 tile rows");
   static_assert(TN_ == 128 || TN_ == 256, "128 or 256 tile columns");
@@ -257,11 +257,13 @@ struct EngBf16T {
   }
 
   static constexpr int JG = RK / 16;  // MFMA k-steps per pair (one region)
-  // The next pair's loads go out one per IV MFMAs from the pair's start (at
-  // most one per two: issued densely at the front of the pair they have the
-  // rest of it to land).
+  // The next pair's loads go out one per IV MFMAs from the pair's start, at
+  // most one per IVMAX: issued densely at the front of the pair, they have
+  // the rest of it to land. Measured at cfg5 (calibrate, one box): one per
+  // MFMA is 2% faster than one per two for the 256x256 tile and 4.6% for
+  // the one-wave 128x128 tile; one per two is 2% faster for 256x128.
   static constexpr int IV_FIT = JG * MFMAS / (GROUP * LOADS);
-  static constexpr int IV = IV_FIT < 2 ? IV_FIT : 2;
+  static constexpr int IV = IV_FIT < IVMAX_ ? IV_FIT : IVMAX_;
   static_assert(IV >= 1, "loads spread over the MFMAs");
 
   // One pair: the region in ring slots slot and slot+1, MFMAS MFMAs per
@@ -337,10 +339,10 @@ struct EngBf16T {
 };
 
 // 256x256 on eight waves, 1 block per CU: 32-deep stages, 64-k regions
-using EngBf16x256 = EngBf16T<256, 256, 512, 1, 32>;
+using EngBf16x256 = EngBf16T<256, 256, 512, 1, 32, 1>;
 // 128x128 on one wave, 4 blocks per CU: 16-deep stages, 32-k regions
-using EngBf16x128 = EngBf16T<128, 128, 64, 4, 16>;
+using EngBf16x128 = EngBf16T<128, 128, 64, 4, 16, 1>;
 // 256x128 on four waves, 2 blocks per CU: 16-deep stages, 32-k regions
-using EngBf16x256x128 = EngBf16T<256, 128, 256, 2, 16>;
+using EngBf16x256x128 = EngBf16T<256, 128, 256, 2, 16, 2>;
 
 }  // namespace apk

@@ -36,7 +36,9 @@
 // --mean-gap-us, --seed, --flag-copies, --verify-rows (float64 rows of C),
 // --poll-every N (--poll boundary: a site at every N-th k-chunk boundary,
 // counted across tasks), --prewarm-ms T (--mode calibrate: T ms of untimed
-// runs before the timed one).
+// runs before the timed one), --fingerprints 0|1 (default 1: fingerprint
+// every background task against its unpreempted tile; 0 for latency runs,
+// since hashing a tile holds its block off its poll sites).
 #pragma once
 
 namespace host {

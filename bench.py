@@ -24,14 +24,17 @@ latency at k-stage and tile-boundary polls (flag set -> last block observes,
 the reference's latency), the retreat arm (one background job; flag raised ->
 urgent GEMM starts on its own stream), the no-preemption baseline, the polling
 overhead (ABAB drains) and the tile time at full residency they are measured
-against -- and `bf16`: the cfg5 bf16 MFMA GEMM throughput (M=N=K=8192,
-256x256 tiles, no yields) with its engine clock: right after the preemption
+against, and the same latencies with the tile taken as a 32- and a 64-deep
+k-chunk (`by_k_chunk`) -- and `bf16`: the cfg5 bf16 MFMA GEMM throughput
+(M=N=K=8192, 256x256 tiles, no yields) with its engine clock: right after the preemption
 runs (`tflops`, the poll-off preemptible kernel over two GEMMs), and
 sustained (one GEMM per launch after a pre-warm of the same launches), beside
 torch.matmul (hipBLASLt) on the same operands under the same conditions (the
 sustained bf16 clock is set by the load on the whole chip; `--bf16-sweep`
-times the GEMM on 64-256 workers), and the retreat arm on the bf16 background
-(10,000 arrivals; retreating tiles re-queued from k = 0).
+times the GEMM on 64-256 workers), the retreat arm on the bf16 background
+(10,000 arrivals; retreating tiles re-queued from k = 0), and cfg5 at 1, 2
+and 4 blocks per CU (`occupancy`: each occupancy's tile, its throughput and
+its cooperative stage-poll latency in k-chunk times).
 
 Usage: python bench.py [--gpus 1] [--steps 10] [--warmup 3] [--no-preempt]
 """
@@ -242,6 +245,47 @@ def preemption_metrics(events, trials):
                   "--mean-gap-us", 2000, "--trials", trials], timeout=900)
     n50, n99 = grab(nb, r"urgent e2e \(us\):\s+p50 ([\d.]+) \| p90 [\d.]+ \| p99 ([\d.]+)")
     out["no_preempt_urgent_e2e_us"] = {"p50": n50, "p99": n99, "trials": trials}
+    out["by_k_chunk"] = latency_by_k_chunk(max(events // 5, 500), tile_us)
+    return out
+
+
+def latency_by_k_chunk(events, tile128_us):
+    """The cfg3 latencies with the tile taken as a 32- and a 64-deep k-chunk
+    (cfg2's per-tile K set {32, 64, 128}): the cooperative arm at every
+    k-stage, and the retreat arm (accumulator checkpoints), each job walking
+    K in chunks of that depth. Polls sit at every 32-deep k-stage in both, so
+    the latency in us hardly moves with the chunk, and its ratio to a tile
+    grows as the tile shrinks. The cooperative tile time is the 128-deep
+    chunk's scaled by depth; the retreat arm measures its own (polls off)."""
+    out = {}
+    for kc in (32, 64):
+        cfg = ["--engine", "mfma128", "--tiles-m", "64", "--tiles-n", "64", "--gemm-k", "4096",
+               "--k", str(kc)]
+        lat = run_bin("yield", ["--mode", "latency"] + cfg + CFG3_URGENT +
+                      ["--poll", "stage", "--arrival", "exp", "--mean-gap-us", 2000,
+                       "--events", events + 100], timeout=600)
+        p50, p99 = grab(lat, r"preemption latency set->last \(us\): p50 ([\d.]+) \| "
+                             r"p90 [\d.]+ \| p99 ([\d.]+)")
+        tile = tile128_us * kc / 128
+        rt = run_bin("urgent_baseline", cfg + CFG3_URGENT +
+                     ["--bg-tasks", 4096, "--urgent-blocks", 4, "--arrival", "exp",
+                      "--mean-gap-us", 2000, "--yield", 1, "--retreat", 4, "--oracle", 1,
+                      "--continuous", 1, "--events", events, "--resume", "acc"], timeout=600)
+        r50, r99 = grab(rt, r"flag raised -> urgent GEMM starts \(us\): p50 ([\d.]+) \| "
+                            r"p90 [\d.]+ \| p99 ([\d.]+)")
+        rtile, = grab(rt, r"tile \(k-chunk\) time at full residency: ([\d.]+) us")
+        bad, total = grab(rt, r"SAFETY: (\d+) of (\d+) task fingerprints", int)
+        out[str(kc)] = {
+            "coop_k_stage": {"p50": p50, "p99": p99, "tile_us": round(tile, 3),
+                             "p50_over_tile": round(p50 / tile, 3),
+                             "p99_over_tile": round(p99 / tile, 3)},
+            "retreat": {"p50": r50, "p99": r99, "tile_us": rtile,
+                        "p50_over_tile": round(r50 / rtile, 3),
+                        "p99_over_tile": round(r99 / rtile, 3), "corrupt_tasks": bad,
+                        "tasks_checked": total,
+                        "oracle": "PASS" if ("ORACLE: PASS" in rt and "yield: PASS" in rt)
+                        else "FAIL"},
+            "events": events}
     return out
 
 
@@ -273,7 +317,9 @@ def bf16_metrics():
     ovh, = grab(rt, r"retreat overhead ([-\d.]+)%")
     _, below = grab(rt, r"background alone with polls off: ([\d.]+) TFLOP/s -> the job "
                         r"with arrivals ([-\d.]+)% below it")
-    return {"workload": "cfg5: bf16 GEMM M=N=K=8192 (2 passes of 1024 256x256 tiles), fp32 "
+    occ = bf16_occupancy_points()
+    return {"occupancy": occ,
+            "workload": "cfg5: bf16 GEMM M=N=K=8192 (2 passes of 1024 256x256 tiles), fp32 "
                         "accumulate, 256 workers, no yields, after 1.5 s of the same runs",
             "tflops": round(tf, 2), "peak": 2516.6, "frac": round(tf / 2516.6, 4),
             "engine_clock_mhz": mhz,
@@ -288,6 +334,50 @@ def bf16_metrics():
                                    "tasks_checked": total,
                                    "oracle": "PASS" if ("ORACLE: PASS" in rt and
                                                         "yield: PASS" in rt) else "FAIL"}}
+
+
+def bf16_occupancy_points(events=2000):
+    """cfg5 at 1, 2 and 4 blocks per CU: the tile each occupancy runs
+    (256x256 on 8 waves, 256x128 on 4 waves, 128x128 on one wave), its
+    poll-off throughput with the engine clock (tcyield calibrate, after 1 s
+    of the same runs), and the cooperative arm's stage-poll latency (set ->
+    last block observes, `events` arrivals at U(150, 400) us gaps, urgent bf16
+    GEMM 256^3, full checkpoints) in k-chunk times (256-deep chunks, 32 per
+    tile). The latency runs hash no task fingerprints (as the reference
+    measures it): their safety rests on every urgent output, the float64
+    check of C and the exactly-once counts; fingerprints are checked by the
+    GPU tests."""
+    out = []
+    for eng, blocks, tm, tn in (("bf16x256", 256, 32, 32), ("bf16x256x128", 512, 32, 64),
+                                ("bf16x128", 1024, 64, 64)):
+        g = ["--engine", eng, "--tiles-m", tm, "--tiles-n", tn, "--gemm-k", 8192, "--k", 256,
+             "--blocks", blocks]
+        t = run_bin("tcyield", ["--mode", "calibrate"] + g + ["--tasks", 2 * blocks * 8,
+                                                              "--prewarm-ms", 1000])
+        us, gf = grab(t, r"-> ([\d.]+) us/task/block \| ([\d.]+) GFLOP/s")
+        mhz, = grab(t, r"engine clock during the run \(\d+ probes\): mean ([\d.]+) MHz")
+        ev = run_bin("tcyield", ["--mode", "events"] + g +
+                     ["--poll", "stage", "--events", events, "--urgent-m", 256, "--urgent-n",
+                      256, "--urgent-k", 256, "--verify-rows", 8, "--oracle", 1,
+                      "--fingerprints", 0], timeout=600)
+        p50, p99 = grab(ev, r"latency set->last \(us\): p50 ([\d.]+) \| p90 [\d.]+ \| "
+                            r"p99 ([\d.]+)")
+        first, = grab(ev, r"first observer p50 ([\d.]+) us")
+        bad, = grab(ev, r"SAFETY: (\d+)/\d+ urgent outputs corrupt", int)
+        chunk_us = us / 32
+        tf = gf / 1e3
+        out.append({"engine": eng, "tile": [8192 // tm, 8192 // tn],
+                    "blocks_per_cu": blocks // 256, "tflops": round(tf, 1),
+                    "frac": round(tf / 2516.6, 4), "engine_clock_mhz": mhz,
+                    "frac_at_measured_clock": round(tf / (2516.6 * mhz / 2400.0), 4),
+                    "k_chunk_us": round(chunk_us, 3),
+                    "coop_stage_latency_us": {"p50": p50, "p99": p99, "first_observer_p50": first,
+                                              "p50_over_k_chunk": round(p50 / chunk_us, 3),
+                                              "events": events},
+                    "corrupt_urgent_outputs": bad,
+                    "c_check": "PASS" if "bg C PASS" in ev else "FAIL",
+                    "oracle": "PASS" if "ORACLE: PASS" in ev else "FAIL"})
+    return out
 
 
 def timed_sustained(launch, flop, steps, prewarm_ms, wall_mhz, torch, apk_amd, stream):

@@ -236,6 +236,11 @@ def test_tcyield(tmp_path):
     assert "SAFETY:" in out
     assert_header(csv, HDR_TCYIELD)
     assert 0 < len(read_csv(csv)) <= 100
+    # the latency runs' variant: no per-task fingerprints, same verdict
+    out = run_bin("tcyield", "--mode", "events", "--poll", "stage", "--events", 100,
+                  "--warmup-events", 10, "--fingerprints", 0, "--oracle", 1)
+    assert "0 of 0 task fingerprints differ from the unpreempted tile (--fingerprints 0)" in out
+    assert "ORACLE: PASS" in out and "events: PASS" in out
 
 
 @pytest.mark.parametrize("loaded,iters", [(0, 0), (1, 64)])
