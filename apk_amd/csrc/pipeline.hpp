@@ -223,16 +223,47 @@ __device__ __forceinline__ uint64_t store_tile(const typename E::Acc& acc, char*
                                                bool want_hash) {
   uint64_t h = 0;
   constexpr int Q = E::TN / 4;  // float4 per row
+  // Every thread moves the same number of float4 per pass, in batches of up
+  // to 4 whose LDS reads are all issued before the batch's first store (one
+  // read per store, each waited for in turn, serialised an LDS round trip
+  // per float4: 16 of them per pass for a one-wave block, ~5 us per tile).
+  // The batch loop stays rolled: unrolled, the 2-wave-per-SIMD polled
+  // kernels took all 256 registers of their half of a SIMD, and a small
+  // kernel on another stream (the retreat arm's flag raise) could no longer
+  // be dispatched beside the grid.
+  constexpr int ITERS = E::PASS_ROWS * Q / E::THREADS;
+  constexpr int BATCH = ITERS < 4 ? ITERS : 4;
+  static_assert(ITERS * E::THREADS == E::PASS_ROWS * Q && ITERS % BATCH == 0,
+                "whole float4 per thread per pass");
 #pragma unroll
   for (int p = 0; p < E::STORE_PASSES; ++p) {
     E::stage_pass(acc, lds, p);
     lds_sync();
-    for (int i = threadIdx.x; i < E::PASS_ROWS * Q; i += E::THREADS) {
-      const int rr = i / Q, c4 = (i % Q) * 4;
-      const int r = E::pass_row(p, rr);
-      const float4 v = *(const float4*)((const float*)lds + rr * E::STAGE_LD + c4);
-      *(float4*)(C + (size_t)(row0 + r) * ldc + col0 + c4) = v;
-      if (want_hash) {
+#pragma unroll 1
+    for (int b0 = 0; b0 < ITERS; b0 += BATCH) {
+      float4 vs[BATCH];
+#pragma unroll
+      for (int it = 0; it < BATCH; ++it) {
+        const int i = (int)threadIdx.x + (b0 + it) * E::THREADS;
+        vs[it] = *(const float4*)((const float*)lds + (i / Q) * E::STAGE_LD + (i % Q) * 4);
+      }
+#pragma unroll
+      for (int it = 0; it < BATCH; ++it) {
+        const int i = (int)threadIdx.x + (b0 + it) * E::THREADS;
+        const int r = E::pass_row(p, i / Q);
+        *(float4*)(C + (size_t)(row0 + r) * ldc + col0 + (i % Q) * 4) = vs[it];
+      }
+    }
+    // The fingerprint reads the pass again, one float4 at a time: hashed
+    // under the unrolled stores, the 64-bit mixing of every value of the
+    // pass at once spilled the polled kernels' registers.
+    if (want_hash) {
+#pragma unroll 1
+      for (int it = 0; it < ITERS; ++it) {
+        const int i = (int)threadIdx.x + it * E::THREADS;
+        const int rr = i / Q, c4 = (i % Q) * 4;
+        const int r = E::pass_row(p, rr);
+        const float4 v = *(const float4*)((const float*)lds + rr * E::STAGE_LD + c4);
         const uint64_t e = (uint64_t)(r * E::TN + c4);
         h += mix64((uint64_t)__float_as_uint(v.x) + (e << 32));
         h += mix64((uint64_t)__float_as_uint(v.y) + ((e + 1) << 32));
