@@ -6,14 +6,17 @@
 //  EngBf16x256     (engine bf16x256, 1 block per CU): 256x256 on 8 waves
 //                  (2x4, each 128x64: 128 fp32 per lane), two waves per SIMD;
 //                  a 256 KiB fp32 accumulator is half of a CU's register
-//                  file, so no second block fits. A wave takes at most 239
-//                  of its SIMD's 256 registers per lane, so a small kernel
-//                  launched on another stream while the grid runs (the
-//                  retreat arm's flag raise, the clock probes) still finds
-//                  registers on every SIMD. (The same tile on 4 waves of
-//                  128x128 measured 1,382 against 1,286 TFLOP/s at cfg5, but
-//                  its polled kernels take all 512 registers of each SIMD:
-//                  the flag-raise kernel then waits for the job to end.)
+//                  file, so no second block fits. A wave of the poll-off,
+//                  stage- and chunk-polled and retreat kernels takes at most
+//                  246 of its SIMD's 256 registers per lane (allocated in 8s),
+//                  so a small kernel launched on another stream while the
+//                  grid runs (the retreat arm's flag raise, the clock probes)
+//                  still finds registers on every SIMD; the issue-site
+//                  kernels, whose generations come from the grid's own
+//                  setter, take 249. (The same tile on 4 waves of 128x128 is
+//                  no faster, and its polled kernels take all 512 registers
+//                  of each SIMD: the flag-raise kernel then waits for the
+//                  job to end.)
 //  EngBf16x128     (engine bf16x128, 4 blocks per CU): 128x128 on ONE wave
 //                  (all 4x4 32x32 accumulators, 256 fp32 per lane, in AGPRs;
 //                  8 operand reads per 16 MFMAs). With one wave per block
@@ -64,10 +67,13 @@
 // and however often it is checkpointed and resumed: the three tiles give
 // bit-identical C.
 //
-// Epilogue: the fp32 tile is staged through LDS one accumulator row block of
-// every wave per pass (32 rows per wave row), row stride TN + 4 floats (the
-// two half-waves write rows 4 apart, which then fall on different banks),
-// then moved to C with 16-byte coalesced stores (and fingerprinted).
+// Epilogue: each wave stores its accumulators straight to C (store_direct:
+// one dword store per register = two whole 128-byte row segments). A tile
+// that is fingerprinted is instead staged through LDS one accumulator row
+// block of every wave per pass (32 rows per wave row), row stride TN + 4
+// floats (the two half-waves write rows 4 apart, which then fall on
+// different banks), then moved to C with 16-byte coalesced stores and
+// hashed.
 #pragma once
 #include "device.hpp"
 
@@ -321,6 +327,27 @@ struct EngBf16T {
   // Epilogue pass p: accumulator row block rb = p of every wave into LDS as
   // rows [wm*32, wm*32+32) of a PASS_ROWS x TN tile; LDS row rr holds tile
   // row pass_row(p, rr).
+  // The C tile straight from the accumulators, no LDS: accumulator register
+  // i of a 32x32 block holds, in lanes 0-31, 32 consecutive columns of one
+  // row, and in lanes 32-63 the same columns 4 rows below, so one dword
+  // store per register writes two whole 128-byte row segments. Every wave
+  // stores its own sub-tile with no barrier. (A fingerprinted tile takes the
+  // staged epilogue: its hash, unrolled over every register here, spilled.)
+  static __device__ __forceinline__ void store_direct(const Acc& acc, float* C, int ldc,
+                                                      int row0, int col0) {
+    const int w = threadIdx.x >> 6, l = lane_id();
+    const int wm = w % WM, wn = w / WM;
+    float* base = C + (size_t)(row0 + wm * WTM + 4 * (l >> 5)) * ldc + col0 + wn * WTN + (l & 31);
+#pragma unroll
+    for (int rb = 0; rb < RB; ++rb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        float* row = base + (size_t)(rb * 32 + 8 * (i >> 2) + (i & 3)) * ldc;
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) row[cb * 32] = acc.c[rb][cb][i];
+      }
+  }
+
   static __device__ __forceinline__ void stage_pass(const Acc& acc, char* lds, int p) {
     const int w = threadIdx.x >> 6, l = lane_id();
     const int wm = w % WM, wn = w / WM;

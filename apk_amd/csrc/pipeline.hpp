@@ -217,10 +217,26 @@ __device__ __forceinline__ void sample_flag(i32x4 flag_rsrc, uint32_t lds_addr) 
 // 16-byte pieces to C (coalesced rows) and, when asked, folds them into the
 // fingerprint. Returns the per-thread partial hash. The caller must have
 // finished every read of the ring (lds_sync) before calling.
+template <class E, class = void>
+struct HasDirectStore {
+  static constexpr bool value = false;
+};
+template <class E>
+struct HasDirectStore<E, std::void_t<decltype(&E::store_direct)>> {
+  static constexpr bool value = true;
+};
 template <class E>
 __device__ __forceinline__ uint64_t store_tile(const typename E::Acc& acc, char* lds,
                                                float* C, int ldc, int row0, int col0,
                                                bool want_hash) {
+  // An engine whose accumulator layout holds whole row segments per register
+  // stores an unfingerprinted tile directly (no LDS, no barrier).
+  if constexpr (HasDirectStore<E>::value) {
+    if (!want_hash) {
+      E::store_direct(acc, C, ldc, row0, col0);
+      return 0;
+    }
+  }
   uint64_t h = 0;
   constexpr int Q = E::TN / 4;  // float4 per row
   // Every thread moves the same number of float4 per pass, in batches of up
