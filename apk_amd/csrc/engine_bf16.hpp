@@ -7,13 +7,13 @@
 //                  (2x4, each 128x64: 128 fp32 per lane), two waves per SIMD;
 //                  a 256 KiB fp32 accumulator is half of a CU's register
 //                  file, so no second block fits. A wave of the poll-off,
-//                  stage- and chunk-polled and retreat kernels takes at most
-//                  246 of its SIMD's 256 registers per lane (allocated in 8s),
-//                  so a small kernel launched on another stream while the
-//                  grid runs (the retreat arm's flag raise, the clock probes)
-//                  still finds registers on every SIMD; the issue-site
-//                  kernels, whose generations come from the grid's own
-//                  setter, take 249. (The same tile on 4 waves of 128x128 is
+//                  chunk-polled and retreat kernels takes at most 246 of its
+//                  SIMD's 256 registers per lane (allocated in 8s), so a
+//                  small kernel launched on another stream while the grid
+//                  runs (the retreat arm's flag raise, the clock probes)
+//                  still finds registers on every SIMD; the cooperative
+//                  stage- and issue-site kernels, whose generations come from
+//                  the grid's own setter or a host store, take 249. (The same tile on 4 waves of 128x128 is
 //                  no faster, and its polled kernels take all 512 registers
 //                  of each SIMD: the flag-raise kernel then waits for the
 //                  job to end.)

@@ -44,7 +44,9 @@ k_persistent_yield(const apk_yield_params) {
   // then keeps its own values in registers without spilling.
   auto P = [&]() -> const KArg<apk_yield_params>& { return *kernel_args<apk_yield_params>(); };
   __shared__ __attribute__((aligned(16))) char ring[E::LDS_BYTES];
-  __shared__ int flagring[E::NS];  // flag sample issued with stage t: [t % NS]
+  // flag sample issued with stage t: [t % NS]; [NS]: the one issued with a
+  // task pop (task-start sites)
+  __shared__ int flagring[E::NS + 1];
   __shared__ unsigned s_u32;
   __shared__ int s_i32[3];
   __shared__ uint64_t s_red[E::THREADS / 64];
@@ -86,6 +88,14 @@ k_persistent_yield(const apk_yield_params) {
       make_rsrc((const char*)P().flag + (size_t)(bid % copies()) * APK_FLAG_STRIDE, 4);
   const bool isSetter = P().flag_set != nullptr && P().sched != nullptr && bid == 0;
   constexpr bool retreatArm = RETREAT && POLL != APK_POLL_OFF;
+  // Task-start sites (cooperative arm, stage polls, drain discipline): thread
+  // 0 samples the flag right before it takes a new task, so the sample lands
+  // with the task pop's own round trip, and a new generation is acted on at
+  // stage 0 before the tile's first loads have landed. Without it the first
+  // site of a task reads a sample only once the first region is in, and that
+  // wait is part of the stretch between two tasks in which a block sees
+  // nothing -- the stretch the last observer of an event is found in.
+  const bool startSites = POLL == APK_POLL_STAGE && !retreatArm && !P().naive;
   auto domain = [&] { return (int)xcc_id() * APK_SES_PER_XCD + (int)se_id(); };
   auto quota = [&] { return (P().retreat + APK_RETREAT_DOMAINS - 1) / APK_RETREAT_DOMAINS; };
   // Retreat arm: whether this block may still retreat at a later generation
@@ -106,7 +116,7 @@ k_persistent_yield(const apk_yield_params) {
 
   const uint32_t wl = wave_lds(ring);
   const uint32_t flag_lds = lds_addr_of(flagring);
-  if (tid < E::NS) flagring[tid] = 0;
+  if (tid <= E::NS) flagring[tid] = 0;
   if (tid < APK_STATS_PER_BLOCK) s_stats[tid] = 0;
   if (tid < 2) s_setter[tid] = 0;
   if (P().run_gt && bid == 0 && tid == 0) P().run_gt[0] = wall_ticks();
@@ -204,6 +214,8 @@ k_persistent_yield(const apk_yield_params) {
     const float* src = nullptr;
     bool urgent = false;
     int rqHeld = -1;  // resume ticket whose checkpoint this job reads back
+    bool startSite = false;  // uniform: a task-start sample was taken for this job
+    int fStart = 0;          // uniform: its value
     if (!RETREAT && serving >= 0) {
       if (uidx < nU()) {
         urgent = true;
@@ -253,8 +265,13 @@ k_persistent_yield(const apk_yield_params) {
             }
           }
         }
-        if (t == 0xffffffffu)
+        if (t == 0xffffffffu) {
+          // the task-start sample goes out in front of the pop's fetch-add,
+          // and the wait for the pop retires it
+          if (startSites) sample_flag<SYS>(flag_rsrc, flag_lds + 4u * (uint32_t)E::NS);
           t = TaskQueue(P().next_task, P().M / E::TM, tilesN(), P().num_tasks).pop((int)xcc_id());
+          if (startSites) wait_vmcnt<0>();
+        }
         s_u32 = t;
         s_i32[0] = kind;
         s_i32[1] = st;
@@ -265,6 +282,10 @@ k_persistent_yield(const apk_yield_params) {
       const int kind = uniform(s_i32[0]);
       const int qStage = uniform(s_i32[1]);
       const int qTicket = uniform(s_i32[2]);
+      if (startSites && kind < 0) {
+        startSite = true;
+        fStart = uniform(flagring[E::NS]);
+      }
       __syncthreads();
       if (task == 0xfffffffeu) continue;  // lost resume entry (counted)
       if (task >= P().num_tasks) break;
@@ -412,7 +433,19 @@ k_persistent_yield(const apk_yield_params) {
       // happen below, outside it, so that none of their state is live in it.
       bool atSite = false;
       int fSeen = 0;
-      while (s < S) {
+      if (startSite) {
+        // Task-start site: stage 0's site, taken on the sample that came back
+        // with the task pop, before the first loads have landed (they are in
+        // flight; a yield drains them). Nothing new: stage 0's own site still
+        // reads its sample.
+        startSite = false;
+        fLatest = fStart;
+        if (fStart != lastSeen) {
+          fSeen = fStart;
+          atSite = true;
+        }
+      }
+      while (!atSite && s < S) {
         if constexpr (E::GROUP == 1) {
           wait_landed<E>();
           lds_sync();
