@@ -7,13 +7,13 @@
 //                  (2x4, each 128x64: 128 fp32 per lane), two waves per SIMD;
 //                  a 256 KiB fp32 accumulator is half of a CU's register
 //                  file, so no second block fits. A wave of the poll-off,
-//                  chunk-polled and retreat kernels takes at most 246 of its
+//                  chunk-polled and retreat kernels takes at most 248 of its
 //                  SIMD's 256 registers per lane (allocated in 8s), so a
 //                  small kernel launched on another stream while the grid
 //                  runs (the retreat arm's flag raise, the clock probes)
 //                  still finds registers on every SIMD; the cooperative
 //                  stage- and issue-site kernels, whose generations come from
-//                  the grid's own setter or a host store, take 249. (The same tile on 4 waves of 128x128 is
+//                  the grid's own setter, take 249-251. (The same tile on 4 waves of 128x128 is
 //                  no faster, and its polled kernels take all 512 registers
 //                  of each SIMD: the flag-raise kernel then waits for the
 //                  job to end.)
@@ -202,12 +202,12 @@ struct EngBf16T {
   static __device__ __forceinline__ Dst stage_dst(uint32_t wave_lds, const Ctx& c, int slot,
                                                   int t, int S) {
     const bool real = t < S;
-    i32x4 za = c.ra, zb = c.rb;
-    za.z = 0;
-    zb.z = 0;
+    // only the resources' record counts differ (one select each)
+    i32x4 ra = c.ra, rb = c.rb;
+    ra.z = real ? c.ra.z : 0;
+    rb.z = real ? c.rb.z : 0;
     const uint32_t k = (t & 1) ? NO_LOADS : (uint32_t)((real ? t : 0) * KS * 2);
-    return Dst{wave_lds + (uint32_t)((slot & ~1) * STAGE), k, real ? c.ra : za,
-               real ? c.rb : zb};
+    return Dst{wave_lds + (uint32_t)((slot & ~1) * STAGE), k, ra, rb};
   }
   // Byte offset inside a region of region load i's piece (thread t's 16
   // bytes of load i land at region + region_off(i) + 16 t).

@@ -538,7 +538,7 @@ k_persistent_yield(const apk_yield_params) {
           typename E::Dst d0 = E::stage_dst(wl, ctx, other, s + 2, S);
           typename E::Dst d1 = E::stage_dst(wl, ctx, other + 1, s + 3, S);
           E::pin(d0);
-          E::pin(d1);
+          if constexpr (!HasIssueGroup<E>::value) E::pin(d1);  // unused by region loads
           wait_landed<E>();
           lds_sync();
           if constexpr (POLL == APK_POLL_ISSUE) {

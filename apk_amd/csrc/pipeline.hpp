@@ -171,7 +171,7 @@ __device__ __forceinline__ void run_stages(char* ring, uint32_t wl, const typena
       typename E::Dst d0 = E::stage_dst(wl, c, other, s + 2, S);
       typename E::Dst d1 = E::stage_dst(wl, c, other + 1, s + 3, S);
       E::pin(d0);
-      E::pin(d1);
+      if constexpr (!HasIssueGroup<E>::value) E::pin(d1);  // unused by region loads
       wait_landed<E>();
       lds_sync();
       if (s + 1 < S) hook(s + 1);
