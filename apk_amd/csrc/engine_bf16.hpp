@@ -324,9 +324,6 @@ struct EngBf16T {
     a.c[(e >> 4) / CB][(e >> 4) % CB][e & 15] = v;
   }
 
-  // Epilogue pass p: accumulator row block rb = p of every wave into LDS as
-  // rows [wm*32, wm*32+32) of a PASS_ROWS x TN tile; LDS row rr holds tile
-  // row pass_row(p, rr).
   // The C tile straight from the accumulators, no LDS: accumulator register
   // i of a 32x32 block holds, in lanes 0-31, 32 consecutive columns of one
   // row, and in lanes 32-63 the same columns 4 rows below, so one dword
@@ -348,6 +345,9 @@ struct EngBf16T {
       }
   }
 
+  // Epilogue pass p: accumulator row block rb = p of every wave into LDS as
+  // rows [wm*32, wm*32+32) of a PASS_ROWS x TN tile; LDS row rr holds tile
+  // row pass_row(p, rr).
   static __device__ __forceinline__ void stage_pass(const Acc& acc, char* lds, int p) {
     const int w = threadIdx.x >> 6, l = lane_id();
     const int wm = w % WM, wn = w / WM;
