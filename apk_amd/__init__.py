@@ -51,7 +51,7 @@ FLAG_STRIDE, FLAG_MAX_COPIES = 4096, 256
 STATS_PER_BLOCK = 16
 # columns of a stats row (APK_ST_* in include/apk.h)
 (ST_YIELDS, ST_SAVE, ST_URGENT, ST_RESTORE, ST_INFLIGHT, ST_RETREATS, ST_RESUMED, ST_ERRORS,
- ST_STALE, ST_CHECKPOINTS, ST_INFLIGHT_ALL, ST_STALE_ALL, ST_DECLINED) = range(13)
+ ST_STALE, ST_CHECKPOINTS, ST_INFLIGHT_ALL, ST_STALE_ALL, ST_DECLINED, ST_START_SITES) = range(14)
 QUEUE_WORDS, QUEUE_XCDS = 16, 8
 RQ_CTL_WORDS = 4  # resume ring control words (APK_RQ_CTL_WORDS)
 SES_PER_XCD, RETREAT_DOMAINS = 4, 32

@@ -155,7 +155,7 @@ k_persistent_yield(const apk_yield_params) {
          ST_RESTORE = APK_ST_RESTORE, ST_INFLIGHT = APK_ST_INFLIGHT,
          ST_RETREATS = APK_ST_RETREATS, ST_RESUMED = APK_ST_RESUMED, ST_ERRORS = APK_ST_ERRORS,
          ST_STALE = APK_ST_STALE, ST_CHECKPOINTS = APK_ST_CHECKPOINTS,
-         ST_DECLINED = APK_ST_DECLINED,
+         ST_DECLINED = APK_ST_DECLINED, ST_START_SITES = APK_ST_START_SITES,
          ST_INFLIGHT_ALL = APK_ST_INFLIGHT_ALL, ST_STALE_ALL = APK_ST_STALE_ALL };
   auto stat = [&](int k, uint64_t v) { s_stats[k] += v; };  // thread 0 only
 
@@ -432,6 +432,7 @@ k_persistent_yield(const apk_yield_params) {
       // event log, the setter, the yield decision and the checkpoint all
       // happen below, outside it, so that none of their state is live in it.
       bool atSite = false;
+      bool startHit = false;  // uniform: this site is a task-start site
       int fSeen = 0;
       if (startSite) {
         // Task-start site: stage 0's site, taken on the sample that came back
@@ -443,6 +444,7 @@ k_persistent_yield(const apk_yield_params) {
         if (fStart != lastSeen) {
           fSeen = fStart;
           atSite = true;
+          startHit = true;
         }
       }
       while (!atSite && s < S) {
@@ -591,10 +593,13 @@ k_persistent_yield(const apk_yield_params) {
       srcKind = AS_IS;
       if (f <= lastSeen) continue;
       const int64_t g = wall_ticks();
-      if (tid == 0 && P().obs_gt) {
-        const int obsStride = P().obs_stride > 0 ? P().obs_stride : (int)gridDim.x;
-        if (row() < obsStride)
-          for (int e = lastSeen; e < f; ++e) P().obs_gt[(size_t)e * obsStride + row()] = g;
+      if (tid == 0) {
+        if (P().obs_gt) {
+          const int obsStride = P().obs_stride > 0 ? P().obs_stride : (int)gridDim.x;
+          if (row() < obsStride)
+            for (int e = lastSeen; e < f; ++e) P().obs_gt[(size_t)e * obsStride + row()] = g;
+        }
+        if (startHit) stat(ST_START_SITES, 1);
       }
       const int ev = f - 1;
       lastSeen = f;

@@ -221,9 +221,13 @@ enum {
   APK_ST_CHECKPOINTS = 9, /* checkpoints taken (issue sites: every observer) */
   APK_ST_INFLIGHT_ALL = 10, /* APK_ST_INFLIGHT over every checkpoint taken */
   APK_ST_STALE_ALL = 11,    /* APK_ST_STALE over every checkpoint taken */
-  APK_ST_DECLINED = 12      /* retreats declined because the resume ring held
+  APK_ST_DECLINED = 12,     /* retreats declined because the resume ring held
                                rq_capacity unreleased tickets (the block kept
                                its tile and worked on; nothing is lost) */
+  APK_ST_START_SITES = 13   /* new flag values first seen at a task-start site
+                               (cooperative arm, stage polls: the sample taken
+                               with the task pop, before the tile's first
+                               loads have landed) */
 };
 
 /* Work queue: every persistent kernel pops tasks from APK_QUEUE_WORDS

@@ -137,6 +137,7 @@ def test_python_constants_match_header():
     assert int(defines["APK_RQ_CTL_WORDS"]) == apk_amd.RQ_CTL_WORDS == 4
     stats = dict(re.findall(r"(APK_ST_\w+) = (\d+)", text))
     assert int(stats["APK_ST_DECLINED"]) == apk_amd.ST_DECLINED == 12
+    assert int(stats["APK_ST_START_SITES"]) == apk_amd.ST_START_SITES == 13
     assert int(stats["APK_ST_ERRORS"]) == apk_amd.ST_ERRORS == 7
 
 

@@ -200,6 +200,34 @@ def test_mfma128_oracle_exactly_once(torch_gpu, apk, mfma_job):
     assert ok and fired >= 5 and bad_u == 0 and uncl == 0
 
 
+def test_mfma128_task_start_sites(torch_gpu, apk):
+    """Tasks two k-stages deep: a large share of the events arrive while
+    blocks are between tasks, where a new generation is first seen at the
+    task-start site (the flag sample taken with the task pop). Those sites
+    must be taken, and the run must stay bit-identical and exactly-once."""
+    say("mfma128 task-start sites: M=N=512 K=64 kc=32, 400 passes")
+    E = apk.ENGINE_MFMA128
+    j = Job(torch_gpu, apk, E, 512, 512, 64, 32, 256, 256, 64, events=40,
+            blocks=_blocks(apk, E, apk.POLL_STAGE), passes=400)
+    off = j.run(apk.POLL_OFF, events=0)
+    assert oracle.rel_frobenius(off["C"], oracle.gemm_f64(j.A, j.B, threads=8)) <= 1e-5
+    ref_h = j.tile_hashes(off["C"])
+    _, u_ref_h = j.urgent_reference()
+    for resume in (apk.RESUME_CKPT_FULL, apk.RESUME_CKPT_ACC, apk.RESUME_RESTART):
+        r = j.run(apk.POLL_STAGE, resume=resume, use_oracle=True)
+        fired = _assert_run_exact(j, r, off["C"], ref_h, u_ref_h)
+        dup, missed, first_bad = oracle.count_tasks(r["exec"])
+        assert (dup, missed) == (0, 0), first_bad
+        starts = _stat(r, apk, apk.ST_START_SITES)
+        say(f"  resume {resume}: fired {fired}, yields {_stat(r, apk, apk.ST_YIELDS)}, "
+            f"generations first seen at a task start {starts}")
+        assert starts > 0
+    # the naive discipline keeps its checkpoints after the stage wait: no
+    # task-start sites
+    r = j.run(apk.POLL_STAGE, resume=apk.RESUME_CKPT_FULL, naive=1)
+    assert _stat(r, apk, apk.ST_START_SITES) == 0
+
+
 def test_valu64_yield_bit_exact_vs_fmaf_chain(torch_gpu, apk):
     say("valu64 yield M=N=256 K=256 kc=64 chunk polls, restart and ckpt")
     E = apk.ENGINE_VALU64

@@ -78,14 +78,28 @@ def test_coop_poll_every_4():
     ("resume-skip", "retreat", [], r"wrong [1-9]"),
     ("resume-skip", "coop", [], r"wrong [1-9]"),
     ("no-release", "retreat", ["--cap", 16], r"unreleased [1-9]"),
-    ("no-gate", "retreat", ["--cap", 2, "--retreat", 16, "--domains", 16, "--rq-wait-us", 500],
-     r"ring left [1-9]"),
+    # tasks of 320 us and a 50 us ring deadline: without the occupancy gate a
+    # producer past the ring's capacity waits for a consumer's next task
+    # boundary and times out holding a ticket (the hole); the gated ring
+    # passes the same job (test_gate_passes_where_no_gate_leaves_a_hole)
+    ("no-gate", "retreat", ["--cap", 2, "--retreat", 16, "--domains", 16, "--rq-wait-us", 50,
+                            "--work-ns", 20000], r"ring left [1-9]"),
     ("double-serve", "coop", [], r"urgent bad [1-9]"),
 ])
 def test_planted_mistakes_are_caught(bug, arm, extra, caught):
     rc, line, _ = run("--arm", arm, "--bug", bug, "--seed", 11, *extra)
     assert rc == 1, line
     assert line.startswith("FAIL") and re.search(caught, line), line
+
+
+def test_gate_passes_where_no_gate_leaves_a_hole():
+    """The planted no-gate job with the ring as built: the same 50 us
+    deadline, 320 us tasks and 2-entry ring, and every task completes once
+    with the ring left empty."""
+    rc, line, f = run("--arm", "retreat", "--seed", 11, "--cap", 2, "--retreat", 16,
+                      "--domains", 16, "--rq-wait-us", 50, "--work-ns", 20000)
+    assert rc == 0, line
+    assert f["miss"] == 0 and f["lost"] == 0 and f["ring left"] == 0 and f["stuck"] == 0, line
 
 
 @pytest.mark.parametrize("resume", ["full", "acc", "restart"])

@@ -27,9 +27,14 @@ ENV = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0",
            UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1",
            TSAN_OPTIONS="halt_on_error=0:exitcode=66")
 # A job long enough for 40 generations at 0.5 ms on 16 blocks, short enough
-# under the sanitizers' 5-15x slowdown.
+# under the sanitizers' 5-15x slowdown. The ring's wait deadlines (20 ms in
+# the kernels, there only to keep a stopped block from hanging the grid) are
+# stretched to 2 s: under ThreadSanitizer, 32 threads on a few cores were
+# seen to stall a consumer past 20 ms, and a deadline that runs out is
+# reported as an error by design.
 JOB = ["--tiles-m", "16", "--tiles-n", "16", "--passes", "32", "--stages", "16",
-       "--mean-gap-us", "500", "--events", "40", "--blocks", "16", "--work-ns", "20000"]
+       "--mean-gap-us", "500", "--events", "40", "--blocks", "16", "--work-ns", "20000",
+       "--rq-wait-us", "2000000"]
 
 
 @pytest.fixture(scope="module")
