@@ -267,23 +267,6 @@ struct EngMfma128T {
           t[row * TN + wn * 64 + cb * 32 + lr] = acc.c[rb][cb][r];
         }
   }
-
-  static __device__ __forceinline__ void store(const Acc& acc, float* C, int ldc,
-                                               int row0, int col0) {
-    const int w = threadIdx.x >> 6, l = lane_id();
-    const int wm = w & 1, wn = w >> 1;
-    const int lr = l & 31, h = l >> 5;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int row = row0 + wm * 64 + rb * 32 + 8 * (r >> 2) + 4 * h + (r & 3);
-          const int col = col0 + wn * 64 + cb * 32 + lr;
-          C[(size_t)row * ldc + col] = acc.c[rb][cb][r];
-        }
-  }
 };
 
 using EngMfma128 = EngMfma128T<1>;

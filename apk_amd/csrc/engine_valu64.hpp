@@ -190,16 +190,6 @@ struct EngValu64 {
       *(float4*)(t + (ty * 4 + i) * TN + tx * 4) = v;
     }
   }
-
-  static __device__ __forceinline__ void store(const Acc& acc, float* C, int ldc,
-                                               int row0, int col0) {
-    const int tx = threadIdx.x & 15, ty = threadIdx.x >> 4;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float4 v = {acc.v[i][0], acc.v[i][1], acc.v[i][2], acc.v[i][3]};
-      *(float4*)(C + (size_t)(row0 + ty * 4 + i) * ldc + col0 + tx * 4) = v;
-    }
-  }
 };
 
 }  // namespace apk
