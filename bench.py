@@ -522,8 +522,8 @@ def main():
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build runs on one GPU only; the preemptible persistent "
-              "GEMM has no multi-GPU path (see DESIGN.md for how it would shard).",
-              file=sys.stderr)
+              "GEMM has no multi-GPU path (each GPU would run its own share of the "
+              "tile grid with its own queue and flag).", file=sys.stderr)
         sys.exit(2)
 
     import numpy as np
