@@ -310,6 +310,97 @@ struct EngBf16T {
     compute(ring, slot, acc, [] { return true; }, [](int) {});
   }
 
+  // The same pair software-pipelined across the barrier: half of its last
+  // k-step -- the MFMAs of accumulator rows rb < RT, whose operands (RT A
+  // and all CB Bt fragments) are kept in a Tail -- runs in the NEXT pair's
+  // call, right after that pair's first operand reads are issued. Those
+  // MFMAs (operands already in registers) cover the reads' LDS latency,
+  // which otherwise leaves both waves of a SIMD idle after every barrier
+  // when both belong to the block that barriered. With TAIL the call first
+  // completes the previous pair, then runs `pre` -- a site's state is that
+  // of the stages before this pair, the previous pair included -- then this
+  // pair's k-steps, the rows rb >= RT of its last one included; the next
+  // pair's loads (`mid`) are spread over all of the call's MFMAs, so some go
+  // out before `pre` (a pair abandoned at a site has them in flight into the
+  // free half of the ring; a checkpoint drains them). Without TAIL (a job's
+  // first pair, or after a site) `pre` comes first. Every accumulator still
+  // sees its k-steps in ascending order.
+  static constexpr int RT = (RB + 1) / 2;  // accumulator rows whose last k-step is deferred
+  struct Tail {
+    bf16x8 a[RT], b[CB];
+  };
+  static constexpr int NT_MF = RT * CB;             // deferred MFMAs
+  static constexpr int NH = JG * MFMAS - NT_MF;      // MFMAs of a pair in its own call
+  static_assert(NH >= GROUP * LOADS, "a pair without a tail still spreads its loads");
+  template <bool TAIL, class Pre, class Mid>
+  static __device__ __forceinline__ bool compute_pl(const char* ring, int slot, Acc& acc,
+                                                    Tail& tail, Pre&& pre, Mid&& mid) {
+    constexpr int NT = TAIL ? NT_MF : 0;  // the previous pair's MFMAs, before `pre`
+    constexpr int IV_P = (NT + NH) / (GROUP * LOADS) < IVMAX_ ? (NT + NH) / (GROUP * LOADS)
+                                                              : IVMAX_;
+    auto hook = [&](int g) {  // after the call's g-th MFMA
+      if (g % IV_P == 0 && g / IV_P <= GROUP * LOADS) {
+        __builtin_amdgcn_sched_barrier(0);
+        mid(g / IV_P - 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    };
+    auto mma = [&](const bf16x8& a, const bf16x8& b, int rb, int cb) {
+      acc.c[rb][cb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc.c[rb][cb], 0, 0, 0);
+    };
+    const char* gbase = ring + slot * STAGE;
+    Frag f[2];
+    bf16x8 rest[RB - RT];  // the last k-step's A rows RT..RB-1
+    load_frag(gbase, 0, f[0]);
+    if constexpr (TAIL) {
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int m = 0; m < NT_MF; ++m) {
+        mma(tail.a[m / CB], tail.b[m % CB], m / CB, m % CB);
+        hook(m + 1);
+      }
+    }
+    if (!pre()) return false;
+#pragma unroll
+    for (int j = 0; j + 1 < JG; ++j) {
+      if (j + 2 < JG) {
+        load_frag(gbase, j + 1, f[(j + 1) & 1]);
+      } else {
+        Frag& last = f[(j + 1) & 1];
+        load_frag(gbase, JG - 1, last);
+#pragma unroll
+        for (int rb = 0; rb < RB; ++rb) {
+          if (rb < RT) tail.a[rb] = last.a[rb];
+          else rest[rb - RT] = last.a[rb];
+        }
+#pragma unroll
+        for (int cb = 0; cb < CB; ++cb) tail.b[cb] = last.b[cb];
+      }
+      const Frag& c = f[j & 1];
+#pragma unroll
+      for (int m = 0; m < MFMAS; ++m) {
+        mma(c.a[m / CB], c.b[m % CB], m / CB, m % CB);
+        hook(NT + j * MFMAS + m + 1);
+      }
+    }
+    // the last k-step's rows RT..RB-1 now; rows 0..RT-1 in the next call
+#pragma unroll
+    for (int m = 0; m < (RB - RT) * CB; ++m) {
+      mma(rest[m / CB], tail.b[m % CB], RT + m / CB, m % CB);
+      hook(NT + (JG - 1) * MFMAS + m + 1);
+    }
+    return true;
+  }
+  // The last pair's deferred MFMAs, before the accumulators are read.
+  static __device__ __forceinline__ void finish_tail(Acc& acc, const Tail& tail) {
+#pragma unroll
+    for (int m = 0; m < NT_MF; ++m) {
+      const int rb = m / CB, cb = m % CB;
+      acc.c[rb][cb] =
+          __builtin_amdgcn_mfma_f32_32x32x16_bf16(tail.a[rb], tail.b[cb], acc.c[rb][cb], 0, 0, 0);
+    }
+  }
+
   // Output element (tile-relative row, col) of accumulator register e.
   static __device__ __forceinline__ void coord(int e, int& r, int& c) {
     const int w = threadIdx.x >> 6, l = lane_id();

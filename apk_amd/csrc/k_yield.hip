@@ -314,6 +314,14 @@ k_persistent_yield(const apk_yield_params) {
     const typename E::Lane ln = E::lane_offsets(ctx, row0, col0);
     typename E::Acc acc;
     int slot = 0, nextSite = 0, lastSlot = -1;
+    // Pipelined pairs: the last computed pair's deferred k-step (its
+    // operands in `tail`) runs at the start of the next pair's call, or
+    // before the epilogue; a call that stops at a site has run it.
+    typename TailFrag<E>::type tail;
+    bool hasTail = false;  // uniform
+    // Only with polls off: a polled kernel has no registers left for the
+    // deferred operands (it would spill in the stage loop).
+    constexpr bool kPipe = PipelinedPairs<E>::value && POLL == APK_POLL_OFF;
 
     // Poll sites are the stages s with s % pollStride == 0; `nextSite` is the
     // next one not yet passed (an urgent tile never reaches one), so a stage
@@ -556,6 +564,24 @@ k_persistent_yield(const apk_yield_params) {
               break;
             }
             E::compute(ring, slot, acc);
+          } else if constexpr (kPipe) {
+            auto mid = [&](int i) {
+              if (i == 0 && carry) sample(other);
+              issue_group_one<E>(ctx, ln, d0, d1, i);
+            };
+            if (hasTail) {
+              hasTail = false;  // run by the call, ahead of its site check
+              if (!E::template compute_pl<true>(ring, slot, acc, tail, poll, mid)) {
+                tail = typename E::Tail{};  // consumed: nothing live across the site
+                break;
+              }
+            } else {
+              if (!E::template compute_pl<false>(ring, slot, acc, tail, poll, mid)) {
+                tail = typename E::Tail{};
+                break;
+              }
+            }
+            hasTail = true;
           } else {
             if (!E::compute(ring, slot, acc, poll, [&](int i) {
                   if (i == 0 && carry) sample(other);
@@ -768,6 +794,9 @@ k_persistent_yield(const apk_yield_params) {
     }
     if (retreated) break;  // the block exits; its tile waits in the resume queue
     if (yielded) continue;  // the event's urgent tiles first, then this tile again
+    if constexpr (kPipe) {
+      if (hasTail) E::finish_tail(acc, tail);
+    }
     wait_vmcnt<0>();  // the refetches past the tile's end have landed
     lds_sync();       // every wave done with the ring; every sample has landed
     if (POLL != APK_POLL_OFF && lastSlot >= 0) fLatest = uniform(flagring[lastSlot]);

@@ -131,6 +131,37 @@ template <class E>
 struct HasIssueGroup<E, std::void_t<decltype(&E::issue_group)>> {
   static constexpr bool value = true;
 };
+// An engine whose pairs are software-pipelined across the barrier
+// (E::compute_pl, E::finish_tail): the stage loops carry its deferred k-step
+// operands (TailFrag) from one pair to the next.
+template <class E, class = void>
+struct HasTailPipe {
+  static constexpr bool value = false;
+};
+template <class E>
+struct HasTailPipe<E, std::void_t<decltype(&E::finish_tail)>> {
+  static constexpr bool value = true;
+};
+template <class E, bool = HasTailPipe<E>::value>
+struct TailFrag {
+  struct type {};
+};
+template <class E>
+struct TailFrag<E, true> {
+  using type = typename E::Tail;
+};
+// Whether the stage loops use it: for a tile whose block holds every wave of
+// its SIMDs (one block per CU). With two blocks per CU the other block's
+// wave already fills the idle stretch after a barrier (measured: no change
+// at 2 and 4 blocks per CU).
+template <class E, bool = HasTailPipe<E>::value>
+struct PipelinedPairs {
+  static constexpr bool value = false;
+};
+template <class E>
+struct PipelinedPairs<E, true> {
+  static constexpr bool value = E::BLOCKS_PER_CU == 1;
+};
 template <class E>
 __device__ __forceinline__ void issue_group_one(const typename E::Ctx& c,
                                                 const typename E::Lane& ln,
@@ -154,6 +185,11 @@ __device__ __forceinline__ void run_stages(char* ring, uint32_t wl, const typena
   issue_loads<E>(c, ln, E::stage_dst(wl, c, 0, 0, S));
   issue_loads<E>(c, ln, E::stage_dst(wl, c, 1, 1, S));
   int slot = 0;
+  // Pairs pipelined across the barrier (E::compute_pl), as in the
+  // preemptible kernel with polls off.
+  constexpr bool kPipe = PipelinedPairs<E>::value;
+  typename TailFrag<E>::type tail;
+  bool hasTail = false;
   for (int s = 0; s < S; s += E::GROUP) {
     hook(s);
     if constexpr (E::GROUP == 1) {
@@ -175,10 +211,19 @@ __device__ __forceinline__ void run_stages(char* ring, uint32_t wl, const typena
       wait_landed<E>();
       lds_sync();
       if (s + 1 < S) hook(s + 1);
-      E::compute(ring, slot, acc, [] { return true; },
-                 [&](int i) { issue_group_one<E>(c, ln, d0, d1, i); });
+      auto mid = [&](int i) { issue_group_one<E>(c, ln, d0, d1, i); };
+      if constexpr (kPipe) {
+        if (hasTail) E::template compute_pl<true>(ring, slot, acc, tail, [] { return true; }, mid);
+        else E::template compute_pl<false>(ring, slot, acc, tail, [] { return true; }, mid);
+        hasTail = true;
+      } else {
+        E::compute(ring, slot, acc, [] { return true; }, mid);
+      }
       slot = other;
     }
+  }
+  if constexpr (kPipe) {
+    if (hasTail) E::finish_tail(acc, tail);
   }
   wait_vmcnt<0>();
   lds_sync();
