@@ -6,14 +6,15 @@
 //  EngBf16x256     (engine bf16x256, 1 block per CU): 256x256 on 8 waves
 //                  (2x4, each 128x64: 128 fp32 per lane), two waves per SIMD;
 //                  a 256 KiB fp32 accumulator is half of a CU's register
-//                  file, so no second block fits. A wave of the poll-off,
-//                  chunk-polled and retreat kernels takes at most 248 of its
-//                  SIMD's 256 registers per lane (allocated in 8s), so a
-//                  small kernel launched on another stream while the grid
-//                  runs (the retreat arm's flag raise, the clock probes)
-//                  still finds registers on every SIMD; the cooperative
-//                  stage- and issue-site kernels, whose generations come from
-//                  the grid's own setter, take 249-251. (The same tile on 4 waves of 128x128 is
+//                  file, so no second block fits. A wave of the poll-off and
+//                  retreat kernels takes at most 248 of its SIMD's 256
+//                  registers per lane (allocated in 8s), so a small kernel
+//                  launched on another stream while the grid runs (the
+//                  retreat arm's flag raise, the clock probes) still finds
+//                  registers on every SIMD; the cooperative chunk-, stage-
+//                  and issue-site kernels, whose generations come from the
+//                  grid's own setter, take 250-255. Its pairs are
+//                  software-pipelined across the barrier (compute_pl). (The same tile on 4 waves of 128x128 is
 //                  no faster, and its polled kernels take all 512 registers
 //                  of each SIMD: the flag-raise kernel then waits for the
 //                  job to end.)
@@ -316,15 +317,18 @@ struct EngBf16T {
   // call, right after that pair's first operand reads are issued. Those
   // MFMAs (operands already in registers) cover the reads' LDS latency,
   // which otherwise leaves both waves of a SIMD idle after every barrier
-  // when both belong to the block that barriered. With TAIL the call first
-  // completes the previous pair, then runs `pre` -- a site's state is that
-  // of the stages before this pair, the previous pair included -- then this
-  // pair's k-steps, the rows rb >= RT of its last one included; the next
-  // pair's loads (`mid`) are spread over all of the call's MFMAs, so some go
-  // out before `pre` (a pair abandoned at a site has them in flight into the
-  // free half of the ring; a checkpoint drains them). Without TAIL (a job's
-  // first pair, or after a site) `pre` comes first. Every accumulator still
-  // sees its k-steps in ascending order.
+  // when both belong to the block that barriered (and the site's flag read
+  // with them). With `hasTail` the call first completes the previous pair;
+  // without (a job's first pair, or the pair a site stopped at) it skips
+  // those MFMAs. Then come the first of the next pair's loads (`mid`, the
+  // ones the tail's MFMAs carry), `pre` -- a site's state is that of the
+  // stages before this pair, the previous pair included; a pair abandoned
+  // there has those loads in flight into the free half of the ring, which a
+  // checkpoint drains -- and this pair's k-steps, the rows rb >= RT of its
+  // last one included, carrying the other loads. One body for both cases
+  // (a uniform branch around the tail's MFMAs): two inlined copies of the
+  // pair spilled in the polled kernels. Every accumulator still sees its
+  // k-steps in ascending order.
   static constexpr int RT = (RB + 1) / 2;  // accumulator rows whose last k-step is deferred
   struct Tail {
     bf16x8 a[RT], b[CB];
@@ -332,10 +336,11 @@ struct EngBf16T {
   static constexpr int NT_MF = RT * CB;             // deferred MFMAs
   static constexpr int NH = JG * MFMAS - NT_MF;      // MFMAs of a pair in its own call
   static_assert(NH >= GROUP * LOADS, "a pair without a tail still spreads its loads");
-  template <bool TAIL, class Pre, class Mid>
+  template <class Pre, class Mid>
   static __device__ __forceinline__ bool compute_pl(const char* ring, int slot, Acc& acc,
-                                                    Tail& tail, Pre&& pre, Mid&& mid) {
-    constexpr int NT = TAIL ? NT_MF : 0;  // the previous pair's MFMAs, before `pre`
+                                                    Tail& tail, bool hasTail, Pre&& pre,
+                                                    Mid&& mid) {
+    constexpr int NT = NT_MF;  // the previous pair's MFMAs, before `pre`
     constexpr int IV_P = (NT + NH) / (GROUP * LOADS) < IVMAX_ ? (NT + NH) / (GROUP * LOADS)
                                                               : IVMAX_;
     auto hook = [&](int g) {  // after the call's g-th MFMA
@@ -352,14 +357,14 @@ struct EngBf16T {
     Frag f[2];
     bf16x8 rest[RB - RT];  // the last k-step's A rows RT..RB-1
     load_frag(gbase, 0, f[0]);
-    if constexpr (TAIL) {
-      __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);
+    if (hasTail) {
 #pragma unroll
-      for (int m = 0; m < NT_MF; ++m) {
-        mma(tail.a[m / CB], tail.b[m % CB], m / CB, m % CB);
-        hook(m + 1);
-      }
+      for (int m = 0; m < NT_MF; ++m) mma(tail.a[m / CB], tail.b[m % CB], m / CB, m % CB);
     }
+    // the loads the tail's MFMAs would have carried (issued either way)
+#pragma unroll
+    for (int m = 0; m < NT_MF; ++m) hook(m + 1);
     if (!pre()) return false;
 #pragma unroll
     for (int j = 0; j + 1 < JG; ++j) {

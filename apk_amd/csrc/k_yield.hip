@@ -319,9 +319,8 @@ k_persistent_yield(const apk_yield_params) {
     // before the epilogue; a call that stops at a site has run it.
     typename TailFrag<E>::type tail;
     bool hasTail = false;  // uniform
-    // Only with polls off: a polled kernel has no registers left for the
-    // deferred operands (it would spill in the stage loop).
-    constexpr bool kPipe = PipelinedPairs<E>::value && POLL == APK_POLL_OFF;
+    // Not at issue sites, whose loop issues the next pair ahead of the poll.
+    constexpr bool kPipe = PipelinedPairs<E>::value && POLL != APK_POLL_ISSUE;
 
     // Poll sites are the stages s with s % pollStride == 0; `nextSite` is the
     // next one not yet passed (an urgent tile never reaches one), so a stage
@@ -569,18 +568,9 @@ k_persistent_yield(const apk_yield_params) {
               if (i == 0 && carry) sample(other);
               issue_group_one<E>(ctx, ln, d0, d1, i);
             };
-            if (hasTail) {
-              hasTail = false;  // run by the call, ahead of its site check
-              if (!E::template compute_pl<true>(ring, slot, acc, tail, poll, mid)) {
-                tail = typename E::Tail{};  // consumed: nothing live across the site
-                break;
-              }
-            } else {
-              if (!E::template compute_pl<false>(ring, slot, acc, tail, poll, mid)) {
-                tail = typename E::Tail{};
-                break;
-              }
-            }
+            const bool had = hasTail;
+            hasTail = false;  // a tail is run by the call, ahead of its site check
+            if (!E::compute_pl(ring, slot, acc, tail, had, poll, mid)) break;
             hasTail = true;
           } else {
             if (!E::compute(ring, slot, acc, poll, [&](int i) {
