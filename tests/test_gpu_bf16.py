@@ -57,10 +57,14 @@ def run_bf16(torch, apk, A_bits, Bt_bits, k_chunk, blocks=None, eng=None):
 
 
 @pytest.mark.parametrize("name", ENGS)
-def test_bf16_layout_exact_small_integers(torch_gpu, apk, name):
+@pytest.mark.parametrize("K", [64, 128, 192])
+def test_bf16_layout_exact_small_integers(torch_gpu, apk, name, K):
+    """Exact products and sums of small integers. K = 64 is one pair of the
+    256x256 tile's 32-deep stages, whose deferred k-step (the pipelined pair)
+    then runs only before the epilogue; 192, an odd number of its pairs."""
     eng = apk.ENGINES[name]
     TM, TN = tile_of(apk, eng)
-    M, N, K = 2 * TM, TN, 128
+    M, N = 2 * TM, TN
     say(f"{name} layout: small integers, M={M} N={N} K={K}")
     rng = np.random.default_rng(5)
     A_bits, A = bits_of_small_ints(rng, (M, K))
