@@ -416,6 +416,11 @@ int main(int argc, char** argv) {
   // Host: raise the generations at exponential gaps while blocks still run;
   // retreat arm: after each, the "urgent kernel" (a short wait) and the
   // continuation that brings back as many blocks as the generation freed.
+  // On the GPU the next flag is raised on the urgent stream behind the urgent
+  // GEMM, which cannot start before a block has retreated (or the job ended):
+  // the host here likewise waits for the generation's first retreat (or
+  // refusal), up to the ring's 20 ms deadline, so that two generations never
+  // land together on a grid that has not reached a site yet.
   std::mt19937 rng(c.seed);
   std::exponential_distribution<double> gap(1.0 / std::max(1.0, c.meanGapUs * 1000.0));
   int nextBid = c.blocks;
@@ -426,6 +431,11 @@ int main(int argc, char** argv) {
     __atomic_store_n(&sim.flag, e + 1, __ATOMIC_RELAXED);
     sim.fired.fetch_add(1);
     if (c.retreat) {
+      const long r0 = sim.retreats.load(), f0 = sim.refused.load();
+      const int64_t t0 = now_ns();
+      while (sim.retreats.load() == r0 && sim.refused.load() == f0 && sim.running.load() > 0 &&
+             now_ns() - t0 < 20000000)
+        std::this_thread::yield();
       spin_ns(20000);  // the urgent kernel on the freed CUs
       const long r = sim.retreats.load();
       const int n = (int)(r - prevRetreats);

@@ -77,11 +77,20 @@ CASES = [
 @pytest.mark.parametrize("san", ["tsan", "asan"])
 @pytest.mark.parametrize("case", CASES, ids=lambda c: "-".join(str(x) for x in c[1::2]))
 def test_protocol_simulator_sanitized(sanitized, san, case):
-    rc, out, err = run(os.path.join(sanitized, f"protocol_sim_{san}"), JOB + case + ["--seed", 4])
-    assert clean(err), err[-6000:]
-    assert rc == 0 and out.startswith("PASS"), out + err[-2000:]
-    if "retreat" in case:
+    # Every run must be clean and pass; a retreat case is run again (up to
+    # four times) while a run had no retreat at all, which the host's thread
+    # scheduling decides (tests/test_protocol_sim.py run_covering).
+    for _ in range(4):
+        rc, out, err = run(os.path.join(sanitized, f"protocol_sim_{san}"),
+                           JOB + case + ["--seed", 4])
+        assert clean(err), err[-6000:]
+        assert rc == 0 and out.startswith("PASS"), out + err[-2000:]
+        if "retreat" not in case:
+            break
         n = int(re.search(r"retreats (\d+)", out).group(1))
+        if n > 0:
+            break
+    if "retreat" in case:
         assert n > 0 and f"resumed {n}" in out, out
 
 
