@@ -325,7 +325,9 @@ struct EngBf16T {
   // stages before this pair, the previous pair included; a pair abandoned
   // there has those loads in flight into the free half of the ring, which a
   // checkpoint drains -- and this pair's k-steps, the rows rb >= RT of its
-  // last one included, carrying the other loads. One body for both cases
+  // last one included, carrying the other loads. Without `early` those first
+  // loads go out right after `pre` instead: a block that may leave at `pre`
+  // then has no fresh loads to wait for before it exits. One body for both cases
   // (a uniform branch around the tail's MFMAs): two inlined copies of the
   // pair spilled in the polled kernels. Every accumulator still sees its
   // k-steps in ascending order.
@@ -338,8 +340,8 @@ struct EngBf16T {
   static_assert(NH >= GROUP * LOADS, "a pair without a tail still spreads its loads");
   template <class Pre, class Mid>
   static __device__ __forceinline__ bool compute_pl(const char* ring, int slot, Acc& acc,
-                                                    Tail& tail, bool hasTail, Pre&& pre,
-                                                    Mid&& mid) {
+                                                    Tail& tail, bool hasTail, bool early,
+                                                    Pre&& pre, Mid&& mid) {
     constexpr int NT = NT_MF;  // the previous pair's MFMAs, before `pre`
     constexpr int IV_P = (NT + NH) / (GROUP * LOADS) < IVMAX_ ? (NT + NH) / (GROUP * LOADS)
                                                               : IVMAX_;
@@ -362,10 +364,18 @@ struct EngBf16T {
 #pragma unroll
       for (int m = 0; m < NT_MF; ++m) mma(tail.a[m / CB], tail.b[m % CB], m / CB, m % CB);
     }
-    // the loads the tail's MFMAs would have carried (issued either way)
+    // the loads the tail's MFMAs would have carried: before `pre` when
+    // `early`, else right after it (a block that may leave at `pre` then has
+    // no fresh loads to drain first)
+    if (early) {
 #pragma unroll
-    for (int m = 0; m < NT_MF; ++m) hook(m + 1);
+      for (int m = 0; m < NT_MF; ++m) hook(m + 1);
+    }
     if (!pre()) return false;
+    if (!early) {
+#pragma unroll
+      for (int m = 0; m < NT_MF; ++m) hook(m + 1);
+    }
 #pragma unroll
     for (int j = 0; j + 1 < JG; ++j) {
       if (j + 2 < JG) {

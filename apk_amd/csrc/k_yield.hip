@@ -570,7 +570,10 @@ k_persistent_yield(const apk_yield_params) {
             };
             const bool had = hasTail;
             hasTail = false;  // a tail is run by the call, ahead of its site check
-            if (!E::compute_pl(ring, slot, acc, tail, had, poll, mid)) break;
+            // A block that may retreat here issues the next pair's first loads
+            // after its check: leaving, it then has nothing in flight to drain.
+            if (!E::compute_pl(ring, slot, acc, tail, had, !(syncPoll && check), poll, mid))
+              break;
             hasTail = true;
           } else {
             if (!E::compute(ring, slot, acc, poll, [&](int i) {

@@ -213,7 +213,7 @@ __device__ __forceinline__ void run_stages(char* ring, uint32_t wl, const typena
       if (s + 1 < S) hook(s + 1);
       auto mid = [&](int i) { issue_group_one<E>(c, ln, d0, d1, i); };
       if constexpr (kPipe) {
-        E::compute_pl(ring, slot, acc, tail, hasTail, [] { return true; }, mid);
+        E::compute_pl(ring, slot, acc, tail, hasTail, true, [] { return true; }, mid);
         hasTail = true;
       } else {
         E::compute(ring, slot, acc, [] { return true; }, mid);
