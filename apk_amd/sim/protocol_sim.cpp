@@ -28,6 +28,8 @@
 // full ("refused") are allowed: the declining block keeps its tile.
 //
 // --rq-wait-us sets the ring's wait deadlines (the kernels' 20 ms by default).
+// --urgent-us: how long the urgent kernel holds the freed CUs before the
+// continuation starts (20 us by default).
 // --bug plants one mistake, to show that the checks see it:
 //   publish-early   (retreat) publish the ticket before writing the slot
 //   resume-skip     resume one stage past the checkpointed stage
@@ -128,6 +130,7 @@ struct Config {
   int workNs = 2000, pollEvery = 1, resume = R_FULL, retreatN = 32, cap = 0, urgentTiles = 4;
   int domains = APK_RETREAT_DOMAINS;
   int64_t rqWaitTicks = proto::RQ_WAIT_TICKS;
+  int64_t urgentNs = 20000;
   unsigned seed = 21;
   Bug bug = B_NONE;
 };
@@ -390,6 +393,7 @@ int main(int argc, char** argv) {
     else if (k == "--domains") c.domains = atoi(v);
     else if (k == "--seed") c.seed = (unsigned)atoi(v);
     else if (k == "--rq-wait-us") c.rqWaitTicks = (int64_t)(atof(v) * 100.0);
+    else if (k == "--urgent-us") c.urgentNs = (int64_t)(atof(v) * 1000.0);
     else if (k == "--bug") bug = v;
     else {
       fprintf(stderr, "unknown option %s\n", k.c_str());
@@ -399,7 +403,7 @@ int main(int argc, char** argv) {
   c.bug = parse_bug(bug);
   if (c.blocks < 1 || c.stages < 2 || c.events < 0 || c.pollEvery < 1 || c.domains < 1 ||
       c.domains > APK_RETREAT_DOMAINS || c.urgentTiles < 1 || c.tilesM < 1 || c.tilesN < 1 ||
-      c.passes < 1 || (c.cap != 0 && c.cap < 2) || c.rqWaitTicks < 0) {
+      c.passes < 1 || (c.cap != 0 && c.cap < 2) || c.rqWaitTicks < 0 || c.urgentNs < 0) {
     fprintf(stderr, "bad configuration\n");
     return 2;
   }
@@ -436,7 +440,7 @@ int main(int argc, char** argv) {
       while (sim.retreats.load() == r0 && sim.refused.load() == f0 && sim.running.load() > 0 &&
              now_ns() - t0 < 20000000)
         std::this_thread::yield();
-      spin_ns(20000);  // the urgent kernel on the freed CUs
+      spin_ns(c.urgentNs);  // the urgent kernel on the freed CUs
       const long r = sim.retreats.load();
       const int n = (int)(r - prevRetreats);
       prevRetreats = r;

@@ -22,7 +22,11 @@ import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 NATIVE = os.path.join(ROOT, "tests", "native")
-BUILD = os.path.join(NATIVE, "_build")
+# One build folder per pytest-xdist worker: workers that rebuilt the same
+# binaries at once ran a file another worker was still writing.
+_WORKER = os.environ.get("PYTEST_XDIST_WORKER", "")
+BUILD_NAME = "_build" + (f"_{_WORKER}" if _WORKER else "")
+BUILD = os.path.join(NATIVE, BUILD_NAME)
 ENV = dict(os.environ, ASAN_OPTIONS="detect_leaks=0:abort_on_error=0",
            UBSAN_OPTIONS="print_stacktrace=1:halt_on_error=1",
            TSAN_OPTIONS="halt_on_error=0:exitcode=66")
@@ -39,8 +43,8 @@ JOB = ["--tiles-m", "16", "--tiles-n", "16", "--passes", "32", "--stages", "16",
 
 @pytest.fixture(scope="module")
 def sanitized():
-    r = subprocess.run(["make", "-s", "-C", NATIVE, "sanitize"], capture_output=True, text=True,
-                       timeout=600)
+    r = subprocess.run(["make", "-s", "-C", NATIVE, "sanitize", f"B={BUILD_NAME}"],
+                       capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stdout[-3000:] + r.stderr[-3000:]
     return BUILD
 
