@@ -15,7 +15,8 @@ and exits non-zero on any violation):
         tile at 2 and 4 blocks per CU, yields at k-stage (and for 256x256
         tile-boundary) sites: C bit-identical, float64 (bf16-rounded inputs)
         within 1e-2, exactly-once; the 1e8-task tiny oracle at 1, 2 and 4
-        blocks per CU.
+        blocks per CU; the retreat arm on the 256x256 background, one job of
+        400 arrivals.
 When tasks cycle the grid (more tasks than tiles) C holds the last pass, so
 every task's fingerprint against its unpreempted tile is checked as well.
 """
@@ -168,6 +169,26 @@ def test_cfg3_retreat_arm_continuous(resume):
     out = run_bin("urgent_baseline", *CFG3, "--bg-tasks", 4096, "--urgent-blocks", 4,
                   "--arrival", "exp", "--mean-gap-us", 2000, "--yield", 1, "--retreat", 4,
                   "--oracle", 1, "--continuous", 1, "--events", 400, "--resume", resume)
+    bad, = grab(out, r"SAFETY: (\d+) of \d+ task fingerprints")
+    assert bad == 0
+    n_in, = grab(out, r"continuous retreat arm: (\d+) arrivals within the job")
+    assert n_in == 400
+    assert "arrivals without a retreat 0" in out
+    assert "ORACLE: PASS" in out and "yield: PASS" in out
+
+
+@pytest.mark.parametrize("resume", ["restart", "acc"])
+def test_cfg5_bf16_retreat_arm_continuous(resume):
+    """cfg5 retreat arm on the bf16 256x256 background (M=N=K=8192, 1 block
+    per CU) as one job with 400 exponential arrivals, tiles re-queued from
+    k = 0 or resumed from their accumulators: the blocks that may retreat
+    poll every pair of stages with the pairs software-pipelined, and every
+    task's fingerprint matches its unpreempted tile, every task runs once,
+    the kept urgent outputs are bit-identical."""
+    out = run_bin("urgent_baseline", "--engine", "bf16x256", *CFG5, "--bg-tasks", 1024,
+                  "--urgent-blocks", 1, "--arrival", "exp", "--mean-gap-us", 2000, "--yield", 1,
+                  "--retreat", 1, "--oracle", 1, "--continuous", 1, "--events", 400,
+                  "--resume", resume)
     bad, = grab(out, r"SAFETY: (\d+) of \d+ task fingerprints")
     assert bad == 0
     n_in, = grab(out, r"continuous retreat arm: (\d+) arrivals within the job")
